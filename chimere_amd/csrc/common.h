@@ -1,0 +1,203 @@
+// common.h -- device helpers shared by the gfx950 kernels of libchimere_hip.
+//
+// Arithmetic contract: every kernel is compiled with -ffp-contract=off; a
+// fused multiply-add appears only where written as __builtin_fmaf.  Float
+// division is IEEE (hipcc's default correctly rounded divide).  Together with
+// det_exp() below this makes every fp32 result reproducible bit for bit by a
+// CPU restatement that performs the same operations in the same order.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "iq3s_grid.inc"
+
+namespace chimere {
+
+// ggml type ids
+enum : int { T_Q4_0 = 2, T_Q8_0 = 8, T_IQ3_S = 21 };
+
+constexpr int QK = 32;             // elements per Q8_0 / Q4_0 / Q8_1 block
+constexpr int Q8_1_BYTES = 36;     // [f16 d][f16 s][i8 q[32]]
+constexpr int ROW_PAD = 512;       // ggml MATRIX_ROW_PADDING
+constexpr int SLOTS = 16;          // lanes per row in the GEMV kernels (the L of the fp32 order)
+constexpr int TILE_ROWS = 16;      // rows per GEMV work-group tile (one per 16-lane group)
+constexpr int GEMV_THREADS = TILE_ROWS * SLOTS;   // 256 = 4 waves of 64
+constexpr int CHUNK_BLOCKS = 64;   // 32-element blocks of one row held in LDS at a time
+
+__host__ __device__ inline int64_t pad_to(int64_t n, int64_t a) { return (n + a - 1) / a * a; }
+
+template <int T> struct QTraits;
+template <> struct QTraits<T_Q8_0>  { static constexpr int BYTES = 34;  static constexpr int ELEMS = 32; };
+template <> struct QTraits<T_Q4_0>  { static constexpr int BYTES = 18;  static constexpr int ELEMS = 32; };
+template <> struct QTraits<T_IQ3_S> { static constexpr int BYTES = 110; static constexpr int ELEMS = 256; };
+
+__host__ __device__ inline int64_t row_bytes(int type, int64_t ncols) {
+    return type == T_Q8_0 ? ncols / 32 * 34 : type == T_Q4_0 ? ncols / 32 * 18 : ncols / 256 * 110;
+}
+
+__device__ __forceinline__ float h2f(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+__device__ __forceinline__ uint32_t f2h(float x) {   // round to nearest even
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+}
+
+// Deterministic exp (same operation sequence as the CPU oracle): Cody-Waite
+// reduction with ln2 split 0x1.62e4p-1 + 0x1.7f7d1cp-20, degree-7 Taylor
+// polynomial of e^r in Horner form, scaling by 2^n.  x < -86 -> 0,
+// x > 88.7228 -> +inf.  Relative error about 1 ulp.
+__device__ __forceinline__ float det_exp(float x) {
+    if (x != x) return x;
+    if (x > 88.72283905f) return __builtin_huge_valf();
+    if (x < -86.0f) return 0.0f;
+    float n = __builtin_rintf(x * 0x1.715476p+0f);
+    float r = __builtin_fmaf(-n, 0x1.62e4p-1f, x);
+    r = __builtin_fmaf(-n, 0x1.7f7d1cp-20f, r);
+    float p = 0x1.a01a02p-13f;
+    p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+    p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    return __builtin_ldexpf(p, (int)n);
+}
+// silu(g) = g / (1 + exp(-g))   (fused_ops.rs:34-45)
+__device__ __forceinline__ float det_silu(float g) { return g / (1.0f + det_exp(-g)); }
+
+__device__ __forceinline__ int dot4(int a, int b, int c) {   // v_dot4_i32_i8
+    return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+// bytes 0xFF where the corresponding bit of the 4-bit nibble is set
+__device__ __forceinline__ uint32_t nib_mask(uint32_t nib) {
+    return ((nib * 0x00204081u) & 0x01010101u) * 0xFFu;
+}
+// (hi:lo) >> 8*s, s in 0..3
+__device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t s) {
+    return __builtin_amdgcn_alignbyte(hi, lo, s);
+}
+// 4 bytes at any byte offset of a 4-byte aligned LDS buffer (needs 4 bytes slack)
+__device__ __forceinline__ uint32_t lds_u32(const uint8_t* base, int off) {
+    const uint32_t* w = (const uint32_t*)(base + (off & ~3));
+    return align_bytes(w[1], w[0], off & 3);
+}
+__device__ __forceinline__ uint32_t lds_u16(const uint8_t* base, int off) {
+    return *(const uint16_t*)(base + off);   // off is even for every block field read this way
+}
+
+// One Q8_1 activation block in registers.
+struct XBlk {
+    int q[8];
+    float d;
+    int sumq;   // sum of the 32 quants (used by Q4_0's "- 8" term)
+};
+
+__device__ __forceinline__ void load_xblk(const uint8_t* __restrict__ p, XBlk& x) {
+    const uint32_t* w = (const uint32_t*)p;   // 36-byte blocks are 4-byte aligned
+    uint32_t w0 = w[0];
+    x.d = h2f(w0 & 0xFFFFu);
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) { x.q[i] = (int)w[1 + i]; s = dot4(x.q[i], 0x01010101, s); }
+    x.sumq = s;
+}
+
+// ---- exact int32 block dots of one weight block (in LDS) with one Q8_1 block.
+// `off` is the byte offset of the block (IQ3_S: of its 110-byte superblock)
+// within `row`; returns sumi and sets *dw = f32(weight scale).
+
+__device__ __forceinline__ int dot_q8_0(const uint8_t* row, int off, const XBlk& x, float* dw) {
+    *dw = h2f(lds_u16(row, off));
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) s = dot4((int)lds_u32(row, off + 2 + 4 * i), x.q[i], s);
+    return s;
+}
+
+__device__ __forceinline__ int dot_q4_0(const uint8_t* row, int off, const XBlk& x, float* dw) {
+    *dw = h2f(lds_u16(row, off));
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint32_t v = lds_u32(row, off + 2 + 4 * i);
+        s = dot4((int)(v & 0x0F0F0F0Fu), x.q[i], s);          // elements 4i..4i+3
+        s = dot4((int)((v >> 4) & 0x0F0F0F0Fu), x.q[4 + i], s); // elements 16+4i..
+    }
+    return s - 8 * x.sumq;
+}
+
+// sub-block ib (0..7) of the IQ3_S superblock at `off`; grid in LDS
+__device__ __forceinline__ int dot_iq3_s(const uint8_t* row, int off, int ib, const XBlk& x,
+                                         const uint32_t* grid, float* dw) {
+    *dw = h2f(lds_u16(row, off));
+    uint32_t qs0 = lds_u32(row, off + 2 + 8 * ib);
+    uint32_t qs1 = lds_u32(row, off + 6 + 8 * ib);
+    uint32_t qh = row[off + 66 + ib];
+    uint32_t sg = lds_u32(row, off + 74 + 4 * ib);
+    uint32_t sc = row[off + 106 + (ib >> 1)];
+    int mult = 1 + 2 * (int)((sc >> (4 * (ib & 1))) & 0xFu);
+    int s = 0;
+#pragma unroll
+    for (int l = 0; l < 4; l++) {
+        uint32_t qsw = l < 2 ? qs0 : qs1;
+        uint32_t i0 = ((qsw >> (16 * (l & 1))) & 0xFFu) | (((qh >> (2 * l)) & 1u) << 8);
+        uint32_t i1 = ((qsw >> (16 * (l & 1) + 8)) & 0xFFu) | (((qh >> (2 * l + 1)) & 1u) << 8);
+        uint32_t sb = (sg >> (8 * l)) & 0xFFu;
+        uint32_t m0 = nib_mask(sb & 0xFu), m1 = nib_mask(sb >> 4);
+        // signed levels: (g ^ m) + (m & 1): per-byte negation, no carry since g >= 1
+        uint32_t v0 = (grid[i0] ^ m0) + (m0 & 0x01010101u);
+        uint32_t v1 = (grid[i1] ^ m1) + (m1 & 0x01010101u);
+        s = dot4((int)v0, x.q[2 * l], s);
+        s = dot4((int)v1, x.q[2 * l + 1], s);
+    }
+    return s * mult;
+}
+
+// Block b (32-element unit; IQ3_S: sub-block) of a row chunk held in LDS.
+template <int T>
+__device__ __forceinline__ int block_dot(const uint8_t* row, int b, const XBlk& x,
+                                         const uint32_t* grid, float* dw) {
+    if constexpr (T == T_Q8_0) return dot_q8_0(row, b * 34, x, dw);
+    else if constexpr (T == T_Q4_0) return dot_q4_0(row, b * 18, x, dw);
+    else return dot_iq3_s(row, (b >> 3) * 110, b & 7, x, grid, dw);
+}
+
+// Copy `nrows` row segments of `seg` bytes (global row stride `gstride`) into
+// LDS rows of stride `lstride`, with the widest access the alignment allows.
+__device__ __forceinline__ void stage_rows(uint8_t* __restrict__ lds, int lstride,
+                                           const uint8_t* __restrict__ g, int64_t gstride,
+                                           int nrows, int seg, int tid, int nthreads) {
+    uintptr_t al = (uintptr_t)g | (uintptr_t)gstride | (uintptr_t)seg | (uintptr_t)lstride;
+    if ((al & 15) == 0) {
+        int per = seg >> 4, tot = per * nrows;
+        for (int i = tid; i < tot; i += nthreads) {
+            int r = i / per, c = i - r * per;
+            *(uint4*)(lds + r * lstride + c * 16) = *(const uint4*)(g + r * gstride + c * 16);
+        }
+    } else if ((al & 3) == 0) {
+        int per = seg >> 2, tot = per * nrows;
+        for (int i = tid; i < tot; i += nthreads) {
+            int r = i / per, c = i - r * per;
+            *(uint32_t*)(lds + r * lstride + c * 4) = *(const uint32_t*)(g + r * gstride + c * 4);
+        }
+    } else {
+        int tot = seg * nrows;
+        for (int i = tid; i < tot; i += nthreads) {
+            int r = i / seg, c = i - r * seg;
+            lds[r * lstride + c] = g[r * gstride + c];
+        }
+    }
+}
+
+// Sum over the 16 lanes of a row group in the halving-tree order
+// (xor 8, 4, 2, 1); every lane of the group ends with the same value.
+__device__ __forceinline__ float slot_reduce16(float v) {
+    v = v + __shfl_xor(v, 8, 16);
+    v = v + __shfl_xor(v, 4, 16);
+    v = v + __shfl_xor(v, 2, 16);
+    v = v + __shfl_xor(v, 1, 16);
+    return v;
+}
+
+}  // namespace chimere

@@ -1,0 +1,235 @@
+// mmvq.hip -- block-quantized GEMV (Q8_0 / Q4_0 / IQ3_S weights x Q8_1
+// activations) for 1..8 tokens, plain / batched-by-expert-id / debug dots.
+//
+// Work-group = 256 threads = 16 row groups of 16 lanes; one tile = 16
+// consecutive rows.  A row is consumed in chunks of 64 blocks: the 16 row
+// segments of a chunk are streamed HBM -> LDS with 16-byte loads, the
+// chunk's Q8_1 activation blocks are decoded once into LDS, then lane j of a
+// row group takes blocks j, j+16, j+32, ... of the chunk.  fp32 order
+// (L=16, G=1): per lane acc = fmaf(f32(d_w)*f32(d_x), (float)sumi, acc) over
+// its blocks in ascending order, then the 16 lanes are summed with the
+// halving tree xor 8,4,2,1.  sumi is the exact int32 block dot.
+#include "api_internal.h"
+#include "common.h"
+#include "tile_gemv.h"
+
+namespace chimere {
+
+void launch_quantize_q8_1(const float* x, void* out, int64_t ncols, int64_t ncols_padded,
+                          int64_t nrows, hipStream_t s);
+
+extern __constant__ uint32_t c_iq3s_grid_mmvq[512];
+__constant__ uint32_t c_iq3s_grid_mmvq[512] = CHIMERE_IQ3S_GRID_INIT;
+
+struct MmvqArgs {
+    const uint8_t* W;
+    const uint8_t* x;
+    float* y;
+    int ncols, nrows, ntok;
+    int64_t x_tok_stride;   // bytes between tokens' Q8_1 rows
+    int64_t y_tok_stride;   // floats between tokens' outputs
+    const int* ids;         // slot k -> expert ids[k]; NULL: expert k
+    int64_t w_slot_stride;  // bytes per expert
+    int64_t x_slot_stride;  // bytes between slots' inputs (0: shared)
+    int64_t y_slot_stride;  // floats between slots' outputs
+};
+
+template <int T, int NTOK>
+__global__ __launch_bounds__(GEMV_THREADS) void k_mmvq(MmvqArgs a) {
+    constexpr int CB = ChunkGeom<T>::BYTES;
+    __shared__ __attribute__((aligned(16))) uint8_t tile[TILE_ROWS * CB + 16];
+    __shared__ XLds xs[NTOK][CHUNK_BLOCKS];
+    __shared__ uint32_t grid[T == T_IQ3_S ? 512 : 1];
+
+    const int tid = threadIdx.x;
+    const int g = tid >> 4, j = tid & 15;
+    const int slot = blockIdx.y;
+    const int r0 = blockIdx.x * TILE_ROWS;
+    const int nr = min(TILE_ROWS, a.nrows - r0);
+    const int64_t e = a.ids ? (int64_t)a.ids[slot] : (int64_t)slot;
+    const int64_t rb = row_bytes(T, a.ncols);
+    if constexpr (T == T_IQ3_S)
+        for (int i = tid; i < 512; i += GEMV_THREADS) grid[i] = c_iq3s_grid_mmvq[i];
+
+    float acc[NTOK];
+    tile_gemv<T, NTOK>(tile, CB, xs, grid, a.W + e * a.w_slot_stride + (int64_t)r0 * rb, nr,
+                       nullptr, 0, rb, a.ncols, a.x + slot * a.x_slot_stride, a.x_tok_stride,
+                       nullptr, a.ntok, acc);
+    if (g < nr) {
+#pragma unroll
+        for (int t = 0; t < NTOK; t++) {
+            float v = slot_reduce16(acc[t]);
+            if (j == 0 && t < a.ntok) a.y[slot * a.y_slot_stride + t * a.y_tok_stride + r0 + g] = v;
+        }
+    }
+}
+
+template <int T>
+static void launch_t(const MmvqArgs& a, int nslots, hipStream_t s) {
+    dim3 grid((unsigned)((a.nrows + TILE_ROWS - 1) / TILE_ROWS), (unsigned)nslots);
+    dim3 blk(GEMV_THREADS);
+    switch (a.ntok) {
+#define CASE(N) case N: hipLaunchKernelGGL((k_mmvq<T, N>), grid, blk, 0, s, a); break;
+        CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8)
+#undef CASE
+    }
+}
+
+bool launch_mmvq(int type, const MmvqArgs& a, int nslots, hipStream_t s) {
+    switch (type) {
+    case T_Q8_0: launch_t<T_Q8_0>(a, nslots, s); break;
+    case T_Q4_0: launch_t<T_Q4_0>(a, nslots, s); break;
+    case T_IQ3_S: launch_t<T_IQ3_S>(a, nslots, s); break;
+    default: return false;
+    }
+    return true;
+}
+
+// Validates a GEMV request; returns false (error recorded) when rejected.
+static bool check_gemv(const char* who, int type, const void* W, const void* x, const float* y,
+                       int ncols, int nrows, int nrows_y_padded, int ntok) {
+    if (!W || !x || !y) { set_error(CHIMERE_ERR_ARG, "%s: null pointer", who); return false; }
+    if (type != T_Q8_0 && type != T_Q4_0 && type != T_IQ3_S) {
+        set_error(CHIMERE_ERR_ARG, "%s: unsupported type %d", who, type); return false;
+    }
+    const int elems = type == T_IQ3_S ? 256 : 32;
+    if (ncols <= 0 || nrows <= 0 || ncols % elems) {
+        set_error(CHIMERE_ERR_ARG, "%s: ncols=%d must be a positive multiple of %d (nrows=%d)",
+                  who, ncols, elems, nrows);
+        return false;
+    }
+    if (nrows_y_padded < ncols / 32) {
+        set_error(CHIMERE_ERR_ARG, "%s: nrows_y_padded=%d < ncols/32=%d", who, nrows_y_padded, ncols / 32);
+        return false;
+    }
+    if (ntok < 1 || ntok > 8) { set_error(CHIMERE_ERR_ARG, "%s: ntok=%d not in 1..8", who, ntok); return false; }
+    if (((uintptr_t)x & 3) != 0 || ((uintptr_t)W & 1) != 0) {
+        set_error(CHIMERE_ERR_ARG, "%s: Q8_1 input must be 4-byte and weights 2-byte aligned", who);
+        return false;
+    }
+    return true;
+}
+
+static void gemv_entry(const char* who, int type, const void* W, const void* x, float* y, int ncols,
+                       int nrows, int nrows_y_padded, int ntok, hipStream_t s) {
+    if (!check_gemv(who, type, W, x, y, ncols, nrows, nrows_y_padded, ntok)) return;
+    MmvqArgs a{(const uint8_t*)W, (const uint8_t*)x, y, ncols, nrows, ntok,
+               (int64_t)nrows_y_padded * Q8_1_BYTES, nrows, nullptr, 0, 0, 0};
+    launch_mmvq(type, a, 1, s);
+    check_launch(who);
+}
+
+static void gemv_f32_entry(const char* who, int type, const void* W, const float* x, float* y,
+                           int ncols, int nrows, int ncols_padded, void* scratch, hipStream_t s) {
+    if (!x || !scratch) { set_error(CHIMERE_ERR_ARG, "%s: null pointer", who); return; }
+    if (ncols_padded < ncols || ncols_padded % 32) {
+        set_error(CHIMERE_ERR_ARG, "%s: ncols_padded=%d invalid for ncols=%d", who, ncols_padded, ncols);
+        return;
+    }
+    if (!check_gemv(who, type, W, scratch, y, ncols, nrows, ncols_padded / 32, 1)) return;
+    launch_quantize_q8_1(x, scratch, ncols, ncols_padded, 1, s);
+    gemv_entry(who, type, W, scratch, y, ncols, nrows, ncols_padded / 32, 1, s);
+}
+
+static void gemv_batched_entry(const char* who, int type, const void* W, const void* x, float* y,
+                               const int* ids, int ncols, int nrows, int nrows_y_padded,
+                               int64_t expert_stride, int64_t input_stride, int top_k,
+                               hipStream_t s) {
+    if (!check_gemv(who, type, W, x, y, ncols, nrows, nrows_y_padded, 1)) return;
+    if (!ids || top_k <= 0 || expert_stride < row_bytes(type, ncols) * nrows || input_stride < 0 ||
+        (input_stride & 3)) {
+        set_error(CHIMERE_ERR_ARG, "%s: bad ids/top_k/strides (top_k=%d expert_stride=%lld input_stride=%lld)",
+                  who, top_k, (long long)expert_stride, (long long)input_stride);
+        return;
+    }
+    MmvqArgs a{(const uint8_t*)W, (const uint8_t*)x, y, ncols, nrows, 1,
+               0, 0, ids, expert_stride, input_stride, nrows};
+    launch_mmvq(type, a, top_k, s);
+    check_launch(who);
+}
+
+// ---- debug: exact int32 per-block dots, one thread per (row, block)
+__global__ void k_block_dots(int type, const uint8_t* __restrict__ W, const uint8_t* __restrict__ x,
+                             int32_t* __restrict__ out, int ncols, int nrows) {
+    __shared__ uint32_t grid[512];
+    for (int i = threadIdx.x; i < 512; i += blockDim.x) grid[i] = c_iq3s_grid_mmvq[i];
+    __syncthreads();
+    const int nb = ncols / 32;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)nb * nrows) return;
+    const int r = (int)(i / nb), b = (int)(i % nb);
+    const uint8_t* row = W + (int64_t)r * row_bytes(type, ncols);
+    // copy the block (or its superblock) into a private 4-byte aligned buffer
+    uint8_t buf[116] __attribute__((aligned(4)));
+    int len, off;
+    if (type == T_IQ3_S) { len = 110; off = (b >> 3) * 110; }
+    else { len = type == T_Q8_0 ? 34 : 18; off = b * len; }
+    for (int k = 0; k < len; k++) buf[k] = row[off + k];
+    XBlk xb;
+    load_xblk(x + (int64_t)b * Q8_1_BYTES, xb);
+    float dw;
+    int s;
+    if (type == T_Q8_0) s = dot_q8_0(buf, 0, xb, &dw);
+    else if (type == T_Q4_0) s = dot_q4_0(buf, 0, xb, &dw);
+    else s = dot_iq3_s(buf, 0, b & 7, xb, grid, &dw);
+    out[i] = s;
+}
+
+}  // namespace chimere
+
+using namespace chimere;
+
+extern "C" {
+
+void chimere_mmvq_iq3s(const void* w, const void* x, float* y, int ncols, int nrows, int nyp, hipStream_t s) {
+    gemv_entry("mmvq_iq3s", T_IQ3_S, w, x, y, ncols, nrows, nyp, 1, s);
+}
+void chimere_mmvq_q8_0(const void* w, const void* x, float* y, int ncols, int nrows, int nyp, hipStream_t s) {
+    gemv_entry("mmvq_q8_0", T_Q8_0, w, x, y, ncols, nrows, nyp, 1, s);
+}
+void chimere_mmvq_q4_0(const void* w, const void* x, float* y, int ncols, int nrows, int nyp, hipStream_t s) {
+    gemv_entry("mmvq_q4_0", T_Q4_0, w, x, y, ncols, nrows, nyp, 1, s);
+}
+
+void chimere_mmvq_iq3s_f32(const void* w, const float* x, float* y, int ncols, int nrows, int ncp,
+                           void* scratch, hipStream_t s) {
+    gemv_f32_entry("mmvq_iq3s_f32", T_IQ3_S, w, x, y, ncols, nrows, ncp, scratch, s);
+}
+void chimere_mmvq_q8_0_f32(const void* w, const float* x, float* y, int ncols, int nrows, int ncp,
+                           void* scratch, hipStream_t s) {
+    gemv_f32_entry("mmvq_q8_0_f32", T_Q8_0, w, x, y, ncols, nrows, ncp, scratch, s);
+}
+void chimere_mmvq_q4_0_f32(const void* w, const float* x, float* y, int ncols, int nrows, int ncp,
+                           void* scratch, hipStream_t s) {
+    gemv_f32_entry("mmvq_q4_0_f32", T_Q4_0, w, x, y, ncols, nrows, ncp, scratch, s);
+}
+
+void chimere_mmvq_iq3s_batched(const void* w, const void* x, float* y, const int* ids, int ncols,
+                               int nrows, int nyp, int64_t es, int64_t is, int top_k, hipStream_t s) {
+    gemv_batched_entry("mmvq_iq3s_batched", T_IQ3_S, w, x, y, ids, ncols, nrows, nyp, es, is, top_k, s);
+}
+void chimere_mmvq_q8_0_batched(const void* w, const void* x, float* y, const int* ids, int ncols,
+                               int nrows, int nyp, int64_t es, int64_t is, int top_k, hipStream_t s) {
+    gemv_batched_entry("mmvq_q8_0_batched", T_Q8_0, w, x, y, ids, ncols, nrows, nyp, es, is, top_k, s);
+}
+void chimere_mmvq_q4_0_batched(const void* w, const void* x, float* y, const int* ids, int ncols,
+                               int nrows, int nyp, int64_t es, int64_t is, int top_k, hipStream_t s) {
+    gemv_batched_entry("mmvq_q4_0_batched", T_Q4_0, w, x, y, ids, ncols, nrows, nyp, es, is, top_k, s);
+}
+
+void chimere_mmvq_multi(int type, const void* w, const void* x, float* y, int ncols, int nrows,
+                        int nyp, int ntok, hipStream_t s) {
+    gemv_entry("mmvq_multi", type, w, x, y, ncols, nrows, nyp, ntok, s);
+}
+
+void chimere_dbg_block_dots(int type, const void* w, const void* x, int32_t* out, int ncols,
+                            int nrows, hipStream_t s) {
+    if (!out || !check_gemv("dbg_block_dots", type, w, x, (const float*)out, ncols, nrows, ncols / 32, 1))
+        return;
+    int64_t n = (int64_t)(ncols / 32) * nrows;
+    hipLaunchKernelGGL(k_block_dots, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, type,
+                       (const uint8_t*)w, (const uint8_t*)x, out, ncols, nrows);
+    check_launch("dbg_block_dots");
+}
+
+}  // extern "C"

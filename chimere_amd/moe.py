@@ -1,0 +1,124 @@
+"""MoE FFN layer over libchimere_hip.so.
+
+``MoeLayer`` holds one layer's device weights (stacked expert tensors in the
+reference's GGUF block layout) and a preallocated workspace, and runs
+``chimere_moe_ffn_decode`` (router -> top-k -> gate/up+SiLU -> down ->
+weighted sum + shared expert) for 1..8 tokens, or ``chimere_moe_prefill``
+for a chunk of tokens.
+
+``forward_moe_v3`` replays the reference's own launch sequence
+(``chimere-server/src/qwen35_model/moe_ffn.rs:1094-1384`` V3 batched path and
+``:1597-1761`` shared expert) through the ``ggml_gpu`` mirror; it computes the
+same values as the fused entry point and serves as its cross-check.
+"""
+import ctypes as C
+
+import torch
+
+from . import ggml_gpu as G
+from ._lib import IQ3_S, Q4_0, Q8_0, MoeLayerC, check, lib
+
+_BLOCK = {Q8_0: (32, 34), Q4_0: (32, 18), IQ3_S: (256, 110)}
+
+
+def row_bytes(wtype, ncols):
+    e, b = _BLOCK[wtype]
+    return ncols // e * b
+
+
+class MoeLayer:
+    """One routed-MoE layer.
+
+    router_w [E, H] f32; gate/up [E, F*row_bytes(H)] u8; down [E, H*row_bytes(F)] u8;
+    shared = (gate [F*rb(H)], up, down [H*rb(F)]) u8 or None; sh_gate_w [H] f32 or None;
+    logit_bias [E] f32 or None.  All tensors on the same ROCm device.
+    """
+
+    def __init__(self, router_w, gate, up, down, expert_type, top_k, shared=None, shared_type=None,
+                 sh_gate_w=None, logit_bias=None, max_ntok=8):
+        E, H = router_w.shape
+        self.H, self.E, self.K = H, E, top_k
+        self.expert_type = expert_type
+        self.F = gate.numel() // E // row_bytes(expert_type, H)
+        self.shared_type = shared_type if shared is not None else -1
+        self.tensors = [router_w, gate, up, down, sh_gate_w, logit_bias] + list(shared or [])
+        self.c = MoeLayerC()
+        c = self.c
+        c.hidden, c.ffn, c.n_experts, c.top_k = H, self.F, E, top_k
+        c.expert_type, c.shared_type = expert_type, self.shared_type
+        c.router_w = router_w.data_ptr()
+        c.logit_bias = logit_bias.data_ptr() if logit_bias is not None else None
+        c.gate_exps, c.up_exps, c.down_exps = gate.data_ptr(), up.data_ptr(), down.data_ptr()
+        c.gate_stride = gate.numel() // E
+        c.up_stride = up.numel() // E
+        c.down_stride = down.numel() // E
+        if shared is not None:
+            c.sh_gate, c.sh_up, c.sh_down = (t.data_ptr() for t in shared)
+        c.sh_gate_w = sh_gate_w.data_ptr() if sh_gate_w is not None else None
+        self.max_ntok = max_ntok
+        self.ws_bytes = lib().chimere_moe_workspace_size(C.byref(c), max_ntok)
+        if self.ws_bytes == 0:
+            raise ValueError("chimere_moe_workspace_size rejected the layer shape")
+        self.workspace = torch.empty(self.ws_bytes, dtype=torch.uint8, device=router_w.device)
+        lib().chimere_moe_workspace_init(C.c_void_p(self.workspace.data_ptr()), self.ws_bytes, G._stream())
+        check()
+        self.device = router_w.device
+
+    def forward(self, x, out=None, ids=None, wts=None):
+        """x [M, H] f32 (M <= max_ntok) -> out [M, H]; ids/wts [M, K] optional outputs."""
+        M = x.shape[0]
+        if out is None:
+            out = torch.empty_like(x)
+        lib().chimere_moe_ffn_decode(C.byref(self.c), C.c_void_p(x.data_ptr()), C.c_void_p(out.data_ptr()), M,
+                                     C.c_void_p(ids.data_ptr()) if ids is not None else None,
+                                     C.c_void_p(wts.data_ptr()) if wts is not None else None,
+                                     C.c_void_p(self.workspace.data_ptr()), self.ws_bytes, G._stream())
+        check()
+        return out
+
+    # ------------------------------------------------------------------
+    def forward_moe_v3(self, x):
+        """One token through the reference's 7-launch V3 sequence + shared expert."""
+        assert x.numel() == self.H
+        H, F, E, K, t = self.H, self.F, self.E, self.K, self.expert_type
+        dev = self.device
+        router_w, gate, up, down, sh_gate_w, logit_bias = self.tensors[:6]
+        bufs = G.GgmlGpuBuffers.with_moe(max(H, F), max(H, F), F, H, K, device=dev)
+        router_out = torch.empty(E, dtype=torch.float32, device=dev)
+        ids = torch.empty(K, dtype=torch.int32, device=dev)
+        w = torch.empty(K, dtype=torch.float32, device=dev)
+        G.raw_f32_gemv(router_w, x, router_out, E, H)
+        if logit_bias is not None:
+            router_out += logit_bias
+        G.gpu_topk_softmax(router_out, ids, w, E, K)
+        G.ggml_gpu_quantize_q8_1(x, bufs.q8_input, H)
+        bat = {Q8_0: G.ggml_gpu_gemv_q8_0_batched, Q4_0: G.ggml_gpu_gemv_q4_0_batched,
+               IQ3_S: G.ggml_gpu_gemv_iq3s_batched}[t]
+        bat(gate, bufs.q8_input, bufs.batched_gate, ids, F, H, gate.numel() // E, 0, K)
+        bat(up, bufs.q8_input, bufs.batched_up, ids, F, H, up.numel() // E, 0, K)
+        G.silu_mul_inplace(bufs.batched_gate, bufs.batched_up, K * F)
+        G.ggml_gpu_quantize_q8_1_batched(bufs.batched_gate, bufs.batched_q8_inter, F, K)
+        bat(down, bufs.batched_q8_inter, bufs.batched_down, ids, H, F, down.numel() // E,
+            G.q8_1_row_bytes(F), K)
+        accum = torch.empty(H, dtype=torch.float32, device=dev)
+        G.weighted_combine_gpu(bufs.batched_down, w, accum, H, K)
+        if self.shared_type < 0:
+            return accum, ids, w
+        sg, su, sd = self.tensors[6:9]
+        st = self.shared_type
+        f32 = {Q8_0: G.ggml_gpu_gemv_q8_0_f32, Q4_0: G.ggml_gpu_gemv_q4_0_f32, IQ3_S: G.ggml_gpu_gemv_iq3s_f32}[st]
+        q8 = {Q8_0: G.ggml_gpu_gemv_q8_0_q8, Q4_0: G.ggml_gpu_gemv_q4_0_q8, IQ3_S: G.ggml_gpu_gemv_iq3s_q8}[st]
+        shg = torch.empty(F, dtype=torch.float32, device=dev)
+        shu = torch.empty(F, dtype=torch.float32, device=dev)
+        shd = torch.empty(H, dtype=torch.float32, device=dev)
+        f32(sg, x, shg, bufs.q8_input, F, H)
+        q8(su, bufs.q8_input, shu, F, H)
+        G.silu_mul_inplace(shg, shu, F)
+        f32(sd, shg, shd, bufs.q8_input_b, H, F)
+        if sh_gate_w is not None:
+            glogit = torch.empty(1, dtype=torch.float32, device=dev)
+            G.raw_f32_gemv(sh_gate_w, x, glogit, 1, H)
+            G.raw_sigmoid_gate_add_inplace(shd, glogit, accum, H)
+        else:
+            shd += accum
+        return shd, ids, w

@@ -1,0 +1,186 @@
+/*
+ * chimere_hip.h -- C ABI of libchimere_hip.so, the MI355X (gfx950) decode-time
+ * quantized GEMV / MoE-FFN path.
+ *
+ * Drop-in for the reference's extern "C" boundary
+ *   chimere-server/ffi/ggml_cuda_gemv.cu:94-463
+ * as declared on the Rust side in
+ *   chimere-server/src/kernels/ggml_gpu.rs:101-240.
+ * Names, argument order and meaning of the mirrored entry points are the
+ * reference's; cudaStream_t becomes hipStream_t (an opaque pointer; NULL is
+ * the default stream).  Every pointer argument is a caller-owned DEVICE
+ * pointer unless stated otherwise; outputs are overwritten.  No entry point
+ * allocates, frees or synchronizes, so all of them may be recorded into a
+ * HIP graph.  Entry points return void like the reference's; a rejected
+ * argument or a failed launch is reported by chimere_hip_get_last_error().
+ *
+ * Block formats (byte-exact with ggml): Q8_0 34 B / 32, Q4_0 18 B / 32,
+ * Q8_1 36 B / 32 ([f16 d][f16 s = sum x][i8 q[32]]), IQ3_S 110 B / 256.
+ * Type ids below follow ggml's enum.
+ */
+#ifndef CHIMERE_HIP_H
+#define CHIMERE_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CHIMERE_TYPE_Q4_0 2
+#define CHIMERE_TYPE_Q8_0 8
+#define CHIMERE_TYPE_IQ3_S 21
+
+/* error codes returned by chimere_hip_get_last_error() */
+#define CHIMERE_OK 0
+#define CHIMERE_ERR_ARG 1      /* rejected argument (shape, alignment, null, range) */
+#define CHIMERE_ERR_LAUNCH 2   /* kernel launch failed */
+#define CHIMERE_ERR_WORKSPACE 3/* workspace too small */
+
+/* ---------------------------------------------------------------- sizes */
+/* ggml_cuda_gemv.cu:197-209 */
+int chimere_q8_1_block_bytes(void);   /* 36 */
+int chimere_q8_1_block_elems(void);   /* 32 */
+int chimere_matrix_row_padding(void); /* 512 */
+
+/* ----------------------------------------------------- activation quant */
+/* ggml_cuda_gemv.cu:184-194.  input f32[ncols] -> Q8_1 blocks; out holds
+ * ncols_padded/32 blocks (elements ncols..ncols_padded-1 quantize as 0). */
+void chimere_quantize_q8_1(const float *input, void *output, int64_t ncols,
+                           int64_t ncols_padded, hipStream_t stream);
+/* ggml_cuda_gemv.cu:393-404.  batch rows of ncols (input row stride ncols);
+ * output row stride ncols_padded/32*36 bytes. */
+void chimere_quantize_q8_1_batched(const float *input, void *output, int64_t ncols,
+                                   int64_t ncols_padded, int batch, hipStream_t stream);
+
+/* --------------------------------------------------------------- GEMV */
+/* y[r] = W[r,:] . x for W [nrows, ncols] quantized, x Q8_1 with
+ * nrows_y_padded (= pad(ncols,512)/32) blocks.  ggml_cuda_gemv.cu:105-116
+ * (iq3s), :133-144 (q8_0); Q4_0 has no counterpart in the reference's ABI
+ * (ggml mul_mat_vec_q4_0_q8_1 is reached there only through libllama) and is
+ * added with the same signature. */
+void chimere_mmvq_iq3s(const void *weights, const void *input_q8, float *output,
+                       int ncols, int nrows, int nrows_y_padded, hipStream_t stream);
+void chimere_mmvq_q8_0(const void *weights, const void *input_q8, float *output,
+                       int ncols, int nrows, int nrows_y_padded, hipStream_t stream);
+void chimere_mmvq_q4_0(const void *weights, const void *input_q8, float *output,
+                       int ncols, int nrows, int nrows_y_padded, hipStream_t stream);
+
+/* Fused F32 -> Q8_1 -> GEMV (ggml_cuda_gemv.cu:302-387): quantizes input_f32
+ * into q8_scratch (pad(ncols,512)/32*36 bytes) then runs the GEMV. */
+void chimere_mmvq_iq3s_f32(const void *weights, const float *input_f32, float *output,
+                           int ncols, int nrows, int ncols_padded, void *q8_scratch,
+                           hipStream_t stream);
+void chimere_mmvq_q8_0_f32(const void *weights, const float *input_f32, float *output,
+                           int ncols, int nrows, int ncols_padded, void *q8_scratch,
+                           hipStream_t stream);
+void chimere_mmvq_q4_0_f32(const void *weights, const float *input_f32, float *output,
+                           int ncols, int nrows, int ncols_padded, void *q8_scratch,
+                           hipStream_t stream);
+
+/* Batched expert GEMV with device-resident expert ids (ggml_cuda_gemv.cu:243-279):
+ * for k < top_k: output[k*nrows + r] = W_{ids[k]}[r,:] . x_k with
+ * W_e = all_weights + e*expert_stride bytes and x_k = input_q8 + k*input_stride
+ * bytes (input_stride 0 = one shared input).  The q8_0 / q4_0 variants are
+ * additions with the same signature. */
+void chimere_mmvq_iq3s_batched(const void *all_weights, const void *input_q8, float *output,
+                               const int *expert_ids, int ncols, int nrows, int nrows_y_padded,
+                               int64_t expert_stride, int64_t input_stride, int top_k,
+                               hipStream_t stream);
+void chimere_mmvq_q8_0_batched(const void *all_weights, const void *input_q8, float *output,
+                               const int *expert_ids, int ncols, int nrows, int nrows_y_padded,
+                               int64_t expert_stride, int64_t input_stride, int top_k,
+                               hipStream_t stream);
+void chimere_mmvq_q4_0_batched(const void *all_weights, const void *input_q8, float *output,
+                               const int *expert_ids, int ncols, int nrows, int nrows_y_padded,
+                               int64_t expert_stride, int64_t input_stride, int top_k,
+                               hipStream_t stream);
+
+/* Multi-token dense GEMV (M <= 8 concurrent decode tokens; no reference
+ * counterpart -- the reference runs one token at a time): token t's Q8_1
+ * input at input_q8 + t*nrows_y_padded*36, output[t*nrows + r]. */
+void chimere_mmvq_multi(int type, const void *weights, const void *input_q8, float *output,
+                        int ncols, int nrows, int nrows_y_padded, int ntok, hipStream_t stream);
+
+/* ------------------------------------------------------- routing / glue */
+/* f32 GEMV, y[r] = sum_c A[r*cols+c] x[c]  (src/kernels/elementwise.rs:186-221,
+ * raw_f32_gemv :599-629); same 256-lane strided order and halving tree. */
+void chimere_f32_gemv(const float *A, const float *x, float *y, int rows, int cols,
+                      hipStream_t stream);
+/* softmax over n_experts logits, top-k by probability (ties -> lowest index),
+ * renormalised weights (kernels/chimere_kernels.cu:1150-1223,
+ * src/kernels/topk_softmax.rs:113).  ntok rows of logits (row stride
+ * n_experts); idx/w rows of top_k.  n_experts <= 1024. */
+void chimere_topk_softmax(const float *logits, int *top_idx, float *top_w, int n_experts,
+                          int top_k, int ntok, hipStream_t stream);
+/* gate[i] = silu(gate[i]) * up[i]   (src/kernels/fused_ops.rs:34-45) */
+void chimere_silu_mul_inplace(float *gate, const float *up, int n, hipStream_t stream);
+/* acc[h] = sum_k w[k] * expert_outs[k*hidden + h], k ascending
+ * (src/kernels/fused_ops.rs:364-378) */
+void chimere_weighted_combine(const float *expert_outs, const float *weights, float *acc,
+                              int hidden, int top_k, hipStream_t stream);
+/* out[i] = out[i] * sigmoid(gate[0]) + combined[i]  (src/scratch_pool.rs:264-277) */
+void chimere_sigmoid_gate_add(float *out, const float *gate_logit, const float *combined,
+                              int n, hipStream_t stream);
+
+/* ------------------------------------------------------ fused MoE layer */
+/* One routed MoE FFN layer (src/qwen35_model/moe_ffn.rs:1081-1768, V3
+ * batched path + shared expert): router f32 GEMV (+ optional per-expert
+ * logit bias) -> softmax/top-k/renorm -> Q8_1(x) -> gate/up GEMV of each
+ * selected expert -> silu(gate)*up -> Q8_1 -> down GEMV -> router-weighted
+ * sum (k ascending) -> + shared expert (times sigmoid(<x, sh_gate_w>) when
+ * sh_gate_w is non-NULL).  ntok <= 8 tokens route independently; each
+ * distinct selected expert's weights are streamed once per call. */
+typedef struct chimere_moe_layer {
+    int hidden;            /* H, multiple of 256 */
+    int ffn;               /* F, multiple of 256 (expert intermediate size) */
+    int n_experts;         /* E <= 1024 */
+    int top_k;             /* K <= 16 */
+    int expert_type;       /* CHIMERE_TYPE_* of gate/up/down experts */
+    int shared_type;       /* CHIMERE_TYPE_* of the shared expert, or -1 for none */
+    const float *router_w; /* [E, H] f32 row-major */
+    const float *logit_bias; /* [E] added to router logits, or NULL */
+    const void *gate_exps; /* [E] x [F rows of H] */
+    const void *up_exps;   /* [E] x [F rows of H] */
+    const void *down_exps; /* [E] x [H rows of F] */
+    int64_t gate_stride, up_stride, down_stride; /* bytes per expert */
+    const void *sh_gate, *sh_up, *sh_down;       /* shared expert, [F,H] [F,H] [H,F] */
+    const float *sh_gate_w;  /* [H] shared-expert gate vector or NULL (gate = 1) */
+} chimere_moe_layer;
+
+/* Workspace bytes for chimere_moe_ffn_decode at up to max_ntok tokens. */
+size_t chimere_moe_workspace_size(const chimere_moe_layer *layer, int max_ntok);
+/* Clears a workspace once after allocation (a fill kernel, graph-safe).  The
+ * MoE kernels leave their counters at zero on exit, so a workspace is reused
+ * across calls without clearing; calls sharing one workspace must not overlap. */
+void chimere_moe_workspace_init(void *workspace, size_t bytes, hipStream_t stream);
+/* x [ntok, H] f32 -> out [ntok, H] f32.  ids_out [ntok, K] / w_out [ntok, K]
+ * receive the routing when non-NULL. */
+void chimere_moe_ffn_decode(const chimere_moe_layer *layer, const float *x, float *out,
+                            int ntok, int *ids_out, float *w_out, void *workspace,
+                            size_t workspace_bytes, hipStream_t stream);
+
+/* ----------------------------------------------- weight quantizers (GPU) */
+/* Not part of the reference's ABI (its weights come pre-quantized from GGUF);
+ * used to build synthetic weights on the device.  n multiple of 32 (IQ3_S:
+ * 256).  Q8_0: src/kernels/kv_q8_0.rs:49-89; Q4_0: ggml reference rule;
+ * IQ3_S: this library's encoder (nearest codebook point per 4 values). */
+void chimere_quantize_weights(int type, const float *x, void *out, int64_t n,
+                              hipStream_t stream);
+
+/* ------------------------------------------------------------ debug */
+/* Exact int32 per-block dots: out[r*(ncols/32) + b] (IQ3_S: per 32-element
+ * sub-block, already multiplied by its (1 + 2*scale)). */
+void chimere_dbg_block_dots(int type, const void *weights, const void *input_q8,
+                            int32_t *out, int ncols, int nrows, hipStream_t stream);
+
+/* ------------------------------------------------------------ errors */
+/* Last error on the calling host thread (CHIMERE_OK if none); clears it. */
+int chimere_hip_get_last_error(void);
+const char *chimere_hip_get_last_error_string(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,91 @@
+/*
+ * oracle.h -- CPU restatement of the reference's decode-time quantized
+ * GEMV / MoE-FFN path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker for the HIP path:
+ * only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load
+ * it.  The product (chimere_amd/, libchimere_hip.so) never links or calls it.
+ *
+ * Block formats (byte-exact with ggml / the reference):
+ *   Q8_0  34 B / 32 elem : [f16 d][i8 q[32]]                 gguf_loader.rs:793-837
+ *   Q4_0  18 B / 32 elem : [f16 d][u8 nib[16]] lo=j, hi=j+16 gguf_loader.rs:752-772
+ *   Q8_1  36 B / 32 elem : [f16 d][f16 s][i8 q[32]]          chimere_kernels.cu:1495-1523
+ *   IQ3_S 110 B / 256 elem: [f16 d][qs 64][qh 8][signs 32][scales 4]
+ *                                                           gguf_loader.rs:1008-1142
+ * Type ids follow ggml's enum: Q4_0 = 2, Q8_0 = 8, IQ3_S = 21.
+ *
+ * Canonical fp32 order ("L,G order") of a quantized row dot product:
+ *   per 32-element block b (IQ3_S: sub-block b = 8*superblock + ib):
+ *     sumi_b  = exact int32 block dot (IQ3_S: times (1 + 2*scale))
+ *     scale_b = f32(d_w) * f32(d_x)                  (one rounding)
+ *   slot j in [0,L) accumulates the blocks with (b / G) % L == j, ascending b:
+ *     acc_j = fmaf(scale_b, (float)sumi_b, acc_j)    starting from +0.0f
+ *   then a halving tree: for m = L/2 .. 1: acc_i += acc_{i+m} (i < m); y = acc_0.
+ * The GPU kernels document the (L, G) they use; the oracle reproduces that
+ * order so that fp32 outputs (and hence every re-quantized intermediate)
+ * are bit-identical.
+ */
+#ifndef CHIMERE_ORACLE_H
+#define CHIMERE_ORACLE_H
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { ORC_Q4_0 = 2, ORC_Q8_0 = 8, ORC_IQ3_S = 21 };
+
+uint16_t orc_f32_to_f16(float x);
+float    orc_f16_to_f32(uint16_t h);
+float    orc_exp(float x);
+float    orc_silu(float g);
+
+int64_t  orc_row_bytes(int type, int64_t ncols);
+
+/* Q8_1 (ggml semantics).  nrows rows of ncols floats (row stride ncols);
+ * each output row is ncols_padded/32 blocks (elements >= ncols read as 0). */
+void orc_quantize_q8_1(const float *x, int64_t ncols, int64_t ncols_padded,
+                       int64_t nrows, uint8_t *out);
+/* weight quantizers; n multiple of 32 (IQ3_S: 256) */
+void orc_quantize_q8_0(const float *x, int64_t n, uint8_t *out);
+void orc_quantize_q4_0(const float *x, int64_t n, uint8_t *out);
+void orc_quantize_iq3_s(const float *x, int64_t n, uint8_t *out);
+void orc_dequantize(int type, const uint8_t *w, int64_t n, float *out);
+
+/* int32 block dots: out[r * (ncols/32) + b] */
+void orc_block_dots(int type, const uint8_t *W, const uint8_t *xq,
+                    int ncols, int nrows, int32_t *out);
+
+/* y[t*nrows + r] = row r of W . token t of xq (token stride xq_stride bytes) */
+void orc_gemv(int type, const uint8_t *W, const uint8_t *xq, int64_t xq_stride,
+              float *y, int ncols, int nrows, int ntok, int L, int G, int nthreads);
+
+/* reference CPU path for Q8_0 (f64 accumulation, unquantized x): ffi/src/lib.rs:107-154 */
+void orc_gemv_q8_0_f64(const uint8_t *W, const float *x, float *y,
+                       int ncols, int nrows);
+
+/* f32 router GEMV in the order of elementwise.rs:186-221 (256 slots, halving tree) */
+void orc_router(const float *Wr, const float *x, float *logits, int E, int H);
+/* softmax + top-k + renorm, chimere_kernels.cu:1150-1223 */
+void orc_topk_softmax(const float *logits, int E, int K, int32_t *idx, float *w);
+
+typedef struct {
+    int H, F, E, K, M;
+    int exp_type, sh_type;                 /* ggml type ids; sh_type < 0: no shared expert */
+    const float   *router;                 /* [E*H] f32 */
+    const float   *logit_bias;             /* [E] or NULL, added to router logits */
+    const uint8_t *gate, *up, *down;       /* stacked experts */
+    int64_t        stride_gate, stride_up, stride_down;  /* bytes per expert */
+    const uint8_t *sh_gate, *sh_up, *sh_down;
+    const float   *sh_gate_w;              /* [H] or NULL (gate = 1) */
+    int L, G;                              /* row-dot order */
+} orc_moe_params;
+
+/* Full MoE FFN layer for M tokens.  x [M*H], out [M*H]; optional debug
+ * outputs (may be NULL): ids [M*K], wts [M*K]. */
+void orc_moe(const orc_moe_params *p, const float *x, float *out,
+             int32_t *ids, float *wts, int nthreads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
