@@ -1,0 +1,256 @@
+"""Benchmark of the MI355X quantized decode path (BASELINE.json metric:
+"MoE decode FFN: effective HBM GB/s (% of peak) + us/layer at M=1 and M=8").
+
+Workload (value): BASELINE config 3 -- one Qwen3.5-35B-A3B-shaped MoE decode
+FFN layer at M=1: hidden 2048, 256 experts (gate/up 512x2048, down 2048x512,
+Q4_0), top-8 + one Q4_0 shared expert, f32 router 256x2048.  A step is one
+layer call (router -> top-k -> gate/up+SiLU -> down -> weighted sum + shared)
+on one token.  value = selected-expert bytes per step (8 x 1,769,472 B) /
+time per step.  Weights are synthetic N(0, 0.02), seeded, quantized on the
+device; each step uses a different (layer copy, token) slot so that the bytes
+come from HBM and not from the 256 MB Infinity Cache.  Timed as one HIP graph
+of exactly K steps between events, after W warm-up steps.
+
+Also reported (extra): M=8 IQ3_S layer (config 4, uniform and Zipf routing),
+the Q4_0 151936x2048 head GEMV (config 2), the Q8_0 4096x2048 GEMV (config 1),
+per-kernel times and the roofline of the dominant kernel, and the CPU
+baseline (the C restatement in oracle/, timed on this host).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+Q4_0, Q8_0, IQ3_S = 2, 8, 21
+
+
+def row_bytes(t, ncols):
+    return {Q8_0: ncols // 32 * 34, Q4_0: ncols // 32 * 18, IQ3_S: ncols // 256 * 110}[t]
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=64)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    return ap.parse_args()
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus > 1 or world > 1:
+        print("bench.py: this build runs on one GPU; --gpus above 1 is not supported", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from chimere_amd import ggml_gpu as G
+    from chimere_amd.moe import MoeLayer
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    def qmat(t, rows, cols, n, g):
+        out = torch.empty(n, rows * row_bytes(t, cols), dtype=torch.uint8, device=dev)
+        for i in range(n):   # chunked to bound the f32 staging memory
+            wf = torch.randn(rows, cols, generator=g, device=dev) * 0.02
+            G.quantize_weights(t, wf, out[i])
+        return out
+
+    def make_layer(seed, t, st, E=256, H=2048, F=512, K=8, bias=None):
+        g = torch.Generator(device=dev).manual_seed(seed)
+        router = torch.randn(E, H, generator=g, device=dev) * 0.02
+        gate, up, down = qmat(t, F, H, E, g), qmat(t, F, H, E, g), qmat(t, H, F, E, g)
+        sh = (qmat(st, F, H, 1, g)[0], qmat(st, F, H, 1, g)[0], qmat(st, H, F, 1, g)[0])
+        return MoeLayer(router, gate, up, down, t, K, shared=sh, shared_type=st, logit_bias=bias)
+
+    def graph_time(fn_list, reps=3):
+        """Capture fn_list (callables, each one step) in one HIP graph; return
+        the best-of-`reps` seconds per replay."""
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for f in fn_list[: min(4, len(fn_list))]:
+                f()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for f in fn_list:
+                f()
+        best = 1e30
+        for _ in range(reps):
+            gr.replay()                     # warm replay
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            gr.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            best = min(best, e0.elapsed_time(e1) / 1e3)
+        return best, gr
+
+    H, F, E, K = 2048, 512, 256, 8
+    sel_bytes = K * (2 * F * row_bytes(Q4_0, H) + H * row_bytes(Q4_0, F))       # 14,155,776
+    expert_bytes = sel_bytes // K
+    all_bytes = sel_bytes + expert_bytes + E * H * 4 + H * 4 * 2                  # + shared, router, x, out
+
+    # ---------------- headline: config 3, M=1 Q4_0, rotated over layer copies and tokens
+    R, NSLOT = 4, 64
+    layers = [make_layer(100 + r, Q4_0, Q4_0) for r in range(R)]
+    gx = torch.Generator(device=dev).manual_seed(7)
+    xs = torch.randn(NSLOT, 1, H, generator=gx, device=dev)
+    outs = torch.empty(NSLOT, 1, H, device=dev)
+    # one workspace per slot, so each slot keeps its own routing plan for the per-kernel timing
+    from chimere_amd._lib import lib
+    import ctypes as C
+    wss = []
+    for sidx in range(NSLOT):
+        L = layers[sidx % R]
+        w = torch.empty(L.ws_bytes, dtype=torch.uint8, device=dev)
+        lib().chimere_moe_workspace_init(C.c_void_p(w.data_ptr()), L.ws_bytes, G._stream())
+        wss.append(w)
+
+    def step_fn(i, stage=-1):
+        sidx = i % NSLOT
+        L = layers[sidx % R]
+        x, o, w = xs[sidx], outs[sidx], wss[sidx]
+
+        def f():
+            lib().chimere_moe_ffn_decode_stage(C.byref(L.c), C.c_void_p(x.data_ptr()), C.c_void_p(o.data_ptr()), 1,
+                                               C.c_void_p(w.data_ptr()), L.ws_bytes, stage, G._stream())
+        return f
+
+    # warm-up: W untimed steps (also prepares every slot's plan)
+    for i in range(max(args.warmup, NSLOT)):
+        step_fn(i)()
+    torch.cuda.synchronize()
+    t_step, _ = graph_time([step_fn(i) for i in range(args.steps)])
+    ms_per_step = t_step / args.steps * 1e3
+    us_layer = ms_per_step * 1e3
+    value = sel_bytes / (t_step / args.steps) / 1e9
+
+    # eager (no graph) time per layer for reference
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step_fn(i)()
+    torch.cuda.synchronize()
+    us_eager = (time.perf_counter() - t0) / args.steps * 1e6
+
+    # per-kernel timing: graphs of NSLOT launches of one stage each (slot plans prepared above)
+    per_kernel = {}
+    kbytes = {
+        "k_moe_route": E * H * 4 + H * 4 + E * 4 + (H // 32) * 36,
+        "k_moe_gate_up": 9 * 2 * F * row_bytes(Q4_0, H) + (H // 32) * 36 + 9 * F * 4 + 9 * (F // 32) * 36,
+        "k_moe_down": 9 * H * row_bytes(Q4_0, F) + 9 * (F // 32) * 36 + H * 4,
+    }
+    for stage, name in enumerate(["k_moe_route", "k_moe_gate_up", "k_moe_down"]):
+        n = 4 * NSLOT
+        t, _ = graph_time([step_fn(i, stage) for i in range(n)])
+        avg = t / n
+        per_kernel[name] = {"us": round(avg * 1e6, 3), "alg_bytes": kbytes[name],
+                            "GBs": round(kbytes[name] / avg / 1e9, 1)}
+    dom = max(per_kernel, key=lambda k: per_kernel[k]["us"])
+    ach = per_kernel[dom]["GBs"]
+    roofline = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom,
+                "alg_bytes_per_launch": kbytes[dom], "avg_launch_us": per_kernel[dom]["us"]}
+
+    extra = {"us_per_layer_m1": round(us_layer, 3), "us_per_layer_m1_eager": round(us_eager, 2),
+             "GBs_selected_m1": round(value, 1), "GBs_all_bytes_m1": round(all_bytes / (t_step / args.steps) / 1e9, 1),
+             "frac_of_peak_selected_m1": round(value / HBM_PEAK_GBS, 4), "per_kernel_m1": per_kernel}
+    del wss
+
+    if not args.no_extra:
+        # ---------------- config 4: M=8, IQ3_S experts + Q8_0 shared, uniform and Zipf routing
+        rng = np.random.default_rng(5)
+        perm = rng.permutation(E)
+        p = np.arange(1, E + 1, dtype=np.float64) ** -1.1
+        p /= p.sum()
+        b = np.empty(E, np.float32)
+        b[perm] = np.log(p).astype(np.float32)
+        zbias = torch.from_numpy(b).to(dev)
+        for label, bias in (("uniform", None), ("zipf1.1", zbias)):
+            R8 = 3
+            l8 = [make_layer(200 + r, IQ3_S, Q8_0, bias=bias) for r in range(R8)]
+            x8 = torch.randn(32, 8, H, generator=gx, device=dev)
+            o8 = torch.empty(8, H, device=dev)
+            ids = torch.empty(8, K, dtype=torch.int32, device=dev)
+            uniq = []
+            for i in range(32):
+                l8[i % R8].forward(x8[i], out=o8, ids=ids, wts=torch.empty(8, K, device=dev))
+                uniq.append(len(set(ids.cpu().numpy().reshape(-1).tolist())))
+            fns = [(lambda i=i: l8[i % R8].forward(x8[i % 32], out=o8)) for i in range(96)]
+            t8, _ = graph_time(fns)
+            us8 = t8 / 96 * 1e6
+            ub = np.mean(uniq) * (2 * F * row_bytes(IQ3_S, H) + H * row_bytes(IQ3_S, F))
+            extra[f"m8_iq3s_{label}"] = {"us_per_layer": round(us8, 2), "mean_unique_experts": round(float(np.mean(uniq)), 2),
+                                         "GBs_unique_expert_bytes": round(ub / (us8 * 1e-6) / 1e9, 1)}
+            del l8
+            torch.cuda.empty_cache()
+
+        # ---------------- config 2: Q4_0 head 151936 x 2048, three copies rotated
+        V = 151936
+        g = torch.Generator(device=dev).manual_seed(2)
+        heads = [qmat(Q4_0, V, H, 1, g)[0] for _ in range(3)]
+        xq = torch.empty(G.q8_1_row_bytes(H), dtype=torch.uint8, device=dev)
+        G.ggml_gpu_quantize_q8_1(torch.randn(H, generator=g, device=dev), xq, H)
+        y = torch.empty(V, device=dev)
+        fns = [(lambda i=i: G.ggml_gpu_gemv_q4_0_q8(heads[i % 3], xq, y, V, H)) for i in range(30)]
+        th, _ = graph_time(fns)
+        hb = V * row_bytes(Q4_0, H) + V * 4 + (H // 32) * 36
+        extra["head_q4_0_151936x2048"] = {"us": round(th / 30 * 1e6, 2), "GBs": round(hb / (th / 30) / 1e9, 1),
+                                          "frac": round(hb / (th / 30) / 1e9 / HBM_PEAK_GBS, 4)}
+        del heads
+        # ---------------- config 1: Q8_0 4096 x 2048, 64 copies rotated (570 MB)
+        q8w = qmat(Q8_0, 4096, H, 64, g)
+        y1 = torch.empty(4096, device=dev)
+        fns = [(lambda i=i: G.ggml_gpu_gemv_q8_0_q8(q8w[i % 64], xq, y1, 4096, H)) for i in range(256)]
+        t1, _ = graph_time(fns)
+        b1 = 4096 * row_bytes(Q8_0, H) + 4096 * 4 + (H // 32) * 36
+        extra["dense_q8_0_4096x2048"] = {"us": round(t1 / 256 * 1e6, 2), "GBs": round(b1 / (t1 / 256) / 1e9, 1)}
+        del q8w
+
+    # ---------------- CPU baseline: the oracle (C restatement, OpenMP) on this host, M=1 Q4_0 layer
+    cpu = None
+    if not args.no_cpu:
+        import oracle as O
+        L = layers[0]
+        h = lambda t: t.cpu().numpy()  # noqa: E731
+        hw = [h(t) for t in L.tensors[:4]]
+        hsh = tuple(h(t) for t in L.tensors[6:9])
+        nthreads = min(16, os.cpu_count() or 1)
+        xh = h(xs[:, 0])
+        O.moe(xh[0:1], *hw, O.Q4_0, K, sh=hsh, sh_type=O.Q4_0, nthreads=nthreads)   # warm
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_seconds and n < 2000:
+            O.moe(xh[n % NSLOT:n % NSLOT + 1], *hw, O.Q4_0, K, sh=hsh, sh_type=O.Q4_0, nthreads=nthreads)
+            n += 1
+        dt = (time.perf_counter() - t0) / n
+        cpu = {"value": round(sel_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
+               "sample": f"{n} M=1 Q4_0 MoE layer calls of config 3 (oracle/oracle.c, OpenMP row-parallel), "
+                         f"{dt * 1e6:.0f} us/layer"}
+
+    line = {"metric": "MoE decode FFN effective HBM GB/s on selected-expert bytes (M=1, Q4_0, Qwen3.5-35B-A3B shape)",
+            "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+            "config": {"workload": "BASELINE config 3: MoE decode FFN layer M=1 Q4_0, H=2048 F=512 E=256 top-8 + shared",
+                       "hidden": H, "ffn": F, "experts": E, "top_k": K, "tokens": 1, "slots_rotated": NSLOT,
+                       "layer_copies": R},
+            "roofline": roofline, "cpu_baseline": cpu, "extra": extra}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

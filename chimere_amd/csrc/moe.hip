@@ -484,29 +484,34 @@ static WsPlan plan_ws(int H, int F, int E, int K, int M) {
     return p;
 }
 
+// stage < 0: all three kernels; 0, 1, 2: only K1, K2 or K3
 template <int TE, int TS>
-static void launch_layer(const MoeArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(k_moe_route, dim3(a.E + (a.sh_gate_w ? 1 : 0)), dim3(256), 0, s, a);
-    hipLaunchKernelGGL((k_moe_gate_up<TE, TS>), dim3(a.F / 8, a.M * a.K + 1), dim3(GEMV_THREADS), 0, s, a);
-    hipLaunchKernelGGL((k_moe_down<TE, TS>), dim3((a.H + TILE_ROWS - 1) / TILE_ROWS), dim3(GEMV_THREADS), 0, s, a);
+static void launch_layer(const MoeArgs& a, int stage, hipStream_t s) {
+    if (stage < 0 || stage == 0)
+        hipLaunchKernelGGL(k_moe_route, dim3(a.E + (a.sh_gate_w ? 1 : 0)), dim3(256), 0, s, a);
+    if (stage < 0 || stage == 1)
+        hipLaunchKernelGGL((k_moe_gate_up<TE, TS>), dim3(a.F / 8, a.M * a.K + 1), dim3(GEMV_THREADS), 0, s, a);
+    if (stage < 0 || stage == 2)
+        hipLaunchKernelGGL((k_moe_down<TE, TS>), dim3((a.H + TILE_ROWS - 1) / TILE_ROWS), dim3(GEMV_THREADS), 0,
+                           s, a);
 }
 
 template <int TE>
-static bool dispatch_ts(int ts, const MoeArgs& a, hipStream_t s) {
+static bool dispatch_ts(int ts, const MoeArgs& a, int stage, hipStream_t s) {
     switch (ts) {
-    case T_Q8_0: launch_layer<TE, T_Q8_0>(a, s); return true;
-    case T_Q4_0: launch_layer<TE, T_Q4_0>(a, s); return true;
-    case T_IQ3_S: launch_layer<TE, T_IQ3_S>(a, s); return true;
+    case T_Q8_0: launch_layer<TE, T_Q8_0>(a, stage, s); return true;
+    case T_Q4_0: launch_layer<TE, T_Q4_0>(a, stage, s); return true;
+    case T_IQ3_S: launch_layer<TE, T_IQ3_S>(a, stage, s); return true;
     }
     return false;
 }
 
-static bool dispatch_layer(int te, int ts, const MoeArgs& a, hipStream_t s) {
+static bool dispatch_layer(int te, int ts, const MoeArgs& a, int stage, hipStream_t s) {
     if (ts < 0) ts = te;
     switch (te) {
-    case T_Q8_0: return dispatch_ts<T_Q8_0>(ts, a, s);
-    case T_Q4_0: return dispatch_ts<T_Q4_0>(ts, a, s);
-    case T_IQ3_S: return dispatch_ts<T_IQ3_S>(ts, a, s);
+    case T_Q8_0: return dispatch_ts<T_Q8_0>(ts, a, stage, s);
+    case T_Q4_0: return dispatch_ts<T_Q4_0>(ts, a, stage, s);
+    case T_IQ3_S: return dispatch_ts<T_IQ3_S>(ts, a, stage, s);
     }
     return false;
 }
@@ -574,9 +579,8 @@ void chimere_moe_workspace_init(void* ws, size_t bytes, hipStream_t s) {
     check_launch("moe_workspace_init");
 }
 
-void chimere_moe_ffn_decode(const chimere_moe_layer* L, const float* x, float* out, int ntok,
-                            int* ids_out, float* w_out, void* workspace, size_t ws_bytes,
-                            hipStream_t stream) {
+static void moe_decode(const chimere_moe_layer* L, const float* x, float* out, int ntok, int* ids_out,
+                       float* w_out, void* workspace, size_t ws_bytes, int stage, hipStream_t stream) {
     CHIMERE_REQUIRE(L && x && out && workspace, CHIMERE_ERR_ARG, "moe_ffn_decode: null pointer");
     const int H = L->hidden, F = L->ffn, E = L->n_experts, K = L->top_k;
     CHIMERE_REQUIRE(ntok >= 1 && ntok <= MAX_TOK, CHIMERE_ERR_ARG, "moe_ffn_decode: ntok=%d not in 1..8", ntok);
@@ -617,8 +621,20 @@ void chimere_moe_ffn_decode(const chimere_moe_layer* L, const float* x, float* o
     a.u_pair = (int*)(w + p.u_pair); a.u_tok = (int*)(w + p.u_tok);
     a.xq = w + p.xq; a.h = (float*)(w + p.h); a.hq = w + p.hq;
     a.xq_stride = p.xq_stride; a.hq_stride = p.hq_stride;
-    dispatch_layer(L->expert_type, L->shared_type, a, stream);
+    dispatch_layer(L->expert_type, L->shared_type, a, stage, stream);
     check_launch("moe_ffn_decode");
+}
+
+void chimere_moe_ffn_decode(const chimere_moe_layer* L, const float* x, float* out, int ntok,
+                            int* ids_out, float* w_out, void* workspace, size_t ws_bytes,
+                            hipStream_t stream) {
+    moe_decode(L, x, out, ntok, ids_out, w_out, workspace, ws_bytes, -1, stream);
+}
+
+void chimere_moe_ffn_decode_stage(const chimere_moe_layer* L, const float* x, float* out, int ntok,
+                                  void* workspace, size_t ws_bytes, int stage, hipStream_t stream) {
+    CHIMERE_REQUIRE(stage >= -1 && stage <= 2, CHIMERE_ERR_ARG, "moe_ffn_decode_stage: stage %d", stage);
+    moe_decode(L, x, out, ntok, nullptr, nullptr, workspace, ws_bytes, stage, stream);
 }
 
 void chimere_f32_gemv(const float* A, const float* x, float* y, int rows, int cols, hipStream_t s) {

@@ -71,7 +71,9 @@ __global__ void k_quant_q4_0(const float* __restrict__ x, uint8_t* __restrict__ 
     }
     float d = mx / -8.0f;
     float id = d != 0.0f ? 1.0f / d : 0.0f;
-    uint32_t h = f2h(d);
+    // an all-zero block has d = 0 / -8 = -0.0 (f16 0x8000), as the reference
+    // rule produces; spelled out because the compiler may fold the sign away
+    uint32_t h = mx == 0.0f ? 0x8000u : f2h(d);
     o[0] = (uint8_t)h; o[1] = (uint8_t)(h >> 8);
     for (int j = 0; j < 16; j++) {
         int a = (int)(v[j] * id + 8.5f), c = (int)(v[j + 16] * id + 8.5f);

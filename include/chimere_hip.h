@@ -161,6 +161,14 @@ void chimere_moe_ffn_decode(const chimere_moe_layer *layer, const float *x, floa
                             int ntok, int *ids_out, float *w_out, void *workspace,
                             size_t workspace_bytes, hipStream_t stream);
 
+/* Profiling variant (no reference counterpart): launches only kernel `stage`
+ * of chimere_moe_ffn_decode (0 router/top-k, 1 gate/up + SiLU, 2 down +
+ * combine; -1 all) on a workspace that a full call with the same layer, x and
+ * ntok has prepared; used to time each kernel on its own. */
+void chimere_moe_ffn_decode_stage(const chimere_moe_layer *layer, const float *x, float *out,
+                                  int ntok, void *workspace, size_t workspace_bytes, int stage,
+                                  hipStream_t stream);
+
 /* ----------------------------------------------- weight quantizers (GPU) */
 /* Not part of the reference's ABI (its weights come pre-quantized from GGUF);
  * used to build synthetic weights on the device.  n multiple of 32 (IQ3_S:
