@@ -3,22 +3,23 @@
 // glue (cs/src/kernels/{elementwise,topk_softmax,fused_ops}.rs,
 // cs/src/scratch_pool.rs).
 //
-// Layer = 3 launches on the caller's stream:
+// Layer = 3 launches on the caller's stream; no work-group ever waits on
+// another (kernel boundaries are the only synchronisation, so no device-scope
+// fences or counters are needed):
 //   K1 k_moe_route    one work-group per router row (+1 for the shared-expert
-//                     gate vector): f32 logits for every token; the last
-//                     work-group to finish (ticket counter) runs softmax/top-k
-//                     per token, quantizes x to Q8_1 and builds the list of
-//                     distinct selected experts with their (token, k) pairs.
-//   K2 k_moe_gate_up  (8-row chunk of F) x (distinct expert | shared): 8 gate
-//                     rows + 8 up rows per 16-row tile, each weight byte read
-//                     once for all tokens routed to the expert; h =
-//                     silu(gate)*up; the last of the four work-groups covering
-//                     a 32-row block quantizes it to Q8_1.
+//                     gate vector) computing f32 logits for every token, plus
+//                     one work-group per token quantizing x to Q8_1.
+//   K2 k_moe_gate_up  (8-row chunk of F) x (distinct expert | shared).  Each
+//                     routed work-group recomputes softmax/top-k (one wave per
+//                     token, registers only) and the distinct-expert plan from
+//                     the 1 KB of logits, then streams 8 gate + 8 up rows of
+//                     its expert once for all tokens routed to it and writes
+//                     h = silu(gate)*up in f32.
 //   K3 k_moe_down     16 hidden rows per work-group over all selected experts
-//                     (tiles of several experts staged together), then the
-//                     router-weighted sum in k order plus the shared expert.
-// Every row dot uses the (L=16, G=1) order of tile_gemv.h.  Ticket counters
-// return to zero before each kernel exits.
+//                     (tiles of several experts staged together with the Q8_1
+//                     re-quantization of their h), then the router-weighted
+//                     sum in k order plus the shared expert.
+// Every row dot uses the (L=16, G=1) order of tile_gemv.h.
 #include "api_internal.h"
 #include "common.h"
 #include "tile_gemv.h"
@@ -30,7 +31,6 @@ __constant__ uint32_t c_iq3s_grid_moe[512] = CHIMERE_IQ3S_GRID_INIT;
 constexpr int MAX_TOK = 8;
 constexpr int MAX_K = 16;
 constexpr int MAX_E = 1024;
-constexpr int DOWN_LDS_BUDGET = 40 * 1024;
 
 // ------------------------------------------------------------ reductions
 
@@ -58,17 +58,6 @@ __device__ __forceinline__ float tree_sum256(float v, float* red) {
     return v;
 }
 
-__device__ __forceinline__ float block_max256(float v, float* red) {
-    const int tid = threadIdx.x;
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, m));
-    if ((tid & 63) == 0) red[tid >> 6] = v;
-    __syncthreads();
-    v = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
-    __syncthreads();
-    return v;
-}
-
 // f32 row dot of `a` (H) against NT tokens of x (token stride H), in the
 // reference's order: thread t accumulates columns t, t+256, ... with fused
 // multiply-add, then tree_sum256.  Results valid in thread 0.
@@ -91,72 +80,97 @@ __device__ __forceinline__ void f32_row_dot(const float* __restrict__ a, const f
 
 // ---------------------------------------------------------------- top-k
 
-// Softmax + top-k + renormalisation of one logits row by a 256-thread group
-// (cs/kernels/chimere_kernels.cu:1150-1223): p = exp(l - max) / sum with the
-// sum taken by the strided halving tree; k rounds of arg-max by probability
-// (ties -> lowest index); weights renormalised by the sequential sum of the
-// selected probabilities.  `logits` may be in global memory; lp/lev are LDS
-// scratch of E floats.
-__device__ void topk_group(const float* logits, int E, int K, int* idx, float* w,
-                           float* lp, float* lev, float* red, int* redi) {
-    const int tid = threadIdx.x;
+// Softmax + top-k + renormalisation of one logits row by ONE wavefront, in
+// registers (cs/kernels/chimere_kernels.cu:1150-1223): lane l holds logits
+// l, l+64, ... (NV = ceil(E/64) values, zero-padded).  p = exp(l - max) / sum
+// where the sum follows the reference's strided halving tree (strides
+// 512..64 pair values inside a lane, strides 32..1 pair lanes; padding adds
+// +0, which leaves the non-negative partial sums unchanged); k rounds of
+// arg-max by probability, ties to the lowest index; weights renormalised by
+// the sequential sum of the selected probabilities.  Every lane ends with
+// the same idx[]/w[]; lane k < K writes entry k.
+template <int NV>
+__device__ __forceinline__ void topk_wave(const float* __restrict__ logits, int E, int K,
+                                          int* __restrict__ idx_out, float* __restrict__ w_out) {
+    const int lane = threadIdx.x & 63;
+    float p[NV], ev[NV];
     float mx = -__builtin_huge_valf();
-    for (int i = tid; i < E; i += 256) mx = __builtin_fmaxf(mx, logits[i]);
-    mx = block_max256(mx, red);
-    for (int i = tid; i < E; i += 256) {
-        const float e = det_exp(logits[i] - mx);
-        lev[i] = e;
-        lp[i] = e;
-    }
-    __syncthreads();
-    for (int st = 512; st >= 1; st >>= 1) {
-        for (int t = tid; t < st; t += 256)
-            if (t + st < E) lp[t] = lp[t] + lp[t + st];
-        __syncthreads();
-    }
-    const float sum = lp[0];
-    __syncthreads();
-    for (int i = tid; i < E; i += 256) lp[i] = sum > 0.0f ? lev[i] / sum : 1.0f / (float)E;
-    __syncthreads();
-    for (int k = 0; k < K; k++) {
-        float bv = -2.0f;
-        int bi = 0x7fffffff;
-        for (int i = tid; i < E; i += 256)
-            if (lp[i] > bv) { bv = lp[i]; bi = i; }
 #pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) {
-            const float ov = __shfl_xor(bv, m);
-            const int oi = __shfl_xor(bi, m);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-        }
-        if ((tid & 63) == 0) { red[tid >> 6] = bv; redi[tid >> 6] = bi; }
-        __syncthreads();
-        if (tid == 0) {
-            for (int q = 1; q < 4; q++)
-                if (red[q] > bv || (red[q] == bv && redi[q] < bi)) { bv = red[q]; bi = redi[q]; }
+    for (int i = 0; i < NV; i++) {
+        const int j = lane + 64 * i;
+        p[i] = j < E ? logits[j] : -__builtin_huge_valf();
+        mx = __builtin_fmaxf(mx, p[i]);
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, m));
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        ev[i] = (lane + 64 * i) < E ? det_exp(p[i] - mx) : 0.0f;
+        p[i] = ev[i];
+    }
+#pragma unroll
+    for (int h = NV / 2; h >= 1; h >>= 1)        // strides 64*h: in-lane pairs
+#pragma unroll
+        for (int i = 0; i < h; i++) p[i] = p[i] + p[i + h];
+    float s = p[0];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) s = s + __shfl_xor(s, m);
+    // s equals lane 0's value of the halving tree on every lane
+#pragma unroll
+    for (int i = 0; i < NV; i++)
+        p[i] = (lane + 64 * i) < E ? (s > 0.0f ? ev[i] / s : 1.0f / (float)E) : -2.0f;
+    int idx[MAX_K];
+    float w[MAX_K];
+#pragma unroll
+    for (int k = 0; k < MAX_K; k++) {
+        if (k < K) {
+            float bv = -3.0f;
+            int bi = 0x7fffffff;
+#pragma unroll
+            for (int i = 0; i < NV; i++)
+                if (p[i] > bv) { bv = p[i]; bi = lane + 64 * i; }
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) {
+                const float ov = __shfl_xor(bv, m);
+                const int oi = __shfl_xor(bi, m);
+                if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+            }
             idx[k] = bi;
             w[k] = bv;
-            lp[bi] = -1.0f;
-        }
-        __syncthreads();
-    }
-    if (tid == 0) {
-        float ws = 0.0f;
-        for (int k = 0; k < K; k++) ws += w[k];
-        if (ws > 0.0f) {
-            const float inv = 1.0f / ws;
-            for (int k = 0; k < K; k++) w[k] = w[k] * inv;
+#pragma unroll
+            for (int i = 0; i < NV; i++)
+                if (lane + 64 * i == bi) p[i] = -1.0f;
         }
     }
-    __syncthreads();
+    float ws = 0.0f;
+#pragma unroll
+    for (int k = 0; k < MAX_K; k++)
+        if (k < K) ws += w[k];
+    const float inv = ws > 0.0f ? 1.0f / ws : 1.0f;
+#pragma unroll
+    for (int k = 0; k < MAX_K; k++) {
+        if (k < K && lane == k) {
+            idx_out[k] = idx[k];
+            w_out[k] = ws > 0.0f ? w[k] * inv : w[k];
+        }
+    }
+}
+
+__device__ __forceinline__ void topk_wave_any(const float* logits, int E, int K, int* idx, float* w) {
+    if (E <= 64) topk_wave<1>(logits, E, K, idx, w);
+    else if (E <= 128) topk_wave<2>(logits, E, K, idx, w);
+    else if (E <= 256) topk_wave<4>(logits, E, K, idx, w);
+    else if (E <= 512) topk_wave<8>(logits, E, K, idx, w);
+    else topk_wave<16>(logits, E, K, idx, w);
 }
 
 // Q8_1 quantization of `nblk` 32-blocks (ggml semantics, see quant.hip) by a
 // 256-thread group, one half-wave per block.  src(b, i) is element i of block
-// b; dst(b) is the 36-byte output block.
-template <class Src, class Dst>
-__device__ __forceinline__ void quantize_blocks(int nblk, Src src, Dst dst) {
-    for (int b = threadIdx.x >> 5; b < nblk; b += 8) {
+// b; emit(b, i, q, d, sum) receives the block's results (every lane gets d
+// and sum).
+template <class Src, class Emit>
+__device__ __forceinline__ void quantize_blocks(int nblk, Src src, Emit emit) {
+    for (int b = threadIdx.x >> 5; b < nblk; b += GEMV_THREADS / 32) {
         const int i = threadIdx.x & 31;
         const float xi = src(b, i);
         float amax = __builtin_fabsf(xi), sum = xi;
@@ -167,9 +181,7 @@ __device__ __forceinline__ void quantize_blocks(int nblk, Src src, Dst dst) {
         }
         const float d = amax / 127.0f;
         const int q = amax == 0.0f ? 0 : (int)__builtin_roundf(xi / d);
-        uint8_t* blk = dst(b);
-        blk[4 + i] = (uint8_t)(int8_t)q;
-        if (i == 0) *(uint32_t*)blk = f2h(d) | (f2h(sum) << 16);
+        emit(b, i, q, d, sum);
     }
 }
 
@@ -189,104 +201,126 @@ struct MoeArgs {
     int* ids_out;
     float* w_out;
     // workspace
-    int* route_cnt;     // [1]
-    int* gu_cnt;        // [(M*K+1) * F/32]
     float* logits;      // [M*E]
     float* glogit;      // [M]
-    int* ids;           // [M*K]
     float* wts;         // [M*K]
-    int* n_unique;      // [1]
-    int* uexp;          // [M*K]
-    int* u_ntok;        // [M*K]
-    int* u_pair;        // [M*K][MAX_TOK]  pair = t*K + k
-    int* u_tok;         // [M*K][MAX_TOK]
+    int* plan;          // n_unique, uexp[M*K], u_ntok[M*K], u_pair[M*K][MAX_TOK]
     uint8_t* xq;        // [M][xq_stride]
     float* h;           // [M*K + M][F]
-    uint8_t* hq;        // [M*K + M][hq_stride]
-    int64_t xq_stride, hq_stride;
+    int64_t xq_stride;
 };
 
+// Expert plan: distinct selected experts and, per expert, its (token, k) pairs.
+struct Plan {
+    int nu;
+    int uexp[MAX_TOK * MAX_K];
+    int untok[MAX_TOK * MAX_K];
+    int upair[MAX_TOK * MAX_K][MAX_TOK];
+    int utok[MAX_TOK * MAX_K][MAX_TOK];
+};
+
+// K1: grid E (router rows) + has_gate (shared-expert gate row) + M (x quantizers).
 __global__ __launch_bounds__(256) void k_moe_route(MoeArgs a) {
     __shared__ float red[256];
-    __shared__ int redi[4];
-    __shared__ int ticket;
-    __shared__ float lp[MAX_E], lev[MAX_E];
     const int row = blockIdx.x;
-    const int tid = threadIdx.x;
+    const int ng = a.sh_gate_w ? 1 : 0;
+    if (row >= a.E + ng) {
+        const int t = row - a.E - ng;
+        const int nb = a.H / QK;
+        const float* xt = a.x + (int64_t)t * a.H;
+        uint8_t* dst = a.xq + t * a.xq_stride;
+        quantize_blocks(
+            nb, [&](int b, int i) { return xt[b * QK + i]; },
+            [&](int b, int i, int q, float d, float sum) {
+                uint8_t* blk = dst + b * Q8_1_BYTES;
+                blk[4 + i] = (uint8_t)(int8_t)q;
+                if (i == 0) *(uint32_t*)blk = f2h(d) | (f2h(sum) << 16);
+            });
+        return;
+    }
     float v[MAX_TOK];
     const float* A = row < a.E ? a.router + (int64_t)row * a.H : a.sh_gate_w;
     f32_row_dot<MAX_TOK>(A, a.x, a.H, a.M, red, v);
-    if (tid == 0) {
+    if (threadIdx.x == 0) {
         for (int t = 0; t < a.M; t++) {
             if (row < a.E) a.logits[t * a.E + row] = a.bias ? v[t] + a.bias[row] : v[t];
             else a.glogit[t] = v[t];
         }
     }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) ticket = atomicAdd(a.route_cnt, 1);
-    __syncthreads();
-    if (ticket != (int)gridDim.x - 1) return;
-    __threadfence();
-    // ---- last work-group: routing for every token, Q8_1(x), expert plan
-    for (int t = 0; t < a.M; t++) {
-        topk_group(a.logits + t * a.E, a.E, a.K, a.ids + t * a.K, a.wts + t * a.K, lp, lev, red, redi);
-    }
-    {
-        const int nbpr = a.H / QK;
-        quantize_blocks(
-            a.M * nbpr,
-            [&](int b, int i) { return a.x[(int64_t)(b / nbpr) * a.H + (b % nbpr) * QK + i]; },
-            [&](int b) { return a.xq + (int64_t)(b / nbpr) * a.xq_stride + (int64_t)(b % nbpr) * Q8_1_BYTES; });
-    }
-    if (tid == 0) {
-        int* map = (int*)lp;   // reuse: expert -> distinct index
-        for (int e = 0; e < a.E; e++) map[e] = -1;
-        int nu = 0;
-        for (int t = 0; t < a.M; t++)
-            for (int k = 0; k < a.K; k++) {
-                const int e = a.ids[t * a.K + k];
-                int u = map[e];
-                if (u < 0) { u = nu++; map[e] = u; a.uexp[u] = e; a.u_ntok[u] = 0; }
-                const int n = a.u_ntok[u]++;
-                a.u_pair[u * MAX_TOK + n] = t * a.K + k;
-                a.u_tok[u * MAX_TOK + n] = t;
-            }
-        *a.n_unique = nu;
-        if (a.ids_out)
-            for (int i = 0; i < a.M * a.K; i++) { a.ids_out[i] = a.ids[i]; a.w_out[i] = a.wts[i]; }
-        *a.route_cnt = 0;
-    }
 }
 
-// K2: grid (F/8, M*K + 1).  blockIdx.y < n_unique: routed expert; == M*K: shared.
+// K2: grid (F/8, M*K + 1).  Every routed work-group recomputes the routing
+// (top-k per token, one wave each) and the distinct-expert plan from the
+// logits, so no work-group waits on another; blockIdx.y < n_unique selects a
+// distinct expert, blockIdx.y == M*K the shared expert.  Work-group (0,0)
+// publishes routing and plan for K3.  8 gate rows + 8 up rows per tile;
+// h = silu(gate) * up is written in f32.
 template <int TE, int TS>
 __global__ __launch_bounds__(GEMV_THREADS) void k_moe_gate_up(MoeArgs a) {
     constexpr int CBE = ChunkGeom<TE>::BYTES, CBS = ChunkGeom<TS>::BYTES;
     constexpr int CB = CBE > CBS ? CBE : CBS;
-    __shared__ __attribute__((aligned(16))) uint8_t tile[TILE_ROWS * CB + 16];
+    // the tile buffer first holds the expert map and the plan (routing phase)
+    constexpr int ROUTE_BYTES = MAX_E * 4 + (int)sizeof(Plan);
+    constexpr int TILE_BYTES = TILE_ROWS * CB + 16 > ROUTE_BYTES ? TILE_ROWS * CB + 16 : ROUTE_BYTES;
+    __shared__ __attribute__((aligned(16))) uint8_t tile[TILE_BYTES];
     __shared__ XLds xs[MAX_TOK][CHUNK_BLOCKS];
     __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
     __shared__ float res[TILE_ROWS][MAX_TOK];
     __shared__ int toks[MAX_TOK], pairs[MAX_TOK];
-    __shared__ int ticket;
+    __shared__ int s_ids[MAX_TOK * MAX_K];
+    __shared__ float s_w[MAX_TOK * MAX_K];
+    Plan& pl = *(Plan*)(tile + MAX_E * 4);
 
     const int u = blockIdx.y;
     const bool shared = u == a.M * a.K;
-    if (shared ? !a.has_shared : u >= *a.n_unique) return;
     const int tid = threadIdx.x;
-    const int r0 = blockIdx.x * 8;
+    if (shared && !a.has_shared) return;
     int ntok;
     if (shared) {
         ntok = a.M;
         if (tid < a.M) { toks[tid] = tid; pairs[tid] = a.M * a.K + tid; }
     } else {
-        ntok = a.u_ntok[u];
-        if (tid < ntok) { toks[tid] = a.u_tok[u * MAX_TOK + tid]; pairs[tid] = a.u_pair[u * MAX_TOK + tid]; }
+        const int wave = tid >> 6;
+        for (int t = wave; t < a.M; t += GEMV_THREADS / 64)
+            topk_wave_any(a.logits + t * a.E, a.E, a.K, s_ids + t * a.K, s_w + t * a.K);
+        int* map = (int*)tile;
+        for (int e = tid; e < a.E; e += GEMV_THREADS) map[e] = -1;
+        __syncthreads();
+        if (tid == 0) {
+            int nu = 0;
+            for (int t = 0; t < a.M; t++)
+                for (int k = 0; k < a.K; k++) {
+                    const int e = s_ids[t * a.K + k];
+                    int uu = map[e];
+                    if (uu < 0) { uu = nu++; map[e] = uu; pl.uexp[uu] = e; pl.untok[uu] = 0; }
+                    const int n = pl.untok[uu]++;
+                    pl.upair[uu][n] = t * a.K + k;
+                    pl.utok[uu][n] = t;
+                }
+            pl.nu = nu;
+        }
+        __syncthreads();
+        if (blockIdx.x == 0 && u == 0) {
+            const int nu = pl.nu;
+            for (int i = tid; i < a.M * a.K; i += GEMV_THREADS) {
+                a.wts[i] = s_w[i];
+                if (a.ids_out) { a.ids_out[i] = s_ids[i]; a.w_out[i] = s_w[i]; }
+            }
+            int* P = a.plan;
+            if (tid == 0) P[0] = nu;
+            for (int i = tid; i < nu; i += GEMV_THREADS) {
+                P[1 + i] = pl.uexp[i];
+                P[1 + MAX_TOK * MAX_K + i] = pl.untok[i];
+                for (int n = 0; n < pl.untok[i]; n++) P[1 + 2 * MAX_TOK * MAX_K + i * MAX_TOK + n] = pl.upair[i][n];
+            }
+        }
+        if (u >= pl.nu) return;
+        ntok = pl.untok[u];
+        if (tid < ntok) { toks[tid] = pl.utok[u][tid]; pairs[tid] = pl.upair[u][tid]; }
     }
     if constexpr (TE == T_IQ3_S || TS == T_IQ3_S)
         for (int i = tid; i < 512; i += GEMV_THREADS) grid[i] = c_iq3s_grid_moe[i];
-
+    const int r0 = blockIdx.x * 8;
     float acc[MAX_TOK];
     if (shared) {
         const int64_t rb = row_bytes(TS, a.H);
@@ -294,7 +328,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_gate_up(MoeArgs a) {
                                a.H, a.xq, a.xq_stride, toks, ntok, acc);
     } else {
         const int64_t rb = row_bytes(TE, a.H);
-        const int64_t e = a.uexp[u];
+        const int64_t e = pl.uexp[u];
         tile_gemv<TE, MAX_TOK>(tile, CB, xs, grid, a.gate + e * a.sg + r0 * rb, 8,
                                a.up + e * a.su + r0 * rb, 8, rb, a.H, a.xq, a.xq_stride, toks, ntok, acc);
     }
@@ -307,52 +341,29 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_gate_up(MoeArgs a) {
     __syncthreads();
     if (tid < 8 * ntok) {
         const int i = tid & 7, t = tid >> 3;
-        const float hv = det_silu(res[i][t]) * res[8 + i][t];
-        a.h[(int64_t)pairs[t] * a.F + r0 + i] = hv;
+        a.h[(int64_t)pairs[t] * a.F + r0 + i] = det_silu(res[i][t]) * res[8 + i][t];
     }
-    __threadfence();
-    __syncthreads();
-    int* cnt = a.gu_cnt + (int64_t)u * (a.F / QK) + r0 / QK;
-    if (tid == 0) ticket = atomicAdd(cnt, 1);
-    __syncthreads();
-    if (ticket != QK / 8 - 1) return;
-    __threadfence();
-    // last of the 4 work-groups of this 32-row block: quantize h for each token
-    const int blk = r0 / QK;
-    if ((tid >> 5) < ntok) {
-        const int t = tid >> 5, i = tid & 31;
-        const float* hp = a.h + (int64_t)pairs[t] * a.F + blk * QK;
-        const float xi = __hip_atomic_load(hp + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        float amax = __builtin_fabsf(xi), sum = xi;
-#pragma unroll
-        for (int m = 16; m >= 1; m >>= 1) {
-            amax = __builtin_fmaxf(amax, __shfl_xor(amax, m, 32));
-            sum = sum + __shfl_xor(sum, m, 32);
-        }
-        const float d = amax / 127.0f;
-        const int q = amax == 0.0f ? 0 : (int)__builtin_roundf(xi / d);
-        uint8_t* o = a.hq + (int64_t)pairs[t] * a.hq_stride + blk * Q8_1_BYTES;
-        o[4 + i] = (uint8_t)(int8_t)q;
-        if (i == 0) *(uint32_t*)o = f2h(d) | (f2h(sum) << 16);
-    }
-    if (tid == 0) *cnt = 0;
 }
 
-// Down-projection rows of one expert tile (in LDS) for the given pairs; writes
-// dn[pair][row] for the 16 rows.  F <= 64 blocks (one chunk).
+// Down-projection rows of one expert tile (in LDS) for its pairs, with the
+// pairs' Q8_1 intermediates already decoded in LDS (xl[p][block]); writes
+// dn[pair][row] for the tile's rows.
 template <int T>
 __device__ __forceinline__ void down_tile(const uint8_t* tile, int lstride, const uint32_t* grid,
-                                          const uint8_t* hq, int64_t hq_stride, int F,
-                                          const int* pairs, int np, int nr, float (*dn)[TILE_ROWS]) {
+                                          const XLds* xl, int nbF, const int* pairs, int np, int nr,
+                                          float (*dn)[TILE_ROWS]) {
     const int tid = threadIdx.x, g = tid >> 4, j = tid & 15;
-    const int nb = F / QK;
     const uint8_t* row = tile + g * lstride;
     for (int p = 0; p < np; p++) {
         float acc = 0.0f;
         if (g < nr) {
-            for (int b = j; b < nb; b += SLOTS) {
+            for (int b = j; b < nbF; b += SLOTS) {
+                const XLds& xs = xl[p * nbF + b];
                 XBlk xb;
-                load_xblk(hq + (int64_t)pairs[p] * hq_stride + (int64_t)b * Q8_1_BYTES, xb);
+#pragma unroll
+                for (int k = 0; k < 8; k++) xb.q[k] = xs.q[k];
+                xb.d = xs.d;
+                xb.sumq = xs.sumq;
                 float dw;
                 const int s = block_dot<T>(row, b, xb, grid, &dw);
                 acc = __builtin_fmaf(dw * xb.d, (float)s, acc);
@@ -363,73 +374,98 @@ __device__ __forceinline__ void down_tile(const uint8_t* tile, int lstride, cons
     }
 }
 
-// K3: grid (ceil(H/16)).
+constexpr int DOWN_LDS = 48 * 1024;
+
+// K3: grid (ceil(H/16)).  Stages the down tiles of a batch of experts and the
+// Q8_1 re-quantization of their pairs' h (quantized here, ggml semantics)
+// together, computes, then combines in k order plus the shared expert.
 template <int TE, int TS>
 __global__ __launch_bounds__(GEMV_THREADS) void k_moe_down(MoeArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t tiles[DOWN_LDS_BUDGET + 16];
+    __shared__ __attribute__((aligned(16))) uint8_t buf[DOWN_LDS + 16];
     __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
     __shared__ float dn[MAX_TOK * MAX_K + MAX_TOK][TILE_ROWS];
     __shared__ int pl[MAX_TOK * MAX_K + 1][MAX_TOK];
     __shared__ int np[MAX_TOK * MAX_K + 1];
     __shared__ int wexp[MAX_TOK * MAX_K + 1];
+    __shared__ int boff[MAX_TOK * MAX_K + 1], xoff[MAX_TOK * MAX_K + 1];
 
     const int tid = threadIdx.x;
     const int r0 = blockIdx.x * TILE_ROWS;
     const int nr = min(TILE_ROWS, a.H - r0);
-    const int nu = *a.n_unique;
+    const int* P = a.plan;
+    const int nu = P[0];
     const int nw = nu + (a.has_shared ? 1 : 0);
+    const int nbF = a.F / QK;
     if constexpr (TE == T_IQ3_S || TS == T_IQ3_S)
         for (int i = tid; i < 512; i += GEMV_THREADS) grid[i] = c_iq3s_grid_moe[i];
     for (int w = tid; w < nw; w += GEMV_THREADS) {
         if (w < nu) {
-            wexp[w] = a.uexp[w];
-            np[w] = a.u_ntok[w];
-            for (int i = 0; i < np[w]; i++) pl[w][i] = a.u_pair[w * MAX_TOK + i];
+            wexp[w] = P[1 + w];
+            np[w] = P[1 + MAX_TOK * MAX_K + w];
+            for (int i = 0; i < np[w]; i++) pl[w][i] = P[1 + 2 * MAX_TOK * MAX_K + w * MAX_TOK + i];
         } else {
             wexp[w] = -1;
             np[w] = a.M;
             for (int i = 0; i < a.M; i++) pl[w][i] = a.M * a.K + i;
         }
     }
+    __syncthreads();
     const int64_t rbE = row_bytes(TE, a.F), rbS = row_bytes(TS, a.F);
     const int lsE = (int)((rbE + 15) & ~15), lsS = (int)((rbS + 15) & ~15);
     int w0 = 0;
     while (w0 < nw) {
-        // choose a batch of work experts whose tiles fit in LDS
+        // a batch of work experts whose tiles and decoded intermediates fit in LDS
         int w1 = w0, used = 0;
         while (w1 < nw) {
-            const int need = TILE_ROWS * ((w1 < nu) ? lsE : lsS);
-            if (used + need > DOWN_LDS_BUDGET && w1 > w0) break;
+            const int need = TILE_ROWS * ((w1 < nu) ? lsE : lsS) + np[w1] * nbF * (int)sizeof(XLds);
+            if (used + need > DOWN_LDS && w1 > w0) break;
             used += need;
             w1++;
         }
+        if (tid == 0) {
+            int o = 0;
+            for (int w = w0; w < w1; w++) { boff[w] = o; o += TILE_ROWS * ((w < nu) ? lsE : lsS); }
+            for (int w = w0; w < w1; w++) { xoff[w] = o; o += np[w] * nbF * (int)sizeof(XLds); }
+        }
         __syncthreads();
-        int off = 0;
         for (int w = w0; w < w1; w++) {
-            if (w < nu) {
-                stage_rows(tiles + off, lsE, a.down + (int64_t)wexp[w] * a.sd + (int64_t)r0 * rbE, rbE, nr,
+            if (w < nu)
+                stage_rows(buf + boff[w], lsE, a.down + (int64_t)wexp[w] * a.sd + (int64_t)r0 * rbE, rbE, nr,
                            (int)rbE, tid, GEMV_THREADS);
-                off += TILE_ROWS * lsE;
-            } else {
-                stage_rows(tiles + off, lsS, a.sh_down + (int64_t)r0 * rbS, rbS, nr, (int)rbS, tid,
+            else
+                stage_rows(buf + boff[w], lsS, a.sh_down + (int64_t)r0 * rbS, rbS, nr, (int)rbS, tid,
                            GEMV_THREADS);
-                off += TILE_ROWS * lsS;
-            }
+        }
+        for (int w = w0; w < w1; w++) {
+            XLds* xl = (XLds*)(buf + xoff[w]);
+            const int* pw = pl[w];
+            quantize_blocks(
+                np[w] * nbF,
+                [&](int b, int i) { return a.h[(int64_t)pw[b / nbF] * a.F + (b % nbF) * QK + i]; },
+                [&](int b, int i, int q, float d, float sum) {
+                    // pack the 32 quants of the block into 8 words through lane shuffles
+                    const int byte = (q & 0xFF) << (8 * (i & 3));
+                    int word = byte | __shfl_xor(byte, 1, 32);
+                    word = word | __shfl_xor(word, 2, 32);
+                    const int sq = q;
+                    int s = sq + __shfl_xor(sq, 1, 32);
+                    s = s + __shfl_xor(s, 2, 32);
+                    s = s + __shfl_xor(s, 4, 32);
+                    s = s + __shfl_xor(s, 8, 32);
+                    s = s + __shfl_xor(s, 16, 32);
+                    if ((i & 3) == 0) xl[b].q[i >> 2] = word;
+                    if (i == 0) { xl[b].d = h2f(f2h(d)); xl[b].sumq = s; }
+                });
         }
         __syncthreads();
-        off = 0;
         for (int w = w0; w < w1; w++) {
-            if (w < nu) {
-                down_tile<TE>(tiles + off, lsE, grid, a.hq, a.hq_stride, a.F, pl[w], np[w], nr, dn);
-                off += TILE_ROWS * lsE;
-            } else {
-                down_tile<TS>(tiles + off, lsS, grid, a.hq, a.hq_stride, a.F, pl[w], np[w], nr, dn);
-                off += TILE_ROWS * lsS;
-            }
+            const XLds* xl = (const XLds*)(buf + xoff[w]);
+            if (w < nu) down_tile<TE>(buf + boff[w], lsE, grid, xl, nbF, pl[w], np[w], nr, dn);
+            else down_tile<TS>(buf + boff[w], lsS, grid, xl, nbF, pl[w], np[w], nr, dn);
         }
+        __syncthreads();
         w0 = w1;
     }
-    __syncthreads();
     // combine: acc = sum_k fmaf(w_k, dn_k, acc); out = fmaf(shared, sigmoid(g), acc)
     if (tid < a.M * TILE_ROWS) {
         const int t = tid / TILE_ROWS, r = tid % TILE_ROWS;
@@ -454,8 +490,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_down(MoeArgs a) {
 // ------------------------------------------------------- workspace plan
 
 struct WsPlan {
-    size_t route_cnt, gu_cnt, logits, glogit, ids, wts, n_unique, uexp, u_ntok, u_pair, u_tok, xq, h, hq, total;
-    int64_t xq_stride, hq_stride;
+    size_t logits, glogit, wts, plan, xq, h, total;
+    int64_t xq_stride;
 };
 
 static size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -465,21 +501,12 @@ static WsPlan plan_ws(int H, int F, int E, int K, int M) {
     size_t o = 0;
     const int P = M * K + M;
     p.xq_stride = pad_to(H, ROW_PAD) / QK * Q8_1_BYTES;
-    p.hq_stride = pad_to(F, ROW_PAD) / QK * Q8_1_BYTES;
-    p.route_cnt = o; o += al256(4);
-    p.gu_cnt = o; o += al256((size_t)(M * K + 1) * (F / QK) * 4);
     p.logits = o; o += al256((size_t)M * E * 4);
     p.glogit = o; o += al256((size_t)M * 4);
-    p.ids = o; o += al256((size_t)M * K * 4);
     p.wts = o; o += al256((size_t)M * K * 4);
-    p.n_unique = o; o += al256(4);
-    p.uexp = o; o += al256((size_t)M * K * 4);
-    p.u_ntok = o; o += al256((size_t)M * K * 4);
-    p.u_pair = o; o += al256((size_t)M * K * MAX_TOK * 4);
-    p.u_tok = o; o += al256((size_t)M * K * MAX_TOK * 4);
+    p.plan = o; o += al256((size_t)(1 + 2 * MAX_TOK * MAX_K + MAX_TOK * MAX_K * MAX_TOK) * 4);
     p.xq = o; o += al256((size_t)M * p.xq_stride);
     p.h = o; o += al256((size_t)P * F * 4);
-    p.hq = o; o += al256((size_t)P * p.hq_stride);
     p.total = o;
     return p;
 }
@@ -488,7 +515,7 @@ static WsPlan plan_ws(int H, int F, int E, int K, int M) {
 template <int TE, int TS>
 static void launch_layer(const MoeArgs& a, int stage, hipStream_t s) {
     if (stage < 0 || stage == 0)
-        hipLaunchKernelGGL(k_moe_route, dim3(a.E + (a.sh_gate_w ? 1 : 0)), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(k_moe_route, dim3(a.E + (a.sh_gate_w ? 1 : 0) + a.M), dim3(256), 0, s, a);
     if (stage < 0 || stage == 1)
         hipLaunchKernelGGL((k_moe_gate_up<TE, TS>), dim3(a.F / 8, a.M * a.K + 1), dim3(GEMV_THREADS), 0, s, a);
     if (stage < 0 || stage == 2)
@@ -527,15 +554,9 @@ __global__ __launch_bounds__(256) void k_f32_gemv(const float* A, const float* x
     if (threadIdx.x == 0) y[blockIdx.x] = v[0];
 }
 
-__global__ __launch_bounds__(256) void k_topk(const float* logits, int* idx, float* w, int E, int K) {
-    __shared__ float red[256];
-    __shared__ int redi[4];
-    __shared__ float lp[MAX_E], lev[MAX_E];
-    __shared__ int sidx[MAX_K * 64];
-    __shared__ float sw[MAX_K * 64];
+__global__ __launch_bounds__(64) void k_topk(const float* logits, int* idx, float* w, int E, int K) {
     const int t = blockIdx.x;
-    topk_group(logits + (int64_t)t * E, E, K, sidx, sw, lp, lev, red, redi);
-    for (int k = threadIdx.x; k < K; k += 256) { idx[t * K + k] = sidx[k]; w[t * K + k] = sw[k]; }
+    topk_wave_any(logits + (int64_t)t * E, E, K, idx + t * K, w + t * K);
 }
 
 __global__ void k_silu_mul(float* g, const float* u, int n) {
@@ -614,13 +635,10 @@ static void moe_decode(const chimere_moe_layer* L, const float* x, float* out, i
     a.sh_gate = (const uint8_t*)L->sh_gate; a.sh_up = (const uint8_t*)L->sh_up; a.sh_down = (const uint8_t*)L->sh_down;
     a.sh_gate_w = has_sh ? L->sh_gate_w : nullptr;
     a.ids_out = ids_out; a.w_out = w_out;
-    a.route_cnt = (int*)(w + p.route_cnt); a.gu_cnt = (int*)(w + p.gu_cnt);
     a.logits = (float*)(w + p.logits); a.glogit = (float*)(w + p.glogit);
-    a.ids = (int*)(w + p.ids); a.wts = (float*)(w + p.wts);
-    a.n_unique = (int*)(w + p.n_unique); a.uexp = (int*)(w + p.uexp); a.u_ntok = (int*)(w + p.u_ntok);
-    a.u_pair = (int*)(w + p.u_pair); a.u_tok = (int*)(w + p.u_tok);
-    a.xq = w + p.xq; a.h = (float*)(w + p.h); a.hq = w + p.hq;
-    a.xq_stride = p.xq_stride; a.hq_stride = p.hq_stride;
+    a.wts = (float*)(w + p.wts); a.plan = (int*)(w + p.plan);
+    a.xq = w + p.xq; a.h = (float*)(w + p.h);
+    a.xq_stride = p.xq_stride;
     dispatch_layer(L->expert_type, L->shared_type, a, stage, stream);
     check_launch("moe_ffn_decode");
 }
@@ -645,9 +663,9 @@ void chimere_f32_gemv(const float* A, const float* x, float* y, int rows, int co
 
 void chimere_topk_softmax(const float* logits, int* idx, float* w, int E, int K, int ntok, hipStream_t s) {
     CHIMERE_REQUIRE(logits && idx && w, CHIMERE_ERR_ARG, "topk_softmax: null pointer");
-    CHIMERE_REQUIRE(E >= 1 && E <= MAX_E && K >= 1 && K <= E && K <= MAX_K * 64 && ntok >= 1, CHIMERE_ERR_ARG,
+    CHIMERE_REQUIRE(E >= 1 && E <= MAX_E && K >= 1 && K <= E && K <= MAX_K && ntok >= 1, CHIMERE_ERR_ARG,
                     "topk_softmax: n_experts=%d top_k=%d ntok=%d out of range", E, K, ntok);
-    hipLaunchKernelGGL(k_topk, dim3(ntok), dim3(256), 0, s, logits, idx, w, E, K);
+    hipLaunchKernelGGL(k_topk, dim3(ntok), dim3(64), 0, s, logits, idx, w, E, K);
     check_launch("topk_softmax");
 }
 
