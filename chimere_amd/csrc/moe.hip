@@ -85,10 +85,15 @@ __device__ __forceinline__ void f32_row_dot(const float* __restrict__ a, const f
 // l, l+64, ... (NV = ceil(E/64) values, zero-padded).  p = exp(l - max) / sum
 // where the sum follows the reference's strided halving tree (strides
 // 512..64 pair values inside a lane, strides 32..1 pair lanes; padding adds
-// +0, which leaves the non-negative partial sums unchanged); k rounds of
-// arg-max by probability, ties to the lowest index; weights renormalised by
-// the sequential sum of the selected probabilities.  Every lane ends with
-// the same idx[]/w[]; lane k < K writes entry k.
+// +0, which leaves the non-negative partial sums unchanged).
+// Selection: the reference takes k rounds of arg-max by probability with ties
+// to the lowest index, i.e. the K largest keys (p, -index).  Here the K-th
+// largest key is found by a radix select over 41-bit keys
+// (f32 bits of p << 11 | 1024 - index) with ballot counts, then each selected
+// entry's rank is the number of larger keys -- same set, same order, no
+// cross-lane shuffles in the loop.  Weights are renormalised by the
+// sequential sum of the selected probabilities (rank order).  Lane k < K
+// writes entry k.  Requires E <= 1024, K <= E.
 template <int NV>
 __device__ __forceinline__ void topk_wave(const float* __restrict__ logits, int E, int K,
                                           int* __restrict__ idx_out, float* __restrict__ w_out) {
@@ -116,43 +121,47 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ logits, int 
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) s = s + __shfl_xor(s, m);
     // s equals lane 0's value of the halving tree on every lane
+    uint64_t key[NV];
 #pragma unroll
-    for (int i = 0; i < NV; i++)
-        p[i] = (lane + 64 * i) < E ? (s > 0.0f ? ev[i] / s : 1.0f / (float)E) : -2.0f;
-    int idx[MAX_K];
-    float w[MAX_K];
+    for (int i = 0; i < NV; i++) {
+        const int j = lane + 64 * i;
+        p[i] = s > 0.0f ? ev[i] / s : 1.0f / (float)E;
+        key[i] = j < E ? (((uint64_t)__builtin_bit_cast(uint32_t, p[i])) << 11) | (uint64_t)(1024 - j) : 0;
+    }
+    // radix select of the K-th largest key (p <= 1, so the f32 bits fit in 30 bits)
+    uint64_t T = 0;
+    for (int b = 40; b >= 0; b--) {
+        const uint64_t cand = T | (1ull << b);
+        int cnt = 0;
 #pragma unroll
-    for (int k = 0; k < MAX_K; k++) {
-        if (k < K) {
-            float bv = -3.0f;
-            int bi = 0x7fffffff;
+        for (int i = 0; i < NV; i++) cnt += __popcll(__ballot(key[i] >= cand));
+        if (cnt >= K) T = cand;
+    }
+    // rank each selected entry: rank = number of keys larger than it
+    int my_idx = 0;
+    float my_w = 0.0f;
 #pragma unroll
-            for (int i = 0; i < NV; i++)
-                if (p[i] > bv) { bv = p[i]; bi = lane + 64 * i; }
+    for (int i = 0; i < NV; i++) {
+        uint64_t m = __ballot(key[i] >= T);
+        while (m) {
+            const int src = __builtin_ctzll(m);
+            m &= m - 1;
+            const uint32_t klo = __builtin_amdgcn_readlane((uint32_t)key[i], src);
+            const uint32_t khi = __builtin_amdgcn_readlane((uint32_t)(key[i] >> 32), src);
+            const uint64_t kx = ((uint64_t)khi << 32) | klo;
+            const float px = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p[i]), src));
+            int r = 0;
 #pragma unroll
-            for (int m = 32; m >= 1; m >>= 1) {
-                const float ov = __shfl_xor(bv, m);
-                const int oi = __shfl_xor(bi, m);
-                if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-            }
-            idx[k] = bi;
-            w[k] = bv;
-#pragma unroll
-            for (int i = 0; i < NV; i++)
-                if (lane + 64 * i == bi) p[i] = -1.0f;
+            for (int i2 = 0; i2 < NV; i2++) r += __popcll(__ballot(key[i2] > kx));
+            if (lane == r) { my_idx = src + 64 * i; my_w = px; }
         }
     }
     float ws = 0.0f;
-#pragma unroll
-    for (int k = 0; k < MAX_K; k++)
-        if (k < K) ws += w[k];
-    const float inv = ws > 0.0f ? 1.0f / ws : 1.0f;
-#pragma unroll
-    for (int k = 0; k < MAX_K; k++) {
-        if (k < K && lane == k) {
-            idx_out[k] = idx[k];
-            w_out[k] = ws > 0.0f ? w[k] * inv : w[k];
-        }
+    for (int k = 0; k < K; k++)
+        ws += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_w), k));
+    if (lane < K) {
+        idx_out[lane] = my_idx;
+        w_out[lane] = ws > 0.0f ? my_w * (1.0f / ws) : my_w;
     }
 }
 
@@ -374,7 +383,7 @@ __device__ __forceinline__ void down_tile(const uint8_t* tile, int lstride, cons
     }
 }
 
-constexpr int DOWN_LDS = 48 * 1024;
+constexpr int DOWN_LDS = 96 * 1024;
 
 // K3: grid (ceil(H/16)).  Stages the down tiles of a batch of experts and the
 // Q8_1 re-quantization of their pairs' h (quantized here, ggml semantics)
@@ -417,15 +426,17 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_down(MoeArgs a) {
         // a batch of work experts whose tiles and decoded intermediates fit in LDS
         int w1 = w0, used = 0;
         while (w1 < nw) {
-            const int need = TILE_ROWS * ((w1 < nu) ? lsE : lsS) + np[w1] * nbF * (int)sizeof(XLds);
+            const int need = TILE_ROWS * ((w1 < nu) ? lsE : lsS) + np[w1] * nbF * (int)sizeof(XLds) + np[w1] * a.F * 4;
             if (used + need > DOWN_LDS && w1 > w0) break;
             used += need;
             w1++;
         }
-        if (tid == 0) {
+        int hoff = 0;
+        {
             int o = 0;
-            for (int w = w0; w < w1; w++) { boff[w] = o; o += TILE_ROWS * ((w < nu) ? lsE : lsS); }
-            for (int w = w0; w < w1; w++) { xoff[w] = o; o += np[w] * nbF * (int)sizeof(XLds); }
+            for (int w = w0; w < w1; w++) { if (tid == 0) boff[w] = o; o += TILE_ROWS * ((w < nu) ? lsE : lsS); }
+            for (int w = w0; w < w1; w++) { if (tid == 0) xoff[w] = o; o += np[w] * nbF * (int)sizeof(XLds); }
+            hoff = o;
         }
         __syncthreads();
         for (int w = w0; w < w1; w++) {
@@ -436,12 +447,25 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_down(MoeArgs a) {
                 stage_rows(buf + boff[w], lsS, a.sh_down + (int64_t)r0 * rbS, rbS, nr, (int)rbS, tid,
                            GEMV_THREADS);
         }
+        // h of every pair in the batch: all loads issued before any is used
+        {
+            float* hs = (float*)(buf + hoff);
+            int o = 0;
+            for (int w = w0; w < w1; w++)
+                for (int pi = 0; pi < np[w]; pi++, o++) {
+                    const float4* src = (const float4*)(a.h + (int64_t)pl[w][pi] * a.F);
+                    for (int c = tid; c < a.F / 4; c += GEMV_THREADS) ((float4*)(hs + o * a.F))[c] = src[c];
+                }
+        }
+        __syncthreads();
+        int hbase = 0;
         for (int w = w0; w < w1; w++) {
             XLds* xl = (XLds*)(buf + xoff[w]);
-            const int* pw = pl[w];
+            const float* hw = (const float*)(buf + hoff) + hbase * a.F;
+            hbase += np[w];
             quantize_blocks(
                 np[w] * nbF,
-                [&](int b, int i) { return a.h[(int64_t)pw[b / nbF] * a.F + (b % nbF) * QK + i]; },
+                [&](int b, int i) { return hw[(b / nbF) * a.F + (b % nbF) * QK + i]; },
                 [&](int b, int i, int q, float d, float sum) {
                     // pack the 32 quants of the block into 8 words through lane shuffles
                     const int byte = (q & 0xFF) << (8 * (i & 3));
