@@ -190,14 +190,57 @@ __device__ __forceinline__ void stage_rows(uint8_t* __restrict__ lds, int lstrid
     }
 }
 
+// Value of lane (lane ^ M) without going through LDS: DPP quad permutes for
+// M = 1, 2, row shifts by M (direction picked per lane) for M = 4, 8, and the
+// gfx950 v_permlane16/32_swap for M = 16, 32.  The partner lane must be
+// active (all uses keep whole 2M-lane groups converged).
+template <int M>
+__device__ __forceinline__ int xlane(int v) {
+    static_assert(M == 1 || M == 2 || M == 4 || M == 8 || M == 16 || M == 32, "xor mask");
+    const int lane = __lane_id();
+    if constexpr (M == 1) return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);   // quad_perm 1,0,3,2
+    else if constexpr (M == 2) return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false); // quad_perm 2,3,0,1
+    else if constexpr (M == 4 || M == 8) {
+        const int up = __builtin_amdgcn_update_dpp(0, v, 0x100 | M, 0xF, 0xF, false);   // row_shl: lane i+M
+        const int dn = __builtin_amdgcn_update_dpp(0, v, 0x110 | M, 0xF, 0xF, false);   // row_shr: lane i-M
+        return (lane & M) ? dn : up;
+    } else if constexpr (M == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+        return (int)((lane & 16) ? r[0] : r[1]);
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+        return (int)((lane & 32) ? r[0] : r[1]);
+    }
+}
+template <int M>
+__device__ __forceinline__ float xlane(float v) {
+    return __builtin_bit_cast(float, xlane<M>(__builtin_bit_cast(int, v)));
+}
+
 // Sum over the 16 lanes of a row group in the halving-tree order
 // (xor 8, 4, 2, 1); every lane of the group ends with the same value.
 __device__ __forceinline__ float slot_reduce16(float v) {
-    v = v + __shfl_xor(v, 8, 16);
-    v = v + __shfl_xor(v, 4, 16);
-    v = v + __shfl_xor(v, 2, 16);
-    v = v + __shfl_xor(v, 1, 16);
+    v = v + xlane<8>(v);
+    v = v + xlane<4>(v);
+    v = v + xlane<2>(v);
+    v = v + xlane<1>(v);
     return v;
+}
+
+// 32-lane xor butterflies (masks 16, 8, 4, 2, 1): max and sum
+__device__ __forceinline__ float bfly32_max(float v) {
+    v = __builtin_fmaxf(v, xlane<16>(v));
+    v = __builtin_fmaxf(v, xlane<8>(v));
+    v = __builtin_fmaxf(v, xlane<4>(v));
+    v = __builtin_fmaxf(v, xlane<2>(v));
+    return __builtin_fmaxf(v, xlane<1>(v));
+}
+__device__ __forceinline__ float bfly32_sum(float v) {
+    v = v + xlane<16>(v);
+    v = v + xlane<8>(v);
+    v = v + xlane<4>(v);
+    v = v + xlane<2>(v);
+    return v + xlane<1>(v);
 }
 
 }  // namespace chimere

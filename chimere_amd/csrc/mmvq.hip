@@ -58,8 +58,10 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_mmvq(MmvqArgs a) {
     if (g < nr) {
 #pragma unroll
         for (int t = 0; t < NTOK; t++) {
-            float v = slot_reduce16(acc[t]);
-            if (j == 0 && t < a.ntok) a.y[slot * a.y_slot_stride + t * a.y_tok_stride + r0 + g] = v;
+            if (t < a.ntok) {
+                const float v = slot_reduce16(acc[t]);
+                if (j == 0) a.y[slot * a.y_slot_stride + t * a.y_tok_stride + r0 + g] = v;
+            }
         }
     }
 }

@@ -46,13 +46,8 @@ __device__ __forceinline__ float tree_sum256(float v, float* red) {
     __syncthreads();
     if (tid < 64) {
         float w = red[tid] + red[tid + 64];
-        w = w + __shfl_xor(w, 32);
-        w = w + __shfl_xor(w, 16);
-        w = w + __shfl_xor(w, 8);
-        w = w + __shfl_xor(w, 4);
-        w = w + __shfl_xor(w, 2);
-        w = w + __shfl_xor(w, 1);
-        v = w;
+        w = w + xlane<32>(w);
+        v = bfly32_sum(w);
     }
     __syncthreads();
     return v;
@@ -106,8 +101,7 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ logits, int 
         p[i] = j < E ? logits[j] : -__builtin_huge_valf();
         mx = __builtin_fmaxf(mx, p[i]);
     }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, m));
+    mx = bfly32_max(__builtin_fmaxf(mx, xlane<32>(mx)));
 #pragma unroll
     for (int i = 0; i < NV; i++) {
         ev[i] = (lane + 64 * i) < E ? det_exp(p[i] - mx) : 0.0f;
@@ -118,8 +112,7 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ logits, int 
 #pragma unroll
         for (int i = 0; i < h; i++) p[i] = p[i] + p[i + h];
     float s = p[0];
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) s = s + __shfl_xor(s, m);
+    s = bfly32_sum(s + xlane<32>(s));
     // s equals lane 0's value of the halving tree on every lane
     uint64_t key[NV];
 #pragma unroll
@@ -182,12 +175,7 @@ __device__ __forceinline__ void quantize_blocks(int nblk, Src src, Emit emit) {
     for (int b = threadIdx.x >> 5; b < nblk; b += GEMV_THREADS / 32) {
         const int i = threadIdx.x & 31;
         const float xi = src(b, i);
-        float amax = __builtin_fabsf(xi), sum = xi;
-#pragma unroll
-        for (int m = 16; m >= 1; m >>= 1) {
-            amax = __builtin_fmaxf(amax, __shfl_xor(amax, m, 32));
-            sum = sum + __shfl_xor(sum, m, 32);
-        }
+        const float amax = bfly32_max(__builtin_fabsf(xi)), sum = bfly32_sum(xi);
         const float d = amax / 127.0f;
         const int q = amax == 0.0f ? 0 : (int)__builtin_roundf(xi / d);
         emit(b, i, q, d, sum);
@@ -344,8 +332,10 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_gate_up(MoeArgs a) {
     const int g = tid >> 4, j = tid & 15;
 #pragma unroll
     for (int t = 0; t < MAX_TOK; t++) {
-        const float v = slot_reduce16(acc[t]);
-        if (j == 0 && t < ntok) res[g][t] = v;
+        if (t < ntok) {
+            const float v = slot_reduce16(acc[t]);
+            if (j == 0) res[g][t] = v;
+        }
     }
     __syncthreads();
     if (tid < 8 * ntok) {
@@ -469,14 +459,13 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_down(MoeArgs a) {
                 [&](int b, int i, int q, float d, float sum) {
                     // pack the 32 quants of the block into 8 words through lane shuffles
                     const int byte = (q & 0xFF) << (8 * (i & 3));
-                    int word = byte | __shfl_xor(byte, 1, 32);
-                    word = word | __shfl_xor(word, 2, 32);
-                    const int sq = q;
-                    int s = sq + __shfl_xor(sq, 1, 32);
-                    s = s + __shfl_xor(s, 2, 32);
-                    s = s + __shfl_xor(s, 4, 32);
-                    s = s + __shfl_xor(s, 8, 32);
-                    s = s + __shfl_xor(s, 16, 32);
+                    int word = byte | xlane<1>(byte);
+                    word = word | xlane<2>(word);
+                    int s = q + xlane<16>(q);
+                    s = s + xlane<8>(s);
+                    s = s + xlane<4>(s);
+                    s = s + xlane<2>(s);
+                    s = s + xlane<1>(s);
                     if ((i & 3) == 0) xl[b].q[i >> 2] = word;
                     if (i == 0) { xl[b].d = h2f(f2h(d)); xl[b].sumq = s; }
                 });

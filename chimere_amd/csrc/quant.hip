@@ -19,12 +19,7 @@ __global__ __launch_bounds__(256) void k_quantize_q8_1(const float* __restrict__
     if (b >= nb) return;   // whole half-wave exits together
     const int64_t col = b * QK + i;
     float xi = col < ncols ? x[row * ncols + col] : 0.0f;
-    float amax = __builtin_fabsf(xi), sum = xi;
-#pragma unroll
-    for (int m = 16; m >= 1; m >>= 1) {
-        amax = __builtin_fmaxf(amax, __shfl_xor(amax, m, 32));
-        sum = sum + __shfl_xor(sum, m, 32);
-    }
+    const float amax = bfly32_max(__builtin_fabsf(xi)), sum = bfly32_sum(xi);
     const float d = amax / 127.0f;
     const int q = amax == 0.0f ? 0 : (int)__builtin_roundf(xi / d);
     uint8_t* blk = out + (row * nb + b) * Q8_1_BYTES;
