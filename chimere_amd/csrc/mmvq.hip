@@ -2,13 +2,8 @@
 // activations) for 1..8 tokens, plain / batched-by-expert-id / debug dots.
 //
 // Work-group = 256 threads = 16 row groups of 16 lanes; one tile = 16
-// consecutive rows.  A row is consumed in chunks of 64 blocks: the 16 row
-// segments of a chunk are streamed HBM -> LDS with 16-byte loads, the
-// chunk's Q8_1 activation blocks are decoded once into LDS, then lane j of a
-// row group takes blocks j, j+16, j+32, ... of the chunk.  fp32 order
-// (L=16, G=1): per lane acc = fmaf(f32(d_w)*f32(d_x), (float)sumi, acc) over
-// its blocks in ascending order, then the 16 lanes are summed with the
-// halving tree xor 8,4,2,1.  sumi is the exact int32 block dot.
+// consecutive rows, streamed through LDS by tile_gemv (which documents the
+// fp32 order: L=16 lanes per row, G=1).
 #include "api_internal.h"
 #include "common.h"
 #include "tile_gemv.h"
@@ -38,7 +33,7 @@ template <int T, int NTOK>
 __global__ __launch_bounds__(GEMV_THREADS) void k_mmvq(MmvqArgs a) {
     constexpr int CB = ChunkGeom<T>::BYTES;
     __shared__ __attribute__((aligned(16))) uint8_t tile[TILE_ROWS * CB + 16];
-    __shared__ XLds xs[NTOK][CHUNK_BLOCKS];
+    __shared__ XLds xs[NTOK][MAX_CHUNK_BLOCKS];
     __shared__ uint32_t grid[T == T_IQ3_S ? 512 : 1];
 
     const int tid = threadIdx.x;
@@ -51,15 +46,15 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_mmvq(MmvqArgs a) {
     if constexpr (T == T_IQ3_S)
         for (int i = tid; i < 512; i += GEMV_THREADS) grid[i] = c_iq3s_grid_mmvq[i];
 
-    float acc[NTOK];
-    tile_gemv<T, NTOK>(tile, CB, xs, grid, a.W + e * a.w_slot_stride + (int64_t)r0 * rb, nr,
-                       nullptr, 0, rb, a.ncols, a.x + slot * a.x_slot_stride, a.x_tok_stride,
-                       nullptr, a.ntok, acc);
+    float acc[1][NTOK];
+    tile_gemv<T, NTOK, TILE_ROWS, 1>(tile, xs, grid, a.W + e * a.w_slot_stride + (int64_t)r0 * rb, nr,
+                                     nullptr, 0, rb, a.ncols, a.x + slot * a.x_slot_stride, a.x_tok_stride,
+                                     nullptr, a.ntok, acc);
     if (g < nr) {
 #pragma unroll
         for (int t = 0; t < NTOK; t++) {
             if (t < a.ntok) {
-                const float v = slot_reduce16(acc[t]);
+                const float v = slot_reduce16(acc[0][t]);
                 if (j == 0) a.y[slot * a.y_slot_stride + t * a.y_tok_stride + r0 + g] = v;
             }
         }

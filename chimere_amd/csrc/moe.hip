@@ -9,16 +9,16 @@
 //   K1 k_moe_route    one work-group per router row (+1 for the shared-expert
 //                     gate vector) computing f32 logits for every token, plus
 //                     one work-group per token quantizing x to Q8_1.
-//   K2 k_moe_gate_up  (8-row chunk of F) x (distinct expert | shared).  Each
+//   K2 k_moe_gate_up  (32-row block of F) x (distinct expert | shared).  Each
 //                     routed work-group recomputes softmax/top-k (one wave per
 //                     token, registers only) and the distinct-expert plan from
-//                     the 1 KB of logits, then streams 8 gate + 8 up rows of
+//                     the 1 KB of logits, then streams 32 gate + 32 up rows of
 //                     its expert once for all tokens routed to it and writes
-//                     h = silu(gate)*up in f32.
+//                     the block of h = silu(gate)*up Q8_1-quantized.
 //   K3 k_moe_down     16 hidden rows per work-group over all selected experts
-//                     (tiles of several experts staged together with the Q8_1
-//                     re-quantization of their h), then the router-weighted
-//                     sum in k order plus the shared expert.
+//                     (tiles of several experts staged together with their
+//                     Q8_1 intermediates), then the router-weighted sum in k
+//                     order plus the shared expert.
 // Every row dot uses the (L=16, G=1) order of tile_gemv.h.
 #include "api_internal.h"
 #include "common.h"
@@ -201,11 +201,14 @@ struct MoeArgs {
     float* logits;      // [M*E]
     float* glogit;      // [M]
     float* wts;         // [M*K]
-    int* plan;          // n_unique, uexp[M*K], u_ntok[M*K], u_pair[M*K][MAX_TOK]
-    uint8_t* xq;        // [M][xq_stride]
-    float* h;           // [M*K + M][F]
-    int64_t xq_stride;
+    int* plan;          // n_unique, uexp[128], u_ntok[128], u_pair[128][MAX_TOK]
+    uint8_t* xq;        // [M][xq_stride]   Q8_1(x)
+    uint8_t* hq;        // [M*K + M][hq_stride]   Q8_1(h) per (token, k) pair and shared
+    int64_t xq_stride, hq_stride;
 };
+
+constexpr int PLAN_UEXP = 1, PLAN_UNTOK = 1 + MAX_TOK * MAX_K, PLAN_UPAIR = 1 + 2 * MAX_TOK * MAX_K;
+constexpr int PLAN_INTS = PLAN_UPAIR + MAX_TOK * MAX_K * MAX_TOK;
 
 // Expert plan: distinct selected experts and, per expert, its (token, k) pairs.
 struct Plan {
@@ -246,23 +249,27 @@ __global__ __launch_bounds__(256) void k_moe_route(MoeArgs a) {
     }
 }
 
-// K2: grid (F/8, M*K + 1).  Every routed work-group recomputes the routing
-// (top-k per token, one wave each) and the distinct-expert plan from the
-// logits, so no work-group waits on another; blockIdx.y < n_unique selects a
-// distinct expert, blockIdx.y == M*K the shared expert.  Work-group (0,0)
-// publishes routing and plan for K3.  8 gate rows + 8 up rows per tile;
-// h = silu(gate) * up is written in f32.
+constexpr int GU_RG = 32;                  // K2 row groups: 512 threads
+constexpr int GU_THREADS = GU_RG * SLOTS;
+
+// K2: grid (F/32, M*K + 1), 512 threads.  Every routed work-group recomputes
+// the routing (top-k per token, one wave each) and the distinct-expert plan
+// from the logits, so no work-group waits on another; blockIdx.y < n_unique
+// selects a distinct expert, blockIdx.y == M*K the shared expert.  Work-group
+// (0,0) publishes routing and plan for K3.  A tile holds 32 gate + 32 up rows
+// (group g computes gate row g and up row g), so the work-group owns whole
+// 32-row blocks of h = silu(gate) * up and writes them Q8_1-quantized.
 template <int TE, int TS>
-__global__ __launch_bounds__(GEMV_THREADS) void k_moe_gate_up(MoeArgs a) {
+__global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
     constexpr int CBE = ChunkGeom<TE>::BYTES, CBS = ChunkGeom<TS>::BYTES;
     constexpr int CB = CBE > CBS ? CBE : CBS;
     // the tile buffer first holds the expert map and the plan (routing phase)
     constexpr int ROUTE_BYTES = MAX_E * 4 + (int)sizeof(Plan);
-    constexpr int TILE_BYTES = TILE_ROWS * CB + 16 > ROUTE_BYTES ? TILE_ROWS * CB + 16 : ROUTE_BYTES;
+    constexpr int TILE_BYTES = 2 * GU_RG * CB + 16 > ROUTE_BYTES ? 2 * GU_RG * CB + 16 : ROUTE_BYTES;
     __shared__ __attribute__((aligned(16))) uint8_t tile[TILE_BYTES];
-    __shared__ XLds xs[MAX_TOK][CHUNK_BLOCKS];
+    __shared__ XLds xs[MAX_TOK][MAX_CHUNK_BLOCKS];
     __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
-    __shared__ float res[TILE_ROWS][MAX_TOK];
+    __shared__ float hres[MAX_TOK][QK];
     __shared__ int toks[MAX_TOK], pairs[MAX_TOK];
     __shared__ int s_ids[MAX_TOK * MAX_K];
     __shared__ float s_w[MAX_TOK * MAX_K];
@@ -278,10 +285,10 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_gate_up(MoeArgs a) {
         if (tid < a.M) { toks[tid] = tid; pairs[tid] = a.M * a.K + tid; }
     } else {
         const int wave = tid >> 6;
-        for (int t = wave; t < a.M; t += GEMV_THREADS / 64)
+        for (int t = wave; t < a.M; t += GU_THREADS / 64)
             topk_wave_any(a.logits + t * a.E, a.E, a.K, s_ids + t * a.K, s_w + t * a.K);
         int* map = (int*)tile;
-        for (int e = tid; e < a.E; e += GEMV_THREADS) map[e] = -1;
+        for (int e = tid; e < a.E; e += GU_THREADS) map[e] = -1;
         __syncthreads();
         if (tid == 0) {
             int nu = 0;
@@ -299,16 +306,16 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_gate_up(MoeArgs a) {
         __syncthreads();
         if (blockIdx.x == 0 && u == 0) {
             const int nu = pl.nu;
-            for (int i = tid; i < a.M * a.K; i += GEMV_THREADS) {
+            for (int i = tid; i < a.M * a.K; i += GU_THREADS) {
                 a.wts[i] = s_w[i];
                 if (a.ids_out) { a.ids_out[i] = s_ids[i]; a.w_out[i] = s_w[i]; }
             }
             int* P = a.plan;
             if (tid == 0) P[0] = nu;
-            for (int i = tid; i < nu; i += GEMV_THREADS) {
-                P[1 + i] = pl.uexp[i];
-                P[1 + MAX_TOK * MAX_K + i] = pl.untok[i];
-                for (int n = 0; n < pl.untok[i]; n++) P[1 + 2 * MAX_TOK * MAX_K + i * MAX_TOK + n] = pl.upair[i][n];
+            for (int i = tid; i < nu; i += GU_THREADS) {
+                P[PLAN_UEXP + i] = pl.uexp[i];
+                P[PLAN_UNTOK + i] = pl.untok[i];
+                for (int n = 0; n < pl.untok[i]; n++) P[PLAN_UPAIR + i * MAX_TOK + n] = pl.upair[i][n];
             }
         }
         if (u >= pl.nu) return;
@@ -316,36 +323,45 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_gate_up(MoeArgs a) {
         if (tid < ntok) { toks[tid] = pl.utok[u][tid]; pairs[tid] = pl.upair[u][tid]; }
     }
     if constexpr (TE == T_IQ3_S || TS == T_IQ3_S)
-        for (int i = tid; i < 512; i += GEMV_THREADS) grid[i] = c_iq3s_grid_moe[i];
-    const int r0 = blockIdx.x * 8;
-    float acc[MAX_TOK];
+        for (int i = tid; i < 512; i += GU_THREADS) grid[i] = c_iq3s_grid_moe[i];
+    const int r0 = blockIdx.x * QK;
+    float acc[2][MAX_TOK];
     if (shared) {
         const int64_t rb = row_bytes(TS, a.H);
-        tile_gemv<TS, MAX_TOK>(tile, CB, xs, grid, a.sh_gate + r0 * rb, 8, a.sh_up + r0 * rb, 8, rb,
-                               a.H, a.xq, a.xq_stride, toks, ntok, acc);
+        tile_gemv<TS, MAX_TOK, GU_RG, 2>(tile, xs, grid, a.sh_gate + r0 * rb, QK, a.sh_up + r0 * rb, QK, rb,
+                                         a.H, a.xq, a.xq_stride, toks, ntok, acc);
     } else {
         const int64_t rb = row_bytes(TE, a.H);
         const int64_t e = pl.uexp[u];
-        tile_gemv<TE, MAX_TOK>(tile, CB, xs, grid, a.gate + e * a.sg + r0 * rb, 8,
-                               a.up + e * a.su + r0 * rb, 8, rb, a.H, a.xq, a.xq_stride, toks, ntok, acc);
+        tile_gemv<TE, MAX_TOK, GU_RG, 2>(tile, xs, grid, a.gate + e * a.sg + r0 * rb, QK,
+                                         a.up + e * a.su + r0 * rb, QK, rb, a.H, a.xq, a.xq_stride, toks,
+                                         ntok, acc);
     }
     const int g = tid >> 4, j = tid & 15;
 #pragma unroll
     for (int t = 0; t < MAX_TOK; t++) {
         if (t < ntok) {
-            const float v = slot_reduce16(acc[t]);
-            if (j == 0) res[g][t] = v;
+            const float gv = slot_reduce16(acc[0][t]);
+            const float uv = slot_reduce16(acc[1][t]);
+            if (j == 0) hres[t][g] = det_silu(gv) * uv;
         }
     }
     __syncthreads();
-    if (tid < 8 * ntok) {
-        const int i = tid & 7, t = tid >> 3;
-        a.h[(int64_t)pairs[t] * a.F + r0 + i] = det_silu(res[i][t]) * res[8 + i][t];
+    // one half-wave per token quantizes the 32-row block of h (ggml Q8_1)
+    if ((tid >> 5) < ntok) {
+        const int t = tid >> 5, i = tid & 31;
+        const float xi = hres[t][i];
+        const float amax = bfly32_max(__builtin_fabsf(xi)), sum = bfly32_sum(xi);
+        const float d = amax / 127.0f;
+        const int q = amax == 0.0f ? 0 : (int)__builtin_roundf(xi / d);
+        uint8_t* o = a.hq + (int64_t)pairs[t] * a.hq_stride + blockIdx.x * Q8_1_BYTES;
+        o[4 + i] = (uint8_t)(int8_t)q;
+        if (i == 0) *(uint32_t*)o = f2h(d) | (f2h(sum) << 16);
     }
 }
 
 // Down-projection rows of one expert tile (in LDS) for its pairs, with the
-// pairs' Q8_1 intermediates already decoded in LDS (xl[p][block]); writes
+// pairs' Q8_1 intermediates decoded in LDS (xl[p][block]); writes
 // dn[pair][row] for the tile's rows.
 template <int T>
 __device__ __forceinline__ void down_tile(const uint8_t* tile, int lstride, const uint32_t* grid,
@@ -357,12 +373,8 @@ __device__ __forceinline__ void down_tile(const uint8_t* tile, int lstride, cons
         float acc = 0.0f;
         if (g < nr) {
             for (int b = j; b < nbF; b += SLOTS) {
-                const XLds& xs = xl[p * nbF + b];
                 XBlk xb;
-#pragma unroll
-                for (int k = 0; k < 8; k++) xb.q[k] = xs.q[k];
-                xb.d = xs.d;
-                xb.sumq = xs.sumq;
+                xlds_to_blk(xl[p * nbF + b], xb);
                 float dw;
                 const int s = block_dot<T>(row, b, xb, grid, &dw);
                 acc = __builtin_fmaf(dw * xb.d, (float)s, acc);
@@ -375,9 +387,9 @@ __device__ __forceinline__ void down_tile(const uint8_t* tile, int lstride, cons
 
 constexpr int DOWN_LDS = 96 * 1024;
 
-// K3: grid (ceil(H/16)).  Stages the down tiles of a batch of experts and the
-// Q8_1 re-quantization of their pairs' h (quantized here, ggml semantics)
-// together, computes, then combines in k order plus the shared expert.
+// K3: grid (ceil(H/16)), 256 threads.  Stages the down tiles of a batch of
+// experts together with their pairs' Q8_1 intermediates (decoded into LDS),
+// computes, then combines in k order plus the shared expert.
 template <int TE, int TS>
 __global__ __launch_bounds__(GEMV_THREADS) void k_moe_down(MoeArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t buf[DOWN_LDS + 16];
@@ -399,9 +411,9 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_down(MoeArgs a) {
         for (int i = tid; i < 512; i += GEMV_THREADS) grid[i] = c_iq3s_grid_moe[i];
     for (int w = tid; w < nw; w += GEMV_THREADS) {
         if (w < nu) {
-            wexp[w] = P[1 + w];
-            np[w] = P[1 + MAX_TOK * MAX_K + w];
-            for (int i = 0; i < np[w]; i++) pl[w][i] = P[1 + 2 * MAX_TOK * MAX_K + w * MAX_TOK + i];
+            wexp[w] = P[PLAN_UEXP + w];
+            np[w] = P[PLAN_UNTOK + w];
+            for (int i = 0; i < np[w]; i++) pl[w][i] = P[PLAN_UPAIR + w * MAX_TOK + i];
         } else {
             wexp[w] = -1;
             np[w] = a.M;
@@ -416,17 +428,15 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_down(MoeArgs a) {
         // a batch of work experts whose tiles and decoded intermediates fit in LDS
         int w1 = w0, used = 0;
         while (w1 < nw) {
-            const int need = TILE_ROWS * ((w1 < nu) ? lsE : lsS) + np[w1] * nbF * (int)sizeof(XLds) + np[w1] * a.F * 4;
+            const int need = TILE_ROWS * ((w1 < nu) ? lsE : lsS) + np[w1] * nbF * (int)sizeof(XLds);
             if (used + need > DOWN_LDS && w1 > w0) break;
             used += need;
             w1++;
         }
-        int hoff = 0;
         {
             int o = 0;
             for (int w = w0; w < w1; w++) { if (tid == 0) boff[w] = o; o += TILE_ROWS * ((w < nu) ? lsE : lsS); }
             for (int w = w0; w < w1; w++) { if (tid == 0) xoff[w] = o; o += np[w] * nbF * (int)sizeof(XLds); }
-            hoff = o;
         }
         __syncthreads();
         for (int w = w0; w < w1; w++) {
@@ -437,38 +447,16 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_down(MoeArgs a) {
                 stage_rows(buf + boff[w], lsS, a.sh_down + (int64_t)r0 * rbS, rbS, nr, (int)rbS, tid,
                            GEMV_THREADS);
         }
-        // h of every pair in the batch: all loads issued before any is used
-        {
-            float* hs = (float*)(buf + hoff);
-            int o = 0;
-            for (int w = w0; w < w1; w++)
-                for (int pi = 0; pi < np[w]; pi++, o++) {
-                    const float4* src = (const float4*)(a.h + (int64_t)pl[w][pi] * a.F);
-                    for (int c = tid; c < a.F / 4; c += GEMV_THREADS) ((float4*)(hs + o * a.F))[c] = src[c];
-                }
-        }
-        __syncthreads();
-        int hbase = 0;
         for (int w = w0; w < w1; w++) {
             XLds* xl = (XLds*)(buf + xoff[w]);
-            const float* hw = (const float*)(buf + hoff) + hbase * a.F;
-            hbase += np[w];
-            quantize_blocks(
-                np[w] * nbF,
-                [&](int b, int i) { return hw[(b / nbF) * a.F + (b % nbF) * QK + i]; },
-                [&](int b, int i, int q, float d, float sum) {
-                    // pack the 32 quants of the block into 8 words through lane shuffles
-                    const int byte = (q & 0xFF) << (8 * (i & 3));
-                    int word = byte | xlane<1>(byte);
-                    word = word | xlane<2>(word);
-                    int s = q + xlane<16>(q);
-                    s = s + xlane<8>(s);
-                    s = s + xlane<4>(s);
-                    s = s + xlane<2>(s);
-                    s = s + xlane<1>(s);
-                    if ((i & 3) == 0) xl[b].q[i >> 2] = word;
-                    if (i == 0) { xl[b].d = h2f(f2h(d)); xl[b].sumq = s; }
-                });
+            for (int i = tid; i < np[w] * nbF; i += GEMV_THREADS) {
+                XBlk xb;
+                load_xblk(a.hq + (int64_t)pl[w][i / nbF] * a.hq_stride + (int64_t)(i % nbF) * Q8_1_BYTES, xb);
+#pragma unroll
+                for (int k = 0; k < 8; k++) xl[i].q[k] = xb.q[k];
+                xl[i].d = xb.d;
+                xl[i].sumq = xb.sumq;
+            }
         }
         __syncthreads();
         for (int w = w0; w < w1; w++) {
@@ -503,8 +491,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_down(MoeArgs a) {
 // ------------------------------------------------------- workspace plan
 
 struct WsPlan {
-    size_t logits, glogit, wts, plan, xq, h, total;
-    int64_t xq_stride;
+    size_t logits, glogit, wts, plan, xq, hq, total;
+    int64_t xq_stride, hq_stride;
 };
 
 static size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -514,12 +502,13 @@ static WsPlan plan_ws(int H, int F, int E, int K, int M) {
     size_t o = 0;
     const int P = M * K + M;
     p.xq_stride = pad_to(H, ROW_PAD) / QK * Q8_1_BYTES;
+    p.hq_stride = pad_to(F, ROW_PAD) / QK * Q8_1_BYTES;
     p.logits = o; o += al256((size_t)M * E * 4);
     p.glogit = o; o += al256((size_t)M * 4);
     p.wts = o; o += al256((size_t)M * K * 4);
-    p.plan = o; o += al256((size_t)(1 + 2 * MAX_TOK * MAX_K + MAX_TOK * MAX_K * MAX_TOK) * 4);
+    p.plan = o; o += al256((size_t)PLAN_INTS * 4);
     p.xq = o; o += al256((size_t)M * p.xq_stride);
-    p.h = o; o += al256((size_t)P * F * 4);
+    p.hq = o; o += al256((size_t)P * p.hq_stride);
     p.total = o;
     return p;
 }
@@ -530,7 +519,7 @@ static void launch_layer(const MoeArgs& a, int stage, hipStream_t s) {
     if (stage < 0 || stage == 0)
         hipLaunchKernelGGL(k_moe_route, dim3(a.E + (a.sh_gate_w ? 1 : 0) + a.M), dim3(256), 0, s, a);
     if (stage < 0 || stage == 1)
-        hipLaunchKernelGGL((k_moe_gate_up<TE, TS>), dim3(a.F / 8, a.M * a.K + 1), dim3(GEMV_THREADS), 0, s, a);
+        hipLaunchKernelGGL((k_moe_gate_up<TE, TS>), dim3(a.F / QK, a.M * a.K + 1), dim3(GU_THREADS), 0, s, a);
     if (stage < 0 || stage == 2)
         hipLaunchKernelGGL((k_moe_down<TE, TS>), dim3((a.H + TILE_ROWS - 1) / TILE_ROWS), dim3(GEMV_THREADS), 0,
                            s, a);
@@ -650,8 +639,8 @@ static void moe_decode(const chimere_moe_layer* L, const float* x, float* out, i
     a.ids_out = ids_out; a.w_out = w_out;
     a.logits = (float*)(w + p.logits); a.glogit = (float*)(w + p.glogit);
     a.wts = (float*)(w + p.wts); a.plan = (int*)(w + p.plan);
-    a.xq = w + p.xq; a.h = (float*)(w + p.h);
-    a.xq_stride = p.xq_stride;
+    a.xq = w + p.xq; a.hq = w + p.hq;
+    a.xq_stride = p.xq_stride; a.hq_stride = p.hq_stride;
     dispatch_layer(L->expert_type, L->shared_type, a, stage, stream);
     check_launch("moe_ffn_decode");
 }

@@ -1,5 +1,16 @@
-// tile_gemv.h -- the 16-row x 16-lane GEMV tile shared by the standalone
-// GEMV and the MoE kernels.  See mmvq.hip for the fp32 order it implements.
+// tile_gemv.h -- the LDS-staged GEMV tile shared by the standalone GEMV and
+// the MoE kernels.
+//
+// A tile is RG*RPG rows handled by RG row groups of 16 lanes (RG*16 threads);
+// group g computes rows g, g+RG, ... (RPG of them).  A row is consumed in
+// chunks of ChunkGeom<T>::BLOCKS 32-element blocks (a multiple of 16): the
+// tile's row segments of a chunk are streamed HBM -> LDS with the widest
+// aligned loads, the chunk's Q8_1 activation blocks are decoded once into LDS,
+// then lane j of a group takes blocks j, j+16, j+32, ... of the chunk.
+// fp32 order (L=16, G=1): per lane acc = fmaf(f32(d_w)*f32(d_x), (float)sumi,
+// acc) over its blocks in ascending order, then the 16 lanes are summed with
+// the halving tree xor 8,4,2,1 (slot_reduce16).  sumi is the exact int32
+// block dot.
 #pragma once
 #include "common.h"
 
@@ -7,8 +18,11 @@ namespace chimere {
 
 template <int T>
 struct ChunkGeom {
-    static constexpr int BYTES = T == T_IQ3_S ? CHUNK_BLOCKS / 8 * 110 : CHUNK_BLOCKS * QTraits<T>::BYTES;
+    // Q8_0 rows are 34 B per block: 32 blocks per chunk keeps 64-row tiles in LDS
+    static constexpr int BLOCKS = T == T_Q8_0 ? 32 : 64;
+    static constexpr int BYTES = T == T_IQ3_S ? BLOCKS / 8 * 110 : BLOCKS * QTraits<T>::BYTES;
 };
+constexpr int MAX_CHUNK_BLOCKS = 64;
 
 // Decoded Q8_1 blocks in LDS
 struct XLds {
@@ -17,34 +31,43 @@ struct XLds {
     int sumq;
 };
 
-// Accumulates, for the 16 rows of a tile, per-lane partial dots against up to
-// NT tokens.  Rows [0, n1) come from base1, rows [n1, n1+n2) from base2 (row
-// stride rb in both).  Token i's Q8_1 row is at X + tok(i) * x_tok_stride
-// where tok(i) = toks ? toks[i] : i.  acc[t] is the lane's partial sum
-// (lane j of row group g covers blocks j, j+16, ... in ascending order);
-// reduce with slot_reduce16.  Contains __syncthreads(): call from all threads.
-template <int T, int NT>
-__device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, int lstride,
-                                          XLds (*__restrict__ xs)[CHUNK_BLOCKS],
+__device__ __forceinline__ void xlds_to_blk(const XLds& s, XBlk& x) {
+#pragma unroll
+    for (int k = 0; k < 8; k++) x.q[k] = s.q[k];
+    x.d = s.d;
+    x.sumq = s.sumq;
+}
+
+// Accumulates per-lane partial dots for the rows of a tile against up to NT
+// tokens.  Tile rows [0, n1) come from base1, rows [n1, n1+n2) from base2
+// (global row stride rb for both); n1 + n2 <= RG*RPG.  Token i's Q8_1 row is
+// at X + tok(i) * x_tok_stride with tok(i) = toks ? toks[i] : i.
+// acc[r][t]: partial sum of the group's r-th row (tile row g + RG*r) for
+// token t; reduce with slot_reduce16.  Contains __syncthreads().
+template <int T, int NT, int RG, int RPG>
+__device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds (*__restrict__ xs)[MAX_CHUNK_BLOCKS],
                                           const uint32_t* __restrict__ grid,
                                           const uint8_t* base1, int n1, const uint8_t* base2, int n2,
                                           int64_t rb, int ncols, const uint8_t* __restrict__ X,
                                           int64_t x_tok_stride, const int* toks, int ntok,
-                                          float (&acc)[NT]) {
+                                          float (&acc)[RPG][NT]) {
+    constexpr int CBLK = ChunkGeom<T>::BLOCKS, CB = ChunkGeom<T>::BYTES, NTH = RG * SLOTS;
     const int tid = threadIdx.x;
     const int g = tid >> 4, j = tid & 15;
     const int nr = n1 + n2;
     const int nb = ncols / QK;
 #pragma unroll
-    for (int t = 0; t < NT; t++) acc[t] = 0.0f;
-    for (int b0 = 0; b0 < nb; b0 += CHUNK_BLOCKS) {
-        const int cb = min(CHUNK_BLOCKS, nb - b0);
+    for (int r = 0; r < RPG; r++)
+#pragma unroll
+        for (int t = 0; t < NT; t++) acc[r][t] = 0.0f;
+    for (int b0 = 0; b0 < nb; b0 += CBLK) {
+        const int cb = min(CBLK, nb - b0);
         const int seg = T == T_IQ3_S ? cb / 8 * 110 : cb * QTraits<T>::BYTES;
         const int64_t goff = T == T_IQ3_S ? (int64_t)b0 / 8 * 110 : (int64_t)b0 * QTraits<T>::BYTES;
         __syncthreads();   // previous users of tile / xs are done
-        if (n1) stage_rows(tile, lstride, base1 + goff, rb, n1, seg, tid, GEMV_THREADS);
-        if (n2) stage_rows(tile + n1 * lstride, lstride, base2 + goff, rb, n2, seg, tid, GEMV_THREADS);
-        for (int i = tid; i < ntok * cb; i += GEMV_THREADS) {
+        if (n1) stage_rows(tile, CB, base1 + goff, rb, n1, seg, tid, NTH);
+        if (n2) stage_rows(tile + n1 * CB, CB, base2 + goff, rb, n2, seg, tid, NTH);
+        for (int i = tid; i < ntok * cb; i += NTH) {
             const int t = i / cb, b = i - t * cb;
             const int tk = toks ? toks[t] : t;
             XBlk xb;
@@ -55,20 +78,21 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, int lstrid
             xs[t][b].sumq = xb.sumq;
         }
         __syncthreads();
-        if (g < nr) {
-            const uint8_t* row = tile + g * lstride;
-            for (int b = j; b < cb; b += SLOTS) {
 #pragma unroll
-                for (int t = 0; t < NT; t++) {
-                    if (t < ntok) {
-                        XBlk xb;
+        for (int r = 0; r < RPG; r++) {
+            const int row_i = g + RG * r;
+            if (row_i < nr) {
+                const uint8_t* row = tile + row_i * CB;
+                for (int b = j; b < cb; b += SLOTS) {
 #pragma unroll
-                        for (int k = 0; k < 8; k++) xb.q[k] = xs[t][b].q[k];
-                        xb.d = xs[t][b].d;
-                        xb.sumq = xs[t][b].sumq;
-                        float dw;
-                        const int s = block_dot<T>(row, b, xb, grid, &dw);
-                        acc[t] = __builtin_fmaf(dw * xb.d, (float)s, acc[t]);
+                    for (int t = 0; t < NT; t++) {
+                        if (t < ntok) {
+                            XBlk xb;
+                            xlds_to_blk(xs[t][b], xb);
+                            float dw;
+                            const int s = block_dot<T>(row, b, xb, grid, &dw);
+                            acc[r][t] = __builtin_fmaf(dw * xb.d, (float)s, acc[r][t]);
+                        }
                     }
                 }
             }
