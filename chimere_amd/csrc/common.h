@@ -163,32 +163,59 @@ __device__ __forceinline__ int block_dot(const uint8_t* row, int b, const XBlk& 
     else return dot_iq3_s(row, (b >> 3) * 110, b & 7, x, grid, dw);
 }
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
+
 // Copy `nrows` row segments of `seg` bytes (global row stride `gstride`) into
-// LDS rows of stride `lstride`, with the widest access the alignment allows.
-__device__ __forceinline__ void stage_rows(uint8_t* __restrict__ lds, int lstride,
-                                           const uint8_t* __restrict__ g, int64_t gstride,
-                                           int nrows, int seg, int tid, int nthreads) {
-    uintptr_t al = (uintptr_t)g | (uintptr_t)gstride | (uintptr_t)seg | (uintptr_t)lstride;
+// LDS, packed with row stride `seg`.  When every piece is 16-byte aligned the
+// copy uses the asynchronous global->LDS loads (global_load_lds_dwordx4: lane
+// l of a wave deposits its 16 bytes at a wave-uniform LDS base + 16*l), so all
+// loads of a phase are in flight together; otherwise all pieces are loaded to
+// registers before any is stored.  The caller completes the copy with
+// lds_copy_wait() + __syncthreads().
+__device__ __forceinline__ void stage_rows(uint8_t* __restrict__ lds, const uint8_t* __restrict__ g,
+                                           int64_t gstride, int nrows, int seg, int tid, int nthreads) {
+    const uintptr_t al = (uintptr_t)g | (uintptr_t)gstride | (uintptr_t)seg | (uintptr_t)lds;
     if ((al & 15) == 0) {
-        int per = seg >> 4, tot = per * nrows;
-        for (int i = tid; i < tot; i += nthreads) {
-            int r = i / per, c = i - r * per;
-            *(uint4*)(lds + r * lstride + c * 16) = *(const uint4*)(g + r * gstride + c * 16);
-        }
-    } else if ((al & 3) == 0) {
-        int per = seg >> 2, tot = per * nrows;
-        for (int i = tid; i < tot; i += nthreads) {
-            int r = i / per, c = i - r * per;
-            *(uint32_t*)(lds + r * lstride + c * 4) = *(const uint32_t*)(g + r * gstride + c * 4);
+        const int per = seg >> 4, tot = per * nrows;
+        const int lane = tid & 63, wave = tid >> 6, nw = nthreads >> 6;
+        for (int c0 = wave * 64; c0 < tot; c0 += nw * 64) {
+            const int c = c0 + lane;
+            if (c < tot) {
+                const int r = c / per, col = c - r * per;
+                __builtin_amdgcn_global_load_lds((const glb_void_t*)(g + r * gstride + col * 16),
+                                                 (lds_void_t*)(lds + c0 * 16), 16, 0, 0);
+            }
         }
     } else {
-        int tot = seg * nrows;
-        for (int i = tid; i < tot; i += nthreads) {
-            int r = i / seg, c = i - r * seg;
-            lds[r * lstride + c] = g[r * gstride + c];
+        // rare unaligned case: whole-dword or byte pieces, up to 8 in flight per thread
+        const bool w4 = (al & 3) == 0;
+        const int unit = w4 ? 4 : 1, per = seg / unit, tot = per * nrows;
+        for (int i0 = 0; i0 < tot; i0 += 8 * nthreads) {
+            uint32_t v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int i = i0 + k * nthreads + tid;
+                if (i < tot) {
+                    const int r = i / per, c = i - r * per;
+                    v[k] = w4 ? *(const uint32_t*)(g + r * gstride + c * 4) : g[r * gstride + c];
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int i = i0 + k * nthreads + tid;
+                if (i < tot) {
+                    if (w4) *(uint32_t*)(lds + i * 4) = v[k];
+                    else lds[i] = (uint8_t)v[k];
+                }
+            }
         }
     }
 }
+
+// Waits for this thread's outstanding memory operations, including the
+// asynchronous global->LDS copies; follow with __syncthreads().
+__device__ __forceinline__ void lds_copy_wait() { __builtin_amdgcn_s_waitcnt(0); }
 
 // Value of lane (lane ^ M) without going through LDS: DPP quad permutes for
 // M = 1, 2, row shifts by M (direction picked per lane) for M = 4, 8, and the

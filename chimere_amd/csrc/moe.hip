@@ -24,6 +24,20 @@
 #include "common.h"
 #include "tile_gemv.h"
 
+// Phase timestamps for latency analysis (debug builds with
+// -DCHIMERE_PHASE_TIMING only): thread 0 of a work-group records the 100 MHz
+// real-time counter at numbered points into workspace.
+#ifdef CHIMERE_PHASE_TIMING
+#define PHASE(kern, i)                                                                      \
+    do {                                                                                     \
+        if (threadIdx.x == 0)                                                                \
+            a.phase[((kern) * 4096 + blockIdx.x + blockIdx.y * gridDim.x) * 8 + (i)] =        \
+                __builtin_amdgcn_s_memrealtime();                                           \
+    } while (0)
+#else
+#define PHASE(kern, i) do {} while (0)
+#endif
+
 namespace chimere {
 
 __constant__ uint32_t c_iq3s_grid_moe[512] = CHIMERE_IQ3S_GRID_INIT;
@@ -59,14 +73,25 @@ __device__ __forceinline__ float tree_sum256(float v, float* red) {
 template <int NT>
 __device__ __forceinline__ void f32_row_dot(const float* __restrict__ a, const float* __restrict__ x,
                                             int H, int ntok, float* red, float (&out)[NT]) {
+    constexpr int U = 8;   // columns per thread loaded together before use
     float acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) acc[t] = 0.0f;
-    for (int j = threadIdx.x; j < H; j += 256) {
-        const float av = a[j];
+    for (int j0 = threadIdx.x; j0 < H; j0 += 256 * U) {
+        float av[U];
 #pragma unroll
-        for (int t = 0; t < NT; t++)
-            if (t < ntok) acc[t] = __builtin_fmaf(av, x[(int64_t)t * H + j], acc[t]);
+        for (int u = 0; u < U; u++) av[u] = j0 + 256 * u < H ? a[j0 + 256 * u] : 0.0f;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            if (t < ntok) {
+                float xv[U];
+#pragma unroll
+                for (int u = 0; u < U; u++) xv[u] = j0 + 256 * u < H ? x[(int64_t)t * H + j0 + 256 * u] : 0.0f;
+#pragma unroll
+                for (int u = 0; u < U; u++)
+                    if (j0 + 256 * u < H) acc[t] = __builtin_fmaf(av[u], xv[u], acc[t]);
+            }
+        }
     }
 #pragma unroll
     for (int t = 0; t < NT; t++)
@@ -205,6 +230,7 @@ struct MoeArgs {
     uint8_t* xq;        // [M][xq_stride]   Q8_1(x)
     uint8_t* hq;        // [M*K + M][hq_stride]   Q8_1(h) per (token, k) pair and shared
     int64_t xq_stride, hq_stride;
+    uint64_t* phase;    // debug timestamps (CHIMERE_PHASE_TIMING builds)
 };
 
 constexpr int PLAN_UEXP = 1, PLAN_UNTOK = 1 + MAX_TOK * MAX_K, PLAN_UPAIR = 1 + 2 * MAX_TOK * MAX_K;
@@ -222,6 +248,7 @@ struct Plan {
 // K1: grid E (router rows) + has_gate (shared-expert gate row) + M (x quantizers).
 __global__ __launch_bounds__(256) void k_moe_route(MoeArgs a) {
     __shared__ float red[256];
+    PHASE(0, 0);
     const int row = blockIdx.x;
     const int ng = a.sh_gate_w ? 1 : 0;
     if (row >= a.E + ng) {
@@ -247,6 +274,7 @@ __global__ __launch_bounds__(256) void k_moe_route(MoeArgs a) {
             else a.glogit[t] = v[t];
         }
     }
+    PHASE(0, 1);
 }
 
 constexpr int GU_RG = 32;                  // K2 row groups: 512 threads
@@ -278,6 +306,7 @@ __global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
     const int u = blockIdx.y;
     const bool shared = u == a.M * a.K;
     const int tid = threadIdx.x;
+    PHASE(1, 0);
     if (shared && !a.has_shared) return;
     int ntok;
     if (shared) {
@@ -290,6 +319,7 @@ __global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
         int* map = (int*)tile;
         for (int e = tid; e < a.E; e += GU_THREADS) map[e] = -1;
         __syncthreads();
+        PHASE(1, 1);
         if (tid == 0) {
             int nu = 0;
             for (int t = 0; t < a.M; t++)
@@ -324,6 +354,7 @@ __global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
     }
     if constexpr (TE == T_IQ3_S || TS == T_IQ3_S)
         for (int i = tid; i < 512; i += GU_THREADS) grid[i] = c_iq3s_grid_moe[i];
+    PHASE(1, 2);
     const int r0 = blockIdx.x * QK;
     float acc[2][MAX_TOK];
     if (shared) {
@@ -337,6 +368,7 @@ __global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
                                          a.up + e * a.su + r0 * rb, QK, rb, a.H, a.xq, a.xq_stride, toks,
                                          ntok, acc);
     }
+    PHASE(1, 3);
     const int g = tid >> 4, j = tid & 15;
 #pragma unroll
     for (int t = 0; t < MAX_TOK; t++) {
@@ -358,6 +390,7 @@ __global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
         o[4 + i] = (uint8_t)(int8_t)q;
         if (i == 0) *(uint32_t*)o = f2h(d) | (f2h(sum) << 16);
     }
+    PHASE(1, 4);
 }
 
 // Down-projection rows of one expert tile (in LDS) for its pairs, with the
@@ -401,6 +434,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_down(MoeArgs a) {
     __shared__ int boff[MAX_TOK * MAX_K + 1], xoff[MAX_TOK * MAX_K + 1];
 
     const int tid = threadIdx.x;
+    PHASE(2, 0);
     const int r0 = blockIdx.x * TILE_ROWS;
     const int nr = min(TILE_ROWS, a.H - r0);
     const int* P = a.plan;
@@ -421,31 +455,31 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_down(MoeArgs a) {
         }
     }
     __syncthreads();
+    PHASE(2, 1);
     const int64_t rbE = row_bytes(TE, a.F), rbS = row_bytes(TS, a.F);
-    const int lsE = (int)((rbE + 15) & ~15), lsS = (int)((rbS + 15) & ~15);
+    const int lsE = (int)rbE, lsS = (int)rbS;   // tiles packed with the row stride
     int w0 = 0;
     while (w0 < nw) {
         // a batch of work experts whose tiles and decoded intermediates fit in LDS
         int w1 = w0, used = 0;
         while (w1 < nw) {
-            const int need = TILE_ROWS * ((w1 < nu) ? lsE : lsS) + np[w1] * nbF * (int)sizeof(XLds);
+            const int need = ((TILE_ROWS * ((w1 < nu) ? lsE : lsS) + 15) & ~15) + np[w1] * nbF * (int)sizeof(XLds);
             if (used + need > DOWN_LDS && w1 > w0) break;
             used += need;
             w1++;
         }
         {
             int o = 0;
-            for (int w = w0; w < w1; w++) { if (tid == 0) boff[w] = o; o += TILE_ROWS * ((w < nu) ? lsE : lsS); }
+            for (int w = w0; w < w1; w++) { if (tid == 0) boff[w] = o; o += (TILE_ROWS * ((w < nu) ? lsE : lsS) + 15) & ~15; }
             for (int w = w0; w < w1; w++) { if (tid == 0) xoff[w] = o; o += np[w] * nbF * (int)sizeof(XLds); }
         }
         __syncthreads();
         for (int w = w0; w < w1; w++) {
             if (w < nu)
-                stage_rows(buf + boff[w], lsE, a.down + (int64_t)wexp[w] * a.sd + (int64_t)r0 * rbE, rbE, nr,
-                           (int)rbE, tid, GEMV_THREADS);
+                stage_rows(buf + boff[w], a.down + (int64_t)wexp[w] * a.sd + (int64_t)r0 * rbE, rbE, nr, (int)rbE,
+                           tid, GEMV_THREADS);
             else
-                stage_rows(buf + boff[w], lsS, a.sh_down + (int64_t)r0 * rbS, rbS, nr, (int)rbS, tid,
-                           GEMV_THREADS);
+                stage_rows(buf + boff[w], a.sh_down + (int64_t)r0 * rbS, rbS, nr, (int)rbS, tid, GEMV_THREADS);
         }
         for (int w = w0; w < w1; w++) {
             XLds* xl = (XLds*)(buf + xoff[w]);
@@ -458,13 +492,17 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_down(MoeArgs a) {
                 xl[i].sumq = xb.sumq;
             }
         }
+        PHASE(2, 2);
+        lds_copy_wait();
         __syncthreads();
+        PHASE(2, 3);
         for (int w = w0; w < w1; w++) {
             const XLds* xl = (const XLds*)(buf + xoff[w]);
             if (w < nu) down_tile<TE>(buf + boff[w], lsE, grid, xl, nbF, pl[w], np[w], nr, dn);
             else down_tile<TS>(buf + boff[w], lsS, grid, xl, nbF, pl[w], np[w], nr, dn);
         }
         __syncthreads();
+        PHASE(2, 4);
         w0 = w1;
     }
     // combine: acc = sum_k fmaf(w_k, dn_k, acc); out = fmaf(shared, sigmoid(g), acc)
@@ -486,12 +524,13 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_down(MoeArgs a) {
             a.out[(int64_t)t * a.H + r0 + r] = o;
         }
     }
+    PHASE(2, 5);
 }
 
 // ------------------------------------------------------- workspace plan
 
 struct WsPlan {
-    size_t logits, glogit, wts, plan, xq, hq, total;
+    size_t logits, glogit, wts, plan, xq, hq, phase, total;
     int64_t xq_stride, hq_stride;
 };
 
@@ -509,6 +548,9 @@ static WsPlan plan_ws(int H, int F, int E, int K, int M) {
     p.plan = o; o += al256((size_t)PLAN_INTS * 4);
     p.xq = o; o += al256((size_t)M * p.xq_stride);
     p.hq = o; o += al256((size_t)P * p.hq_stride);
+#ifdef CHIMERE_PHASE_TIMING
+    p.phase = o; o += al256((size_t)3 * 4096 * 8 * 8);
+#endif
     p.total = o;
     return p;
 }
@@ -641,6 +683,7 @@ static void moe_decode(const chimere_moe_layer* L, const float* x, float* out, i
     a.wts = (float*)(w + p.wts); a.plan = (int*)(w + p.plan);
     a.xq = w + p.xq; a.hq = w + p.hq;
     a.xq_stride = p.xq_stride; a.hq_stride = p.hq_stride;
+    a.phase = (uint64_t*)(w + p.phase);
     dispatch_layer(L->expert_type, L->shared_type, a, stage, stream);
     check_launch("moe_ffn_decode");
 }

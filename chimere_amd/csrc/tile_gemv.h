@@ -51,7 +51,7 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds (*__r
                                           int64_t rb, int ncols, const uint8_t* __restrict__ X,
                                           int64_t x_tok_stride, const int* toks, int ntok,
                                           float (&acc)[RPG][NT]) {
-    constexpr int CBLK = ChunkGeom<T>::BLOCKS, CB = ChunkGeom<T>::BYTES, NTH = RG * SLOTS;
+    constexpr int CBLK = ChunkGeom<T>::BLOCKS, NTH = RG * SLOTS;
     const int tid = threadIdx.x;
     const int g = tid >> 4, j = tid & 15;
     const int nr = n1 + n2;
@@ -65,8 +65,9 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds (*__r
         const int seg = T == T_IQ3_S ? cb / 8 * 110 : cb * QTraits<T>::BYTES;
         const int64_t goff = T == T_IQ3_S ? (int64_t)b0 / 8 * 110 : (int64_t)b0 * QTraits<T>::BYTES;
         __syncthreads();   // previous users of tile / xs are done
-        if (n1) stage_rows(tile, CB, base1 + goff, rb, n1, seg, tid, NTH);
-        if (n2) stage_rows(tile + n1 * CB, CB, base2 + goff, rb, n2, seg, tid, NTH);
+        // rows are packed with stride seg (== CB except in a ragged last chunk)
+        if (n1) stage_rows(tile, base1 + goff, rb, n1, seg, tid, NTH);
+        if (n2) stage_rows(tile + n1 * seg, base2 + goff, rb, n2, seg, tid, NTH);
         for (int i = tid; i < ntok * cb; i += NTH) {
             const int t = i / cb, b = i - t * cb;
             const int tk = toks ? toks[t] : t;
@@ -77,12 +78,13 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds (*__r
             xs[t][b].d = xb.d;
             xs[t][b].sumq = xb.sumq;
         }
+        lds_copy_wait();
         __syncthreads();
 #pragma unroll
         for (int r = 0; r < RPG; r++) {
             const int row_i = g + RG * r;
             if (row_i < nr) {
-                const uint8_t* row = tile + row_i * CB;
+                const uint8_t* row = tile + row_i * seg;
                 for (int b = j; b < cb; b += SLOTS) {
 #pragma unroll
                     for (int t = 0; t < NT; t++) {
