@@ -179,12 +179,21 @@ __device__ __forceinline__ void stage_rows(uint8_t* __restrict__ lds, const uint
     if ((al & 15) == 0) {
         const int per = seg >> 4, tot = per * nrows;
         const int lane = tid & 63, wave = tid >> 6, nw = nthreads >> 6;
-        for (int c0 = wave * 64; c0 < tot; c0 += nw * 64) {
-            const int c = c0 + lane;
-            if (c < tot) {
-                const int r = c / per, col = c - r * per;
-                __builtin_amdgcn_global_load_lds((const glb_void_t*)(g + r * gstride + col * 16),
-                                                 (lds_void_t*)(lds + c0 * 16), 16, 0, 0);
+        if (gstride == seg) {   // rows contiguous in memory: one linear copy
+            for (int c0 = wave * 64; c0 < tot; c0 += nw * 64) {
+                const int c = c0 + lane;
+                if (c < tot)
+                    __builtin_amdgcn_global_load_lds((const glb_void_t*)(g + c * 16), (lds_void_t*)(lds + c0 * 16),
+                                                     16, 0, 0);
+            }
+        } else {
+            for (int c0 = wave * 64; c0 < tot; c0 += nw * 64) {
+                const int c = c0 + lane;
+                if (c < tot) {
+                    const int r = c / per, col = c - r * per;
+                    __builtin_amdgcn_global_load_lds((const glb_void_t*)(g + r * gstride + col * 16),
+                                                     (lds_void_t*)(lds + c0 * 16), 16, 0, 0);
+                }
             }
         }
     } else {

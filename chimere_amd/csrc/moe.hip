@@ -44,7 +44,8 @@ __constant__ uint32_t c_iq3s_grid_moe[512] = CHIMERE_IQ3S_GRID_INIT;
 
 constexpr int MAX_TOK = 8;
 constexpr int MAX_K = 16;
-constexpr int MAX_E = 1024;
+constexpr int MAX_E = 1024;        // standalone top-k
+constexpr int MAX_E_FUSED = 256;   // fused MoE layer (one logit per thread of a 256-thread group)
 
 // ------------------------------------------------------------ reductions
 
@@ -191,6 +192,89 @@ __device__ __forceinline__ void topk_wave_any(const float* logits, int E, int K,
     else topk_wave<16>(logits, E, K, idx, w);
 }
 
+// Softmax + top-k of one logits row (E <= 256) by a 256-thread group, with
+// low dependent depth.  Thread i owns logit i (padding i >= E).  max: wave
+// DPP butterflies + LDS; sum: the reference's strided halving tree (strides
+// 128 and 64 through LDS, 32..1 by xor exchanges, which equal the tree at
+// lane 0); p = ev / sum.  Selection: a bitonic sort, descending, of the
+// 41-bit keys (f32 bits of p << 11 | 1024 - index) -- the same set and order
+// as k rounds of arg-max with ties to the lowest index; strides >= 64 go
+// through LDS, smaller ones are in-wave DPP / permlane exchanges.  The first
+// K threads of the group then hold the result; weights are renormalised by
+// the sequential sum of the selected probabilities.  `scr` is LDS scratch of
+// 256 uint64 + 8 floats for this group; every thread of the work-group must
+// call this the same number of times (it contains __syncthreads()).
+__device__ __forceinline__ uint64_t xlane64(uint64_t v, int m) {
+    uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+    switch (m) {
+    case 1: lo = xlane<1>((int)lo); hi = xlane<1>((int)hi); break;
+    case 2: lo = xlane<2>((int)lo); hi = xlane<2>((int)hi); break;
+    case 4: lo = xlane<4>((int)lo); hi = xlane<4>((int)hi); break;
+    case 8: lo = xlane<8>((int)lo); hi = xlane<8>((int)hi); break;
+    case 16: lo = xlane<16>((int)lo); hi = xlane<16>((int)hi); break;
+    default: lo = xlane<32>((int)lo); hi = xlane<32>((int)hi); break;
+    }
+    return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ void topk_block256(const float* __restrict__ logits, int E, int K, bool active, int* idx_out,
+                              float* w_out, uint64_t* scr) {
+    const int i = threadIdx.x & 255;
+    const int wv = i >> 6;
+    float* fs = (float*)(scr + 256);
+    const float l = (active && i < E) ? logits[i] : -__builtin_huge_valf();
+    float m = bfly32_max(__builtin_fmaxf(l, xlane<32>(l)));
+    if ((i & 63) == 0) fs[wv] = m;
+    __syncthreads();
+    m = __builtin_fmaxf(__builtin_fmaxf(fs[0], fs[1]), __builtin_fmaxf(fs[2], fs[3]));
+    const float ev = (active && i < E) ? det_exp(l - m) : 0.0f;
+    float* ps = (float*)scr;
+    ps[i] = ev;
+    __syncthreads();
+    if (i < 128) ps[i] = ps[i] + ps[i + 128];
+    __syncthreads();
+    float sum = 0.0f;
+    if (i < 64) {
+        float v = ps[i] + ps[i + 64];
+        v = v + xlane<32>(v);
+        sum = bfly32_sum(v);
+        if (i == 0) fs[4] = sum;
+    }
+    __syncthreads();
+    sum = fs[4];
+    const float p = sum > 0.0f ? ev / sum : 1.0f / (float)E;
+    uint64_t key = (active && i < E) ? (((uint64_t)__builtin_bit_cast(uint32_t, p)) << 11) | (uint64_t)(1024 - i) : 0;
+    __syncthreads();   // ps (aliases scr) is free again
+    for (int k = 2; k <= 256; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            uint64_t other;
+            if (j >= 64) {
+                scr[i] = key;
+                __syncthreads();
+                other = scr[i ^ j];
+                __syncthreads();
+            } else {
+                other = xlane64(key, j);
+            }
+            const bool lower = (i & j) == 0;
+            const bool desc = (i & k) == 0 || k == 256;
+            const uint64_t mx = key > other ? key : other, mn = key > other ? other : key;
+            key = (lower == desc) ? mx : mn;
+        }
+    }
+    // threads 0..K-1 (wave 0 of the group) hold the K largest keys in order
+    const uint32_t pb = (uint32_t)(key >> 11);
+    const float pv = __builtin_bit_cast(float, pb);
+    float ws = 0.0f;
+    if (wv == 0) {
+        for (int k = 0; k < K; k++) ws += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pv), k));
+    }
+    if (active && i < K) {
+        idx_out[i] = 1024 - (int)(key & 0x7FF);
+        w_out[i] = ws > 0.0f ? pv * (1.0f / ws) : pv;
+    }
+}
+
 // Q8_1 quantization of `nblk` 32-blocks (ggml semantics, see quant.hip) by a
 // 256-thread group, one half-wave per block.  src(b, i) is element i of block
 // b; emit(b, i, q, d, sum) receives the block's results (every lane gets d
@@ -277,31 +361,33 @@ __global__ __launch_bounds__(256) void k_moe_route(MoeArgs a) {
     PHASE(0, 1);
 }
 
-constexpr int GU_RG = 32;                  // K2 row groups: 512 threads
+constexpr int GU_RG = 64;                  // K2 row groups: 1024 threads
 constexpr int GU_THREADS = GU_RG * SLOTS;
 
-// K2: grid (F/32, M*K + 1), 512 threads.  Every routed work-group recomputes
+// K2: grid (F/32, M*K + 1), 1024 threads.  Every routed work-group recomputes
 // the routing (top-k per token, one wave each) and the distinct-expert plan
 // from the logits, so no work-group waits on another; blockIdx.y < n_unique
 // selects a distinct expert, blockIdx.y == M*K the shared expert.  Work-group
 // (0,0) publishes routing and plan for K3.  A tile holds 32 gate + 32 up rows
-// (group g computes gate row g and up row g), so the work-group owns whole
-// 32-row blocks of h = silu(gate) * up and writes them Q8_1-quantized.
+// (group g < 32 computes gate row g, group 32 + g up row g), so the
+// work-group owns whole 32-row blocks of h = silu(gate) * up and writes them
+// Q8_1-quantized.
 template <int TE, int TS>
 __global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
     constexpr int CBE = ChunkGeom<TE>::BYTES, CBS = ChunkGeom<TS>::BYTES;
     constexpr int CB = CBE > CBS ? CBE : CBS;
     // the tile buffer first holds the expert map and the plan (routing phase)
-    constexpr int ROUTE_BYTES = MAX_E * 4 + (int)sizeof(Plan);
-    constexpr int TILE_BYTES = 2 * GU_RG * CB + 16 > ROUTE_BYTES ? 2 * GU_RG * CB + 16 : ROUTE_BYTES;
+    constexpr int ROUTE_BYTES = MAX_E_FUSED * 4 + (int)sizeof(Plan) + 4 * (256 + 32) * 8;
+    constexpr int TILE_BYTES = GU_RG * CB + 16 > ROUTE_BYTES ? GU_RG * CB + 16 : ROUTE_BYTES;
     __shared__ __attribute__((aligned(16))) uint8_t tile[TILE_BYTES];
     __shared__ XLds xs[MAX_TOK][MAX_CHUNK_BLOCKS];
     __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
-    __shared__ float hres[MAX_TOK][QK];
+    __shared__ float hg[MAX_TOK][QK], hu[MAX_TOK][QK];
     __shared__ int toks[MAX_TOK], pairs[MAX_TOK];
     __shared__ int s_ids[MAX_TOK * MAX_K];
     __shared__ float s_w[MAX_TOK * MAX_K];
-    Plan& pl = *(Plan*)(tile + MAX_E * 4);
+    Plan& pl = *(Plan*)(tile + MAX_E_FUSED * 4);
+    uint64_t* tscr = (uint64_t*)(tile + MAX_E_FUSED * 4 + sizeof(Plan));
 
     const int u = blockIdx.y;
     const bool shared = u == a.M * a.K;
@@ -313,9 +399,14 @@ __global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
         ntok = a.M;
         if (tid < a.M) { toks[tid] = tid; pairs[tid] = a.M * a.K + tid; }
     } else {
-        const int wave = tid >> 6;
-        for (int t = wave; t < a.M; t += GU_THREADS / 64)
-            topk_wave_any(a.logits + t * a.E, a.E, a.K, s_ids + t * a.K, s_w + t * a.K);
+        const int grp = tid >> 8;   // four 256-thread groups, one token each per pass
+        for (int t0 = 0; t0 < a.M; t0 += GU_THREADS / 256) {
+            const int t = t0 + grp;
+            const bool act = t < a.M;
+            topk_block256(a.logits + (act ? t : 0) * a.E, a.E, a.K, act, s_ids + (act ? t : 0) * a.K,
+                          s_w + (act ? t : 0) * a.K, tscr + grp * (256 + 32));
+        }
+        __syncthreads();
         int* map = (int*)tile;
         for (int e = tid; e < a.E; e += GU_THREADS) map[e] = -1;
         __syncthreads();
@@ -356,15 +447,15 @@ __global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
         for (int i = tid; i < 512; i += GU_THREADS) grid[i] = c_iq3s_grid_moe[i];
     PHASE(1, 2);
     const int r0 = blockIdx.x * QK;
-    float acc[2][MAX_TOK];
+    float acc[1][MAX_TOK];
     if (shared) {
         const int64_t rb = row_bytes(TS, a.H);
-        tile_gemv<TS, MAX_TOK, GU_RG, 2>(tile, xs, grid, a.sh_gate + r0 * rb, QK, a.sh_up + r0 * rb, QK, rb,
+        tile_gemv<TS, MAX_TOK, GU_RG, 1>(tile, xs, grid, a.sh_gate + r0 * rb, QK, a.sh_up + r0 * rb, QK, rb,
                                          a.H, a.xq, a.xq_stride, toks, ntok, acc);
     } else {
         const int64_t rb = row_bytes(TE, a.H);
         const int64_t e = pl.uexp[u];
-        tile_gemv<TE, MAX_TOK, GU_RG, 2>(tile, xs, grid, a.gate + e * a.sg + r0 * rb, QK,
+        tile_gemv<TE, MAX_TOK, GU_RG, 1>(tile, xs, grid, a.gate + e * a.sg + r0 * rb, QK,
                                          a.up + e * a.su + r0 * rb, QK, rb, a.H, a.xq, a.xq_stride, toks,
                                          ntok, acc);
     }
@@ -373,16 +464,18 @@ __global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
 #pragma unroll
     for (int t = 0; t < MAX_TOK; t++) {
         if (t < ntok) {
-            const float gv = slot_reduce16(acc[0][t]);
-            const float uv = slot_reduce16(acc[1][t]);
-            if (j == 0) hres[t][g] = det_silu(gv) * uv;
+            const float v = slot_reduce16(acc[0][t]);
+            if (j == 0) {
+                if (g < QK) hg[t][g] = v;
+                else hu[t][g - QK] = v;
+            }
         }
     }
     __syncthreads();
     // one half-wave per token quantizes the 32-row block of h (ggml Q8_1)
     if ((tid >> 5) < ntok) {
         const int t = tid >> 5, i = tid & 31;
-        const float xi = hres[t][i];
+        const float xi = det_silu(hg[t][i]) * hu[t][i];
         const float amax = bfly32_max(__builtin_fabsf(xi)), sum = bfly32_sum(xi);
         const float d = amax / 127.0f;
         const int q = amax == 0.0f ? 0 : (int)__builtin_roundf(xi / d);
@@ -481,11 +574,18 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_down(MoeArgs a) {
             else
                 stage_rows(buf + boff[w], a.sh_down + (int64_t)r0 * rbS, rbS, nr, (int)rbS, tid, GEMV_THREADS);
         }
-        for (int w = w0; w < w1; w++) {
-            XLds* xl = (XLds*)(buf + xoff[w]);
-            for (int i = tid; i < np[w] * nbF; i += GEMV_THREADS) {
+        // decode every pair's Q8_1 intermediate of the batch in one parallel pass
+        // (xoff of consecutive work experts is contiguous, so block i of the batch
+        // lands at xoff[w0] + i)
+        {
+            int tot = 0;
+            for (int w = w0; w < w1; w++) tot += np[w] * nbF;
+            XLds* xl = (XLds*)(buf + xoff[w0]);
+            for (int i = tid; i < tot; i += GEMV_THREADS) {
+                int w = w0, r = i;
+                while (r >= np[w] * nbF) { r -= np[w] * nbF; w++; }
                 XBlk xb;
-                load_xblk(a.hq + (int64_t)pl[w][i / nbF] * a.hq_stride + (int64_t)(i % nbF) * Q8_1_BYTES, xb);
+                load_xblk(a.hq + (int64_t)pl[w][r / nbF] * a.hq_stride + (int64_t)(r % nbF) * Q8_1_BYTES, xb);
 #pragma unroll
                 for (int k = 0; k < 8; k++) xl[i].q[k] = xb.q[k];
                 xl[i].d = xb.d;
@@ -651,8 +751,8 @@ static void moe_decode(const chimere_moe_layer* L, const float* x, float* out, i
     CHIMERE_REQUIRE(ntok >= 1 && ntok <= MAX_TOK, CHIMERE_ERR_ARG, "moe_ffn_decode: ntok=%d not in 1..8", ntok);
     CHIMERE_REQUIRE(H > 0 && H % 256 == 0 && F > 0 && F % 256 == 0 && F <= 2048, CHIMERE_ERR_ARG,
                     "moe_ffn_decode: hidden=%d / ffn=%d must be multiples of 256 (ffn <= 2048)", H, F);
-    CHIMERE_REQUIRE(E >= 1 && E <= MAX_E && K >= 1 && K <= MAX_K && K <= E, CHIMERE_ERR_ARG,
-                    "moe_ffn_decode: n_experts=%d top_k=%d out of range", E, K);
+    CHIMERE_REQUIRE(E >= 1 && E <= MAX_E_FUSED && K >= 1 && K <= MAX_K && K <= E, CHIMERE_ERR_ARG,
+                    "moe_ffn_decode: n_experts=%d (<= 256) top_k=%d (<= 16) out of range", E, K);
     CHIMERE_REQUIRE(valid_type(L->expert_type), CHIMERE_ERR_ARG, "moe_ffn_decode: expert_type %d", L->expert_type);
     const bool has_sh = L->shared_type >= 0;
     CHIMERE_REQUIRE(!has_sh || (valid_type(L->shared_type) && L->sh_gate && L->sh_up && L->sh_down),
