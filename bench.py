@@ -149,12 +149,17 @@ def main():
 
     # per-kernel timing: graphs of NSLOT launches of one stage each (slot plans prepared above)
     per_kernel = {}
+    NBF = F // 32
     kbytes = {
+        # router weights + x + logits + Q8_1(x)
         "k_moe_route": E * H * 4 + H * 4 + E * 4 + (H // 32) * 36,
-        "k_moe_gate_up": 9 * 2 * F * row_bytes(Q4_0, H) + (H // 32) * 36 + 9 * F * 4 + 9 * (F // 32) * 36,
-        "k_moe_down": 9 * H * row_bytes(Q4_0, F) + 9 * (F // 32) * 36 + H * 4,
+        # 9 experts' gate/up/down weights + logits + Q8_1(x) + down terms written
+        "k_moe_expert": 9 * (2 * F * row_bytes(Q4_0, H) + H * row_bytes(Q4_0, F)) + E * 4 + (H // 32) * 36
+                        + 9 * H * NBF * 4,
+        # down terms read + routing weights + output
+        "k_moe_combine": 9 * H * NBF * 4 + K * 4 + H * 4,
     }
-    for stage, name in enumerate(["k_moe_route", "k_moe_gate_up", "k_moe_down"]):
+    for stage, name in enumerate(["k_moe_route", "k_moe_expert", "k_moe_combine"]):
         n = 4 * NSLOT
         t, _ = graph_time([step_fn(i, stage) for i in range(n)])
         avg = t / n

@@ -103,56 +103,118 @@ __device__ __forceinline__ void load_xblk(const uint8_t* __restrict__ p, XBlk& x
     x.sumq = s;
 }
 
-// ---- exact int32 block dots of one weight block (in LDS) with one Q8_1 block.
-// `off` is the byte offset of the block (IQ3_S: of its 110-byte superblock)
-// within `row`; returns sumi and sets *dw = f32(weight scale).
+// ---- exact int32 block dots of one weight block with one Q8_1 block.
+// The *_core functions take the block's fields already in registers; the
+// LDS versions read them at byte offset `off` (IQ3_S: of the 110-byte
+// superblock) within `row`.  They return sumi and set *dw = f32(weight scale).
 
-__device__ __forceinline__ int dot_q8_0(const uint8_t* row, int off, const XBlk& x, float* dw) {
-    *dw = h2f(lds_u16(row, off));
+__device__ __forceinline__ int dot_q8_0_core(uint32_t dbits, const uint32_t (&q)[8], const XBlk& x, float* dw) {
+    *dw = h2f(dbits);
     int s = 0;
 #pragma unroll
-    for (int i = 0; i < 8; i++) s = dot4((int)lds_u32(row, off + 2 + 4 * i), x.q[i], s);
+    for (int i = 0; i < 8; i++) s = dot4((int)q[i], x.q[i], s);
     return s;
 }
 
-__device__ __forceinline__ int dot_q4_0(const uint8_t* row, int off, const XBlk& x, float* dw) {
-    *dw = h2f(lds_u16(row, off));
+__device__ __forceinline__ int dot_q4_0_core(uint32_t dbits, const uint32_t (&qs)[4], const XBlk& x, float* dw) {
+    *dw = h2f(dbits);
     int s = 0;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        uint32_t v = lds_u32(row, off + 2 + 4 * i);
-        s = dot4((int)(v & 0x0F0F0F0Fu), x.q[i], s);          // elements 4i..4i+3
-        s = dot4((int)((v >> 4) & 0x0F0F0F0Fu), x.q[4 + i], s); // elements 16+4i..
+        s = dot4((int)(qs[i] & 0x0F0F0F0Fu), x.q[i], s);          // elements 4i..4i+3
+        s = dot4((int)((qs[i] >> 4) & 0x0F0F0F0Fu), x.q[4 + i], s); // elements 16+4i..
     }
     return s - 8 * x.sumq;
 }
 
-// sub-block ib (0..7) of the IQ3_S superblock at `off`; grid in LDS
-__device__ __forceinline__ int dot_iq3_s(const uint8_t* row, int off, int ib, const XBlk& x,
-                                         const uint32_t* grid, float* dw) {
-    *dw = h2f(lds_u16(row, off));
-    uint32_t qs0 = lds_u32(row, off + 2 + 8 * ib);
-    uint32_t qs1 = lds_u32(row, off + 6 + 8 * ib);
-    uint32_t qh = row[off + 66 + ib];
-    uint32_t sg = lds_u32(row, off + 74 + 4 * ib);
-    uint32_t sc = row[off + 106 + (ib >> 1)];
-    int mult = 1 + 2 * (int)((sc >> (4 * (ib & 1))) & 0xFu);
+// IQ3_S sub-block: qs0/qs1 its 8 index bytes, qh its high-bit byte, sg its 4
+// sign bytes, nib its 4-bit scale; grid = codebook (LDS)
+__device__ __forceinline__ int dot_iq3_s_core(uint32_t dbits, uint32_t qs0, uint32_t qs1, uint32_t qh, uint32_t sg,
+                                              uint32_t nib, const XBlk& x, const uint32_t* grid, float* dw) {
+    *dw = h2f(dbits);
+    const int mult = 1 + 2 * (int)nib;
     int s = 0;
 #pragma unroll
     for (int l = 0; l < 4; l++) {
-        uint32_t qsw = l < 2 ? qs0 : qs1;
-        uint32_t i0 = ((qsw >> (16 * (l & 1))) & 0xFFu) | (((qh >> (2 * l)) & 1u) << 8);
-        uint32_t i1 = ((qsw >> (16 * (l & 1) + 8)) & 0xFFu) | (((qh >> (2 * l + 1)) & 1u) << 8);
-        uint32_t sb = (sg >> (8 * l)) & 0xFFu;
-        uint32_t m0 = nib_mask(sb & 0xFu), m1 = nib_mask(sb >> 4);
+        const uint32_t qsw = l < 2 ? qs0 : qs1;
+        const uint32_t i0 = ((qsw >> (16 * (l & 1))) & 0xFFu) | (((qh >> (2 * l)) & 1u) << 8);
+        const uint32_t i1 = ((qsw >> (16 * (l & 1) + 8)) & 0xFFu) | (((qh >> (2 * l + 1)) & 1u) << 8);
+        const uint32_t sb = (sg >> (8 * l)) & 0xFFu;
+        const uint32_t m0 = nib_mask(sb & 0xFu), m1 = nib_mask(sb >> 4);
         // signed levels: (g ^ m) + (m & 1): per-byte negation, no carry since g >= 1
-        uint32_t v0 = (grid[i0] ^ m0) + (m0 & 0x01010101u);
-        uint32_t v1 = (grid[i1] ^ m1) + (m1 & 0x01010101u);
+        const uint32_t v0 = (grid[i0] ^ m0) + (m0 & 0x01010101u);
+        const uint32_t v1 = (grid[i1] ^ m1) + (m1 & 0x01010101u);
         s = dot4((int)v0, x.q[2 * l], s);
         s = dot4((int)v1, x.q[2 * l + 1], s);
     }
     return s * mult;
 }
+
+__device__ __forceinline__ int dot_q8_0(const uint8_t* row, int off, const XBlk& x, float* dw) {
+    uint32_t q[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) q[i] = lds_u32(row, off + 2 + 4 * i);
+    return dot_q8_0_core(lds_u16(row, off), q, x, dw);
+}
+
+__device__ __forceinline__ int dot_q4_0(const uint8_t* row, int off, const XBlk& x, float* dw) {
+    uint32_t qs[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) qs[i] = lds_u32(row, off + 2 + 4 * i);
+    return dot_q4_0_core(lds_u16(row, off), qs, x, dw);
+}
+
+__device__ __forceinline__ int dot_iq3_s(const uint8_t* row, int off, int ib, const XBlk& x,
+                                         const uint32_t* grid, float* dw) {
+    const uint32_t sc = row[off + 106 + (ib >> 1)];
+    return dot_iq3_s_core(lds_u16(row, off), lds_u32(row, off + 2 + 8 * ib), lds_u32(row, off + 6 + 8 * ib),
+                          row[off + 66 + ib], lds_u32(row, off + 74 + 4 * ib), (sc >> (4 * (ib & 1))) & 0xFu, x,
+                          grid, dw);
+}
+
+// One weight block held in registers (read straight from global memory with
+// 2-byte loads, so no access leaves the block), decoded on use.
+template <int T> struct RegBlk;
+template <> struct RegBlk<T_Q4_0> {
+    uint32_t d, qs[4];
+    __device__ __forceinline__ void load(const uint8_t* blk) {   // 18-byte block
+        const uint16_t* h = (const uint16_t*)blk;
+        d = h[0];
+#pragma unroll
+        for (int i = 0; i < 4; i++) qs[i] = (uint32_t)h[1 + 2 * i] | ((uint32_t)h[2 + 2 * i] << 16);
+    }
+    __device__ __forceinline__ int dot(const XBlk& x, const uint32_t*, float* dw) const {
+        return dot_q4_0_core(d, qs, x, dw);
+    }
+};
+template <> struct RegBlk<T_Q8_0> {
+    uint32_t d, q[8];
+    __device__ __forceinline__ void load(const uint8_t* blk) {   // 34-byte block
+        const uint16_t* h = (const uint16_t*)blk;
+        d = h[0];
+#pragma unroll
+        for (int i = 0; i < 8; i++) q[i] = (uint32_t)h[1 + 2 * i] | ((uint32_t)h[2 + 2 * i] << 16);
+    }
+    __device__ __forceinline__ int dot(const XBlk& x, const uint32_t*, float* dw) const {
+        return dot_q8_0_core(d, q, x, dw);
+    }
+};
+template <> struct RegBlk<T_IQ3_S> {
+    uint32_t d, qs0, qs1, qh, sg, nib;
+    // sub-block ib of the 110-byte superblock at sb
+    __device__ __forceinline__ void load(const uint8_t* sb, int ib) {
+        const uint16_t* h = (const uint16_t*)sb;
+        d = h[0];
+        qs0 = (uint32_t)h[1 + 4 * ib] | ((uint32_t)h[2 + 4 * ib] << 16);
+        qs1 = (uint32_t)h[3 + 4 * ib] | ((uint32_t)h[4 + 4 * ib] << 16);
+        qh = sb[66 + ib];
+        sg = (uint32_t)h[37 + 2 * ib] | ((uint32_t)h[38 + 2 * ib] << 16);
+        nib = (sb[106 + (ib >> 1)] >> (4 * (ib & 1))) & 0xFu;
+    }
+    __device__ __forceinline__ int dot(const XBlk& x, const uint32_t* grid, float* dw) const {
+        return dot_iq3_s_core(d, qs0, qs1, qh, sg, nib, x, grid, dw);
+    }
+};
 
 // Block b (32-element unit; IQ3_S: sub-block) of a row chunk held in LDS.
 template <int T>

@@ -9,16 +9,16 @@
 //   K1 k_moe_route    one work-group per router row (+1 for the shared-expert
 //                     gate vector) computing f32 logits for every token, plus
 //                     one work-group per token quantizing x to Q8_1.
-//   K2 k_moe_gate_up  (32-row block of F) x (distinct expert | shared).  Each
-//                     routed work-group recomputes softmax/top-k (one wave per
-//                     token, registers only) and the distinct-expert plan from
-//                     the 1 KB of logits, then streams 32 gate + 32 up rows of
-//                     its expert once for all tokens routed to it and writes
-//                     the block of h = silu(gate)*up Q8_1-quantized.
-//   K3 k_moe_down     16 hidden rows per work-group over all selected experts
-//                     (tiles of several experts staged together with their
-//                     Q8_1 intermediates), then the router-weighted sum in k
-//                     order plus the shared expert.
+//   K2 k_moe_expert   (distinct expert | shared) x (32-row block w of F).
+//                     Each routed work-group recomputes softmax/top-k (one wave
+//                     per token, registers only) and the distinct-expert plan
+//                     from the logits, then streams 32 gate + 32 up rows and
+//                     the block-w column slice of the down matrix together,
+//                     once for all tokens routed to the expert, computes
+//                     Q8_1(h) for its block and the exact down terms.
+//   K3 k_moe_combine  replays the down dots' fp32 order from the terms, then
+//                     the router-weighted sum in k order plus the shared
+//                     expert.
 // Every row dot uses the (L=16, G=1) order of tile_gemv.h.
 #include "api_internal.h"
 #include "common.h"
@@ -44,8 +44,7 @@ __constant__ uint32_t c_iq3s_grid_moe[512] = CHIMERE_IQ3S_GRID_INIT;
 
 constexpr int MAX_TOK = 8;
 constexpr int MAX_K = 16;
-constexpr int MAX_E = 1024;        // standalone top-k
-constexpr int MAX_E_FUSED = 256;   // fused MoE layer (one logit per thread of a 256-thread group)
+constexpr int MAX_E = 1024;
 
 // ------------------------------------------------------------ reductions
 
@@ -148,6 +147,7 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ logits, int 
         key[i] = j < E ? (((uint64_t)__builtin_bit_cast(uint32_t, p[i])) << 11) | (uint64_t)(1024 - j) : 0;
     }
     // radix select of the K-th largest key (p <= 1, so the f32 bits fit in 30 bits)
+    // (stops as soon as exactly K keys reach the candidate: the set is fixed then)
     uint64_t T = 0;
     for (int b = 40; b >= 0; b--) {
         const uint64_t cand = T | (1ull << b);
@@ -155,6 +155,7 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ logits, int 
 #pragma unroll
         for (int i = 0; i < NV; i++) cnt += __popcll(__ballot(key[i] >= cand));
         if (cnt >= K) T = cand;
+        if (cnt == K) break;
     }
     // rank each selected entry: rank = number of keys larger than it
     int my_idx = 0;
@@ -190,89 +191,6 @@ __device__ __forceinline__ void topk_wave_any(const float* logits, int E, int K,
     else if (E <= 256) topk_wave<4>(logits, E, K, idx, w);
     else if (E <= 512) topk_wave<8>(logits, E, K, idx, w);
     else topk_wave<16>(logits, E, K, idx, w);
-}
-
-// Softmax + top-k of one logits row (E <= 256) by a 256-thread group, with
-// low dependent depth.  Thread i owns logit i (padding i >= E).  max: wave
-// DPP butterflies + LDS; sum: the reference's strided halving tree (strides
-// 128 and 64 through LDS, 32..1 by xor exchanges, which equal the tree at
-// lane 0); p = ev / sum.  Selection: a bitonic sort, descending, of the
-// 41-bit keys (f32 bits of p << 11 | 1024 - index) -- the same set and order
-// as k rounds of arg-max with ties to the lowest index; strides >= 64 go
-// through LDS, smaller ones are in-wave DPP / permlane exchanges.  The first
-// K threads of the group then hold the result; weights are renormalised by
-// the sequential sum of the selected probabilities.  `scr` is LDS scratch of
-// 256 uint64 + 8 floats for this group; every thread of the work-group must
-// call this the same number of times (it contains __syncthreads()).
-__device__ __forceinline__ uint64_t xlane64(uint64_t v, int m) {
-    uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-    switch (m) {
-    case 1: lo = xlane<1>((int)lo); hi = xlane<1>((int)hi); break;
-    case 2: lo = xlane<2>((int)lo); hi = xlane<2>((int)hi); break;
-    case 4: lo = xlane<4>((int)lo); hi = xlane<4>((int)hi); break;
-    case 8: lo = xlane<8>((int)lo); hi = xlane<8>((int)hi); break;
-    case 16: lo = xlane<16>((int)lo); hi = xlane<16>((int)hi); break;
-    default: lo = xlane<32>((int)lo); hi = xlane<32>((int)hi); break;
-    }
-    return ((uint64_t)hi << 32) | lo;
-}
-
-__device__ void topk_block256(const float* __restrict__ logits, int E, int K, bool active, int* idx_out,
-                              float* w_out, uint64_t* scr) {
-    const int i = threadIdx.x & 255;
-    const int wv = i >> 6;
-    float* fs = (float*)(scr + 256);
-    const float l = (active && i < E) ? logits[i] : -__builtin_huge_valf();
-    float m = bfly32_max(__builtin_fmaxf(l, xlane<32>(l)));
-    if ((i & 63) == 0) fs[wv] = m;
-    __syncthreads();
-    m = __builtin_fmaxf(__builtin_fmaxf(fs[0], fs[1]), __builtin_fmaxf(fs[2], fs[3]));
-    const float ev = (active && i < E) ? det_exp(l - m) : 0.0f;
-    float* ps = (float*)scr;
-    ps[i] = ev;
-    __syncthreads();
-    if (i < 128) ps[i] = ps[i] + ps[i + 128];
-    __syncthreads();
-    float sum = 0.0f;
-    if (i < 64) {
-        float v = ps[i] + ps[i + 64];
-        v = v + xlane<32>(v);
-        sum = bfly32_sum(v);
-        if (i == 0) fs[4] = sum;
-    }
-    __syncthreads();
-    sum = fs[4];
-    const float p = sum > 0.0f ? ev / sum : 1.0f / (float)E;
-    uint64_t key = (active && i < E) ? (((uint64_t)__builtin_bit_cast(uint32_t, p)) << 11) | (uint64_t)(1024 - i) : 0;
-    __syncthreads();   // ps (aliases scr) is free again
-    for (int k = 2; k <= 256; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            uint64_t other;
-            if (j >= 64) {
-                scr[i] = key;
-                __syncthreads();
-                other = scr[i ^ j];
-                __syncthreads();
-            } else {
-                other = xlane64(key, j);
-            }
-            const bool lower = (i & j) == 0;
-            const bool desc = (i & k) == 0 || k == 256;
-            const uint64_t mx = key > other ? key : other, mn = key > other ? other : key;
-            key = (lower == desc) ? mx : mn;
-        }
-    }
-    // threads 0..K-1 (wave 0 of the group) hold the K largest keys in order
-    const uint32_t pb = (uint32_t)(key >> 11);
-    const float pv = __builtin_bit_cast(float, pb);
-    float ws = 0.0f;
-    if (wv == 0) {
-        for (int k = 0; k < K; k++) ws += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pv), k));
-    }
-    if (active && i < K) {
-        idx_out[i] = 1024 - (int)(key & 0x7FF);
-        w_out[i] = ws > 0.0f ? pv * (1.0f / ws) : pv;
-    }
 }
 
 // Q8_1 quantization of `nblk` 32-blocks (ggml semantics, see quant.hip) by a
@@ -312,8 +230,8 @@ struct MoeArgs {
     float* wts;         // [M*K]
     int* plan;          // n_unique, uexp[128], u_ntok[128], u_pair[128][MAX_TOK]
     uint8_t* xq;        // [M][xq_stride]   Q8_1(x)
-    uint8_t* hq;        // [M*K + M][hq_stride]   Q8_1(h) per (token, k) pair and shared
-    int64_t xq_stride, hq_stride;
+    uint2* terms;       // [M*K + M][H][F/32]  down block terms (f32 scale bits, int32 sumi)
+    int64_t xq_stride;
     uint64_t* phase;    // debug timestamps (CHIMERE_PHASE_TIMING builds)
 };
 
@@ -361,54 +279,96 @@ __global__ __launch_bounds__(256) void k_moe_route(MoeArgs a) {
     PHASE(0, 1);
 }
 
-constexpr int GU_RG = 64;                  // K2 row groups: 1024 threads
-constexpr int GU_THREADS = GU_RG * SLOTS;
+constexpr int EX_RG = 64;                    // K2 row groups: 1024 threads
+constexpr int EX_THREADS = EX_RG * SLOTS;
+constexpr int EX_MAX_RPT = 4;                // down rows per thread: H <= 4096
 
-// K2: grid (F/32, M*K + 1), 1024 threads.  Every routed work-group recomputes
-// the routing (top-k per token, one wave each) and the distinct-expert plan
-// from the logits, so no work-group waits on another; blockIdx.y < n_unique
-// selects a distinct expert, blockIdx.y == M*K the shared expert.  Work-group
-// (0,0) publishes routing and plan for K3.  A tile holds 32 gate + 32 up rows
-// (group g < 32 computes gate row g, group 32 + g up row g), so the
-// work-group owns whole 32-row blocks of h = silu(gate) * up and writes them
-// Q8_1-quantized.
+// Loads, for the down rows of this thread, the weight block w (32 columns of
+// F) of expert matrix `down` (row stride rbF).
+template <int T>
+__device__ __forceinline__ void load_down_blocks(RegBlk<T> (&rb)[EX_MAX_RPT], const uint8_t* down, int64_t rbF,
+                                                 int w, int H) {
+#pragma unroll
+    for (int k = 0; k < EX_MAX_RPT; k++) {
+        const int r = threadIdx.x + EX_THREADS * k;
+        if (r < H) {
+            const uint8_t* rowp = down + (int64_t)r * rbF;
+            if constexpr (T == T_IQ3_S) rb[k].load(rowp + (w >> 3) * 110, w & 7);
+            else rb[k].load(rowp + w * QTraits<T>::BYTES);
+        }
+    }
+}
+
+// Exact down-projection terms of block w for the thread's rows and every
+// token of the unit: terms[pair][r][w] = (f32(d_w) * f32(d_h), sumi).
+template <int T>
+__device__ __forceinline__ void down_terms(const RegBlk<T> (&rb)[EX_MAX_RPT], const XLds* hx, const int* pairs,
+                                           int ntok, const uint32_t* grid, uint2* terms, int H, int NB, int w) {
+#pragma unroll
+    for (int k = 0; k < EX_MAX_RPT; k++) {
+        const int r = threadIdx.x + EX_THREADS * k;
+        if (r < H) {
+            for (int t = 0; t < ntok; t++) {
+                XBlk xb;
+                xlds_to_blk(hx[t], xb);
+                float dw;
+                const int s = rb[k].dot(xb, grid, &dw);
+                terms[((int64_t)pairs[t] * H + r) * NB + w] =
+                    make_uint2(__builtin_bit_cast(uint32_t, dw * xb.d), (uint32_t)s);
+            }
+        }
+    }
+}
+
+// K2: one work-group per (unit, w): unit = a distinct selected expert (or the
+// shared expert), w = a 32-row block of its F dimension.  1024 threads.
+//  1. Routing: waves 0..M-1 each run softmax/top-k for one token from the
+//     logits (registers only); thread 0 builds the distinct-expert plan.  No
+//     work-group waits on another: each recomputes it; work-group (0,0)
+//     publishes weights and plan for K3.
+//  2. Issues, together: the 32 gate + 32 up rows of block w (HBM -> LDS,
+//     asynchronous) and the block-w column slice of the down matrix (one
+//     weight block per down row, into registers).
+//  3. gate/up dots (group g < 32: gate row g, 32 + g: up row g), h =
+//     silu(gate)*up, Q8_1(h) for the 32-row block (ggml semantics).
+//  4. Exact down terms of block w for every down row (the L=16 order needs
+//     only these per-block (scale, sumi) pairs; K3 replays the order).
+// Work-groups are laid out so that the NB blocks of one unit run on one XCD
+// (work-group ids are dealt round-robin to the 8 XCDs), so the down slices
+// of an expert share that XCD's L2.
 template <int TE, int TS>
-__global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
+__global__ __launch_bounds__(EX_THREADS) void k_moe_expert(MoeArgs a) {
     constexpr int CBE = ChunkGeom<TE>::BYTES, CBS = ChunkGeom<TS>::BYTES;
     constexpr int CB = CBE > CBS ? CBE : CBS;
-    // the tile buffer first holds the expert map and the plan (routing phase)
-    constexpr int ROUTE_BYTES = MAX_E_FUSED * 4 + (int)sizeof(Plan) + 4 * (256 + 32) * 8;
-    constexpr int TILE_BYTES = GU_RG * CB + 16 > ROUTE_BYTES ? GU_RG * CB + 16 : ROUTE_BYTES;
+    constexpr int ROUTE_BYTES = MAX_E * 4 + (int)sizeof(Plan);
+    constexpr int TILE_BYTES = EX_RG * CB + 16 > ROUTE_BYTES ? EX_RG * CB + 16 : ROUTE_BYTES;
     __shared__ __attribute__((aligned(16))) uint8_t tile[TILE_BYTES];
     __shared__ XLds xs[MAX_TOK][MAX_CHUNK_BLOCKS];
     __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
     __shared__ float hg[MAX_TOK][QK], hu[MAX_TOK][QK];
+    __shared__ XLds hx[MAX_TOK];
     __shared__ int toks[MAX_TOK], pairs[MAX_TOK];
     __shared__ int s_ids[MAX_TOK * MAX_K];
     __shared__ float s_w[MAX_TOK * MAX_K];
-    Plan& pl = *(Plan*)(tile + MAX_E_FUSED * 4);
-    uint64_t* tscr = (uint64_t*)(tile + MAX_E_FUSED * 4 + sizeof(Plan));
+    Plan& pl = *(Plan*)(tile + MAX_E * 4);
 
-    const int u = blockIdx.y;
-    const bool shared = u == a.M * a.K;
+    const int NB = a.F / QK;
+    const int L = blockIdx.x, xcd = L & 7, li = L >> 3;
+    const int u = xcd + 8 * (li / NB), w = li % NB;
     const int tid = threadIdx.x;
-    PHASE(1, 0);
+    if (u > a.M * a.K) return;
+    const bool shared = u == a.M * a.K;
     if (shared && !a.has_shared) return;
+    PHASE(1, 0);
     int ntok;
     if (shared) {
         ntok = a.M;
         if (tid < a.M) { toks[tid] = tid; pairs[tid] = a.M * a.K + tid; }
     } else {
-        const int grp = tid >> 8;   // four 256-thread groups, one token each per pass
-        for (int t0 = 0; t0 < a.M; t0 += GU_THREADS / 256) {
-            const int t = t0 + grp;
-            const bool act = t < a.M;
-            topk_block256(a.logits + (act ? t : 0) * a.E, a.E, a.K, act, s_ids + (act ? t : 0) * a.K,
-                          s_w + (act ? t : 0) * a.K, tscr + grp * (256 + 32));
-        }
-        __syncthreads();
+        const int wave = tid >> 6;
+        if (wave < a.M) topk_wave_any(a.logits + wave * a.E, a.E, a.K, s_ids + wave * a.K, s_w + wave * a.K);
         int* map = (int*)tile;
-        for (int e = tid; e < a.E; e += GU_THREADS) map[e] = -1;
+        for (int e = tid; e < a.E; e += EX_THREADS) map[e] = -1;
         __syncthreads();
         PHASE(1, 1);
         if (tid == 0) {
@@ -425,15 +385,15 @@ __global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
             pl.nu = nu;
         }
         __syncthreads();
-        if (blockIdx.x == 0 && u == 0) {
+        if (u == 0 && w == 0) {
             const int nu = pl.nu;
-            for (int i = tid; i < a.M * a.K; i += GU_THREADS) {
+            for (int i = tid; i < a.M * a.K; i += EX_THREADS) {
                 a.wts[i] = s_w[i];
                 if (a.ids_out) { a.ids_out[i] = s_ids[i]; a.w_out[i] = s_w[i]; }
             }
             int* P = a.plan;
             if (tid == 0) P[0] = nu;
-            for (int i = tid; i < nu; i += GU_THREADS) {
+            for (int i = tid; i < nu; i += EX_THREADS) {
                 P[PLAN_UEXP + i] = pl.uexp[i];
                 P[PLAN_UNTOK + i] = pl.untok[i];
                 for (int n = 0; n < pl.untok[i]; n++) P[PLAN_UPAIR + i * MAX_TOK + n] = pl.upair[i][n];
@@ -444,20 +404,24 @@ __global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
         if (tid < ntok) { toks[tid] = pl.utok[u][tid]; pairs[tid] = pl.upair[u][tid]; }
     }
     if constexpr (TE == T_IQ3_S || TS == T_IQ3_S)
-        for (int i = tid; i < 512; i += GU_THREADS) grid[i] = c_iq3s_grid_moe[i];
+        for (int i = tid; i < 512; i += EX_THREADS) grid[i] = c_iq3s_grid_moe[i];
     PHASE(1, 2);
-    const int r0 = blockIdx.x * QK;
+    const int r0 = w * QK;
+    const int64_t e = shared ? 0 : pl.uexp[u];
+    RegBlk<TE> dbE[EX_MAX_RPT];
+    RegBlk<TS> dbS[EX_MAX_RPT];
     float acc[1][MAX_TOK];
     if (shared) {
+        load_down_blocks<TS>(dbS, a.sh_down, row_bytes(TS, a.F), w, a.H);
         const int64_t rb = row_bytes(TS, a.H);
-        tile_gemv<TS, MAX_TOK, GU_RG, 1>(tile, xs, grid, a.sh_gate + r0 * rb, QK, a.sh_up + r0 * rb, QK, rb,
+        tile_gemv<TS, MAX_TOK, EX_RG, 1>(tile, xs, grid, a.sh_gate + r0 * rb, QK, a.sh_up + r0 * rb, QK, rb,
                                          a.H, a.xq, a.xq_stride, toks, ntok, acc);
     } else {
+        load_down_blocks<TE>(dbE, a.down + e * a.sd, row_bytes(TE, a.F), w, a.H);
         const int64_t rb = row_bytes(TE, a.H);
-        const int64_t e = pl.uexp[u];
-        tile_gemv<TE, MAX_TOK, GU_RG, 1>(tile, xs, grid, a.gate + e * a.sg + r0 * rb, QK,
-                                         a.up + e * a.su + r0 * rb, QK, rb, a.H, a.xq, a.xq_stride, toks,
-                                         ntok, acc);
+        tile_gemv<TE, MAX_TOK, EX_RG, 1>(tile, xs, grid, a.gate + e * a.sg + r0 * rb, QK,
+                                         a.up + e * a.su + r0 * rb, QK, rb, a.H, a.xq, a.xq_stride, toks, ntok,
+                                         acc);
     }
     PHASE(1, 3);
     const int g = tid >> 4, j = tid & 15;
@@ -472,166 +436,103 @@ __global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
         }
     }
     __syncthreads();
-    // one half-wave per token quantizes the 32-row block of h (ggml Q8_1)
+    // one half-wave per token: Q8_1 of the 32-row block of h (ggml semantics),
+    // kept decoded in LDS for the down terms
     if ((tid >> 5) < ntok) {
         const int t = tid >> 5, i = tid & 31;
         const float xi = det_silu(hg[t][i]) * hu[t][i];
-        const float amax = bfly32_max(__builtin_fabsf(xi)), sum = bfly32_sum(xi);
+        const float amax = bfly32_max(__builtin_fabsf(xi));
         const float d = amax / 127.0f;
         const int q = amax == 0.0f ? 0 : (int)__builtin_roundf(xi / d);
-        uint8_t* o = a.hq + (int64_t)pairs[t] * a.hq_stride + blockIdx.x * Q8_1_BYTES;
-        o[4 + i] = (uint8_t)(int8_t)q;
-        if (i == 0) *(uint32_t*)o = f2h(d) | (f2h(sum) << 16);
+        const int byte = (q & 0xFF) << (8 * (i & 3));
+        int word = byte | xlane<1>(byte);
+        word = word | xlane<2>(word);
+        int sq = q + xlane<16>(q);
+        sq = sq + xlane<8>(sq);
+        sq = sq + xlane<4>(sq);
+        sq = sq + xlane<2>(sq);
+        sq = sq + xlane<1>(sq);
+        if ((i & 3) == 0) hx[t].q[i >> 2] = word;
+        if (i == 0) { hx[t].d = h2f(f2h(d)); hx[t].sumq = sq; }
     }
+    __syncthreads();
+    if (shared) down_terms<TS>(dbS, hx, pairs, ntok, grid, a.terms, a.H, NB, w);
+    else down_terms<TE>(dbE, hx, pairs, ntok, grid, a.terms, a.H, NB, w);
     PHASE(1, 4);
 }
 
-// Down-projection rows of one expert tile (in LDS) for its pairs, with the
-// pairs' Q8_1 intermediates decoded in LDS (xl[p][block]); writes
-// dn[pair][row] for the tile's rows.
-template <int T>
-__device__ __forceinline__ void down_tile(const uint8_t* tile, int lstride, const uint32_t* grid,
-                                          const XLds* xl, int nbF, const int* pairs, int np, int nr,
-                                          float (*dn)[TILE_ROWS]) {
-    const int tid = threadIdx.x, g = tid >> 4, j = tid & 15;
-    const uint8_t* row = tile + g * lstride;
-    for (int p = 0; p < np; p++) {
-        float acc = 0.0f;
-        if (g < nr) {
-            for (int b = j; b < nbF; b += SLOTS) {
-                XBlk xb;
-                xlds_to_blk(xl[p * nbF + b], xb);
-                float dw;
-                const int s = block_dot<T>(row, b, xb, grid, &dw);
-                acc = __builtin_fmaf(dw * xb.d, (float)s, acc);
-            }
-            const float v = slot_reduce16(acc);
-            if (j == 0) dn[pairs[p]][g] = v;
-        }
-    }
-}
+// K3: grid (ceil(H/16)), 256 threads: 16 down rows per work-group, 16 lanes
+// per row.  Lane j replays the L=16 order for every (token, k) pair from the
+// exact block terms (acc = fmaf(scale_b, sumi_b, acc) over b = j, j+16, ...,
+// then the halving tree), then the router-weighted sum in k order plus the
+// shared expert.
+constexpr int CMB_CHUNK = 8;    // pairs whose terms are loaded together
 
-constexpr int DOWN_LDS = 96 * 1024;
-
-// K3: grid (ceil(H/16)), 256 threads.  Stages the down tiles of a batch of
-// experts together with their pairs' Q8_1 intermediates (decoded into LDS),
-// computes, then combines in k order plus the shared expert.
-template <int TE, int TS>
-__global__ __launch_bounds__(GEMV_THREADS) void k_moe_down(MoeArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t buf[DOWN_LDS + 16];
-    __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
-    __shared__ float dn[MAX_TOK * MAX_K + MAX_TOK][TILE_ROWS];
-    __shared__ int pl[MAX_TOK * MAX_K + 1][MAX_TOK];
-    __shared__ int np[MAX_TOK * MAX_K + 1];
-    __shared__ int wexp[MAX_TOK * MAX_K + 1];
-    __shared__ int boff[MAX_TOK * MAX_K + 1], xoff[MAX_TOK * MAX_K + 1];
-
-    const int tid = threadIdx.x;
+__global__ __launch_bounds__(GEMV_THREADS) void k_moe_combine(MoeArgs a) {
+    __shared__ float s_w[MAX_TOK * MAX_K];
+    __shared__ float s_g[MAX_TOK];
+    __shared__ float dn[TILE_ROWS][MAX_TOK * MAX_K + MAX_TOK];
     PHASE(2, 0);
-    const int r0 = blockIdx.x * TILE_ROWS;
-    const int nr = min(TILE_ROWS, a.H - r0);
-    const int* P = a.plan;
-    const int nu = P[0];
-    const int nw = nu + (a.has_shared ? 1 : 0);
-    const int nbF = a.F / QK;
-    if constexpr (TE == T_IQ3_S || TS == T_IQ3_S)
-        for (int i = tid; i < 512; i += GEMV_THREADS) grid[i] = c_iq3s_grid_moe[i];
-    for (int w = tid; w < nw; w += GEMV_THREADS) {
-        if (w < nu) {
-            wexp[w] = P[PLAN_UEXP + w];
-            np[w] = P[PLAN_UNTOK + w];
-            for (int i = 0; i < np[w]; i++) pl[w][i] = P[PLAN_UPAIR + w * MAX_TOK + i];
-        } else {
-            wexp[w] = -1;
-            np[w] = a.M;
-            for (int i = 0; i < a.M; i++) pl[w][i] = a.M * a.K + i;
+    const int tid = threadIdx.x;
+    const int rr = tid >> 4, j = tid & 15;
+    const int r = blockIdx.x * TILE_ROWS + rr;
+    const int NB = a.F / QK;
+    const int MK = a.M * a.K;
+    for (int i = tid; i < MK; i += GEMV_THREADS) s_w[i] = a.wts[i];
+    if (tid < a.M) s_g[tid] = a.sh_gate_w ? a.glogit[tid] : 0.0f;
+    const int np = MK + (a.has_shared ? a.M : 0);
+    if (r < a.H) {
+        for (int p0 = 0; p0 < np; p0 += CMB_CHUNK) {
+            // issue every term load of the chunk before using any
+            uint2 tv[CMB_CHUNK][EX_MAX_RPT];
+#pragma unroll
+            for (int c = 0; c < CMB_CHUNK; c++)
+#pragma unroll
+                for (int q = 0; q < EX_MAX_RPT; q++) {
+                    const int b = j + SLOTS * q;
+                    tv[c][q] = (p0 + c < np && b < NB) ? a.terms[((int64_t)(p0 + c) * a.H + r) * NB + b]
+                                                       : make_uint2(0, 0);
+                }
+#pragma unroll
+            for (int c = 0; c < CMB_CHUNK; c++) {
+                if (p0 + c < np) {
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < EX_MAX_RPT; q++)
+                        if (j + SLOTS * q < NB)
+                            acc = __builtin_fmaf(__builtin_bit_cast(float, tv[c][q].x), (float)(int)tv[c][q].y, acc);
+                    const float v = slot_reduce16(acc);
+                    if (j == 0) dn[rr][p0 + c] = v;
+                }
+            }
         }
     }
     __syncthreads();
     PHASE(2, 1);
-    const int64_t rbE = row_bytes(TE, a.F), rbS = row_bytes(TS, a.F);
-    const int lsE = (int)rbE, lsS = (int)rbS;   // tiles packed with the row stride
-    int w0 = 0;
-    while (w0 < nw) {
-        // a batch of work experts whose tiles and decoded intermediates fit in LDS
-        int w1 = w0, used = 0;
-        while (w1 < nw) {
-            const int need = ((TILE_ROWS * ((w1 < nu) ? lsE : lsS) + 15) & ~15) + np[w1] * nbF * (int)sizeof(XLds);
-            if (used + need > DOWN_LDS && w1 > w0) break;
-            used += need;
-            w1++;
-        }
-        {
-            int o = 0;
-            for (int w = w0; w < w1; w++) { if (tid == 0) boff[w] = o; o += (TILE_ROWS * ((w < nu) ? lsE : lsS) + 15) & ~15; }
-            for (int w = w0; w < w1; w++) { if (tid == 0) xoff[w] = o; o += np[w] * nbF * (int)sizeof(XLds); }
-        }
-        __syncthreads();
-        for (int w = w0; w < w1; w++) {
-            if (w < nu)
-                stage_rows(buf + boff[w], a.down + (int64_t)wexp[w] * a.sd + (int64_t)r0 * rbE, rbE, nr, (int)rbE,
-                           tid, GEMV_THREADS);
-            else
-                stage_rows(buf + boff[w], a.sh_down + (int64_t)r0 * rbS, rbS, nr, (int)rbS, tid, GEMV_THREADS);
-        }
-        // decode every pair's Q8_1 intermediate of the batch in one parallel pass
-        // (xoff of consecutive work experts is contiguous, so block i of the batch
-        // lands at xoff[w0] + i)
-        {
-            int tot = 0;
-            for (int w = w0; w < w1; w++) tot += np[w] * nbF;
-            XLds* xl = (XLds*)(buf + xoff[w0]);
-            for (int i = tid; i < tot; i += GEMV_THREADS) {
-                int w = w0, r = i;
-                while (r >= np[w] * nbF) { r -= np[w] * nbF; w++; }
-                XBlk xb;
-                load_xblk(a.hq + (int64_t)pl[w][r / nbF] * a.hq_stride + (int64_t)(r % nbF) * Q8_1_BYTES, xb);
-#pragma unroll
-                for (int k = 0; k < 8; k++) xl[i].q[k] = xb.q[k];
-                xl[i].d = xb.d;
-                xl[i].sumq = xb.sumq;
-            }
-        }
-        PHASE(2, 2);
-        lds_copy_wait();
-        __syncthreads();
-        PHASE(2, 3);
-        for (int w = w0; w < w1; w++) {
-            const XLds* xl = (const XLds*)(buf + xoff[w]);
-            if (w < nu) down_tile<TE>(buf + boff[w], lsE, grid, xl, nbF, pl[w], np[w], nr, dn);
-            else down_tile<TS>(buf + boff[w], lsS, grid, xl, nbF, pl[w], np[w], nr, dn);
-        }
-        __syncthreads();
-        PHASE(2, 4);
-        w0 = w1;
-    }
-    // combine: acc = sum_k fmaf(w_k, dn_k, acc); out = fmaf(shared, sigmoid(g), acc)
-    if (tid < a.M * TILE_ROWS) {
-        const int t = tid / TILE_ROWS, r = tid % TILE_ROWS;
-        if (r < nr) {
+    // combine: one thread per (row, token)
+    if (tid < TILE_ROWS * a.M) {
+        const int row = tid % TILE_ROWS, t = tid / TILE_ROWS;
+        const int rg = blockIdx.x * TILE_ROWS + row;
+        if (rg < a.H) {
             float acc = 0.0f;
-            for (int k = 0; k < a.K; k++) acc = __builtin_fmaf(a.wts[t * a.K + k], dn[t * a.K + k][r], acc);
+            for (int k = 0; k < a.K; k++) acc = __builtin_fmaf(s_w[t * a.K + k], dn[row][t * a.K + k], acc);
             float o = acc;
             if (a.has_shared) {
-                const float sh = dn[a.M * a.K + t][r];
-                if (a.sh_gate_w) {
-                    const float sc = 1.0f / (1.0f + det_exp(-a.glogit[t]));
-                    o = __builtin_fmaf(sh, sc, acc);
-                } else {
-                    o = sh + acc;
-                }
+                const float sh = dn[row][MK + t];
+                if (a.sh_gate_w) o = __builtin_fmaf(sh, 1.0f / (1.0f + det_exp(-s_g[t])), acc);
+                else o = sh + acc;
             }
-            a.out[(int64_t)t * a.H + r0 + r] = o;
+            a.out[(int64_t)t * a.H + rg] = o;
         }
     }
-    PHASE(2, 5);
+    PHASE(2, 2);
 }
 
 // ------------------------------------------------------- workspace plan
 
 struct WsPlan {
-    size_t logits, glogit, wts, plan, xq, hq, phase, total;
-    int64_t xq_stride, hq_stride;
+    size_t logits, glogit, wts, plan, xq, terms, phase, total;
+    int64_t xq_stride;
 };
 
 static size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -641,13 +542,12 @@ static WsPlan plan_ws(int H, int F, int E, int K, int M) {
     size_t o = 0;
     const int P = M * K + M;
     p.xq_stride = pad_to(H, ROW_PAD) / QK * Q8_1_BYTES;
-    p.hq_stride = pad_to(F, ROW_PAD) / QK * Q8_1_BYTES;
     p.logits = o; o += al256((size_t)M * E * 4);
     p.glogit = o; o += al256((size_t)M * 4);
     p.wts = o; o += al256((size_t)M * K * 4);
     p.plan = o; o += al256((size_t)PLAN_INTS * 4);
     p.xq = o; o += al256((size_t)M * p.xq_stride);
-    p.hq = o; o += al256((size_t)P * p.hq_stride);
+    p.terms = o; o += al256((size_t)P * H * (F / QK) * 8);
 #ifdef CHIMERE_PHASE_TIMING
     p.phase = o; o += al256((size_t)3 * 4096 * 8 * 8);
 #endif
@@ -658,13 +558,13 @@ static WsPlan plan_ws(int H, int F, int E, int K, int M) {
 // stage < 0: all three kernels; 0, 1, 2: only K1, K2 or K3
 template <int TE, int TS>
 static void launch_layer(const MoeArgs& a, int stage, hipStream_t s) {
+    const int NB = a.F / QK, NU = a.M * a.K + 1;
     if (stage < 0 || stage == 0)
         hipLaunchKernelGGL(k_moe_route, dim3(a.E + (a.sh_gate_w ? 1 : 0) + a.M), dim3(256), 0, s, a);
     if (stage < 0 || stage == 1)
-        hipLaunchKernelGGL((k_moe_gate_up<TE, TS>), dim3(a.F / QK, a.M * a.K + 1), dim3(GU_THREADS), 0, s, a);
+        hipLaunchKernelGGL((k_moe_expert<TE, TS>), dim3(8 * ((NU + 7) / 8) * NB), dim3(EX_THREADS), 0, s, a);
     if (stage < 0 || stage == 2)
-        hipLaunchKernelGGL((k_moe_down<TE, TS>), dim3((a.H + TILE_ROWS - 1) / TILE_ROWS), dim3(GEMV_THREADS), 0,
-                           s, a);
+        hipLaunchKernelGGL(k_moe_combine, dim3((a.H + TILE_ROWS - 1) / TILE_ROWS), dim3(GEMV_THREADS), 0, s, a);
 }
 
 template <int TE>
@@ -749,10 +649,10 @@ static void moe_decode(const chimere_moe_layer* L, const float* x, float* out, i
     CHIMERE_REQUIRE(L && x && out && workspace, CHIMERE_ERR_ARG, "moe_ffn_decode: null pointer");
     const int H = L->hidden, F = L->ffn, E = L->n_experts, K = L->top_k;
     CHIMERE_REQUIRE(ntok >= 1 && ntok <= MAX_TOK, CHIMERE_ERR_ARG, "moe_ffn_decode: ntok=%d not in 1..8", ntok);
-    CHIMERE_REQUIRE(H > 0 && H % 256 == 0 && F > 0 && F % 256 == 0 && F <= 2048, CHIMERE_ERR_ARG,
-                    "moe_ffn_decode: hidden=%d / ffn=%d must be multiples of 256 (ffn <= 2048)", H, F);
-    CHIMERE_REQUIRE(E >= 1 && E <= MAX_E_FUSED && K >= 1 && K <= MAX_K && K <= E, CHIMERE_ERR_ARG,
-                    "moe_ffn_decode: n_experts=%d (<= 256) top_k=%d (<= 16) out of range", E, K);
+    CHIMERE_REQUIRE(H > 0 && H % 256 == 0 && H <= 4096 && F > 0 && F % 256 == 0 && F <= 2048, CHIMERE_ERR_ARG,
+                    "moe_ffn_decode: hidden=%d (<= 4096) / ffn=%d (<= 2048) must be multiples of 256", H, F);
+    CHIMERE_REQUIRE(E >= 1 && E <= MAX_E && K >= 1 && K <= MAX_K && K <= E, CHIMERE_ERR_ARG,
+                    "moe_ffn_decode: n_experts=%d top_k=%d out of range", E, K);
     CHIMERE_REQUIRE(valid_type(L->expert_type), CHIMERE_ERR_ARG, "moe_ffn_decode: expert_type %d", L->expert_type);
     const bool has_sh = L->shared_type >= 0;
     CHIMERE_REQUIRE(!has_sh || (valid_type(L->shared_type) && L->sh_gate && L->sh_up && L->sh_down),
@@ -781,8 +681,8 @@ static void moe_decode(const chimere_moe_layer* L, const float* x, float* out, i
     a.ids_out = ids_out; a.w_out = w_out;
     a.logits = (float*)(w + p.logits); a.glogit = (float*)(w + p.glogit);
     a.wts = (float*)(w + p.wts); a.plan = (int*)(w + p.plan);
-    a.xq = w + p.xq; a.hq = w + p.hq;
-    a.xq_stride = p.xq_stride; a.hq_stride = p.hq_stride;
+    a.xq = w + p.xq; a.terms = (uint2*)(w + p.terms);
+    a.xq_stride = p.xq_stride;
     a.phase = (uint64_t*)(w + p.phase);
     dispatch_layer(L->expert_type, L->shared_type, a, stage, stream);
     check_launch("moe_ffn_decode");
