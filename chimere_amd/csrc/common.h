@@ -172,47 +172,78 @@ __device__ __forceinline__ int dot_iq3_s(const uint8_t* row, int off, int ib, co
                           grid, dw);
 }
 
-// One weight block held in registers (read straight from global memory with
-// 2-byte loads, so no access leaves the block), decoded on use.
+// One weight block held in registers, read straight from global memory with
+// loads that never leave the block.  load() only issues the loads (the raw
+// words are kept as loaded, so no wait is forced there); dot() assembles the
+// fields on use.
 template <int T> struct RegBlk;
 template <> struct RegBlk<T_Q4_0> {
-    uint32_t d, qs[4];
-    __device__ __forceinline__ void load(const uint8_t* blk) {   // 18-byte block
-        const uint16_t* h = (const uint16_t*)blk;
-        d = h[0];
-#pragma unroll
-        for (int i = 0; i < 4; i++) qs[i] = (uint32_t)h[1 + 2 * i] | ((uint32_t)h[2 + 2 * i] << 16);
+    // 18-byte block at an even address: 16-byte + 2-byte loads, ordered by the
+    // block's 4-byte phase (ph = 0: [0,16) + [16,18); ph = 2: [0,2) + [2,18))
+    uint4 v;
+    uint32_t t;
+    bool ph2;
+    __device__ __forceinline__ void load(const uint8_t* blk) {
+        ph2 = ((uintptr_t)blk & 3) != 0;
+        if (!ph2) { v = *(const uint4*)blk; t = *(const uint16_t*)(blk + 16); }
+        else { t = *(const uint16_t*)blk; v = *(const uint4*)(blk + 2); }
     }
     __device__ __forceinline__ int dot(const XBlk& x, const uint32_t*, float* dw) const {
+        uint32_t d, qs[4];
+        if (!ph2) {
+            d = v.x & 0xFFFFu;
+            qs[0] = (v.x >> 16) | (v.y << 16);
+            qs[1] = (v.y >> 16) | (v.z << 16);
+            qs[2] = (v.z >> 16) | (v.w << 16);
+            qs[3] = (v.w >> 16) | (t << 16);
+        } else {
+            d = t;
+            qs[0] = v.x; qs[1] = v.y; qs[2] = v.z; qs[3] = v.w;
+        }
         return dot_q4_0_core(d, qs, x, dw);
     }
 };
 template <> struct RegBlk<T_Q8_0> {
-    uint32_t d, q[8];
-    __device__ __forceinline__ void load(const uint8_t* blk) {   // 34-byte block
-        const uint16_t* h = (const uint16_t*)blk;
-        d = h[0];
-#pragma unroll
-        for (int i = 0; i < 8; i++) q[i] = (uint32_t)h[1 + 2 * i] | ((uint32_t)h[2 + 2 * i] << 16);
+    // 34-byte block at an even address: two 16-byte loads and one 2-byte load
+    uint4 v0, v1;
+    uint32_t t;
+    bool ph2;
+    __device__ __forceinline__ void load(const uint8_t* blk) {
+        ph2 = ((uintptr_t)blk & 3) != 0;
+        if (!ph2) { v0 = *(const uint4*)blk; v1 = *(const uint4*)(blk + 16); t = *(const uint16_t*)(blk + 32); }
+        else { t = *(const uint16_t*)blk; v0 = *(const uint4*)(blk + 2); v1 = *(const uint4*)(blk + 18); }
     }
     __device__ __forceinline__ int dot(const XBlk& x, const uint32_t*, float* dw) const {
+        uint32_t d, q[8];
+        if (!ph2) {
+            const uint32_t w[9] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w, t};
+            d = w[0] & 0xFFFFu;
+#pragma unroll
+            for (int i = 0; i < 8; i++) q[i] = (w[i] >> 16) | (w[i + 1] << 16);
+        } else {
+            d = t;
+            q[0] = v0.x; q[1] = v0.y; q[2] = v0.z; q[3] = v0.w;
+            q[4] = v1.x; q[5] = v1.y; q[6] = v1.z; q[7] = v1.w;
+        }
         return dot_q8_0_core(d, q, x, dw);
     }
 };
 template <> struct RegBlk<T_IQ3_S> {
-    uint32_t d, qs0, qs1, qh, sg, nib;
-    // sub-block ib of the 110-byte superblock at sb
-    __device__ __forceinline__ void load(const uint8_t* sb, int ib) {
+    // sub-block ib of a 110-byte superblock: its fields by 2-byte / 1-byte loads
+    uint32_t d, q0, q1, q2, q3, qh, s0, s1, sc;
+    int ib;
+    __device__ __forceinline__ void load(const uint8_t* sb, int ib_) {
+        ib = ib_;
         const uint16_t* h = (const uint16_t*)sb;
         d = h[0];
-        qs0 = (uint32_t)h[1 + 4 * ib] | ((uint32_t)h[2 + 4 * ib] << 16);
-        qs1 = (uint32_t)h[3 + 4 * ib] | ((uint32_t)h[4 + 4 * ib] << 16);
+        q0 = h[1 + 4 * ib]; q1 = h[2 + 4 * ib]; q2 = h[3 + 4 * ib]; q3 = h[4 + 4 * ib];
         qh = sb[66 + ib];
-        sg = (uint32_t)h[37 + 2 * ib] | ((uint32_t)h[38 + 2 * ib] << 16);
-        nib = (sb[106 + (ib >> 1)] >> (4 * (ib & 1))) & 0xFu;
+        s0 = h[37 + 2 * ib]; s1 = h[38 + 2 * ib];
+        sc = sb[106 + (ib >> 1)];
     }
     __device__ __forceinline__ int dot(const XBlk& x, const uint32_t* grid, float* dw) const {
-        return dot_iq3_s_core(d, qs0, qs1, qh, sg, nib, x, grid, dw);
+        return dot_iq3_s_core(d, q0 | (q1 << 16), q2 | (q3 << 16), qh, s0 | (s1 << 16), (sc >> (4 * (ib & 1))) & 0xFu,
+                              x, grid, dw);
     }
 };
 

@@ -31,11 +31,13 @@
 #define PHASE(kern, i)                                                                      \
     do {                                                                                     \
         if (threadIdx.x == 0)                                                                \
-            a.phase[((kern) * 4096 + blockIdx.x + blockIdx.y * gridDim.x) * 8 + (i)] =        \
+            a.phase[((kern) * 4096 + blockIdx.x + blockIdx.y * gridDim.x) * 16 + (i)] =        \
                 __builtin_amdgcn_s_memrealtime();                                           \
     } while (0)
+#define PHASE_PTR(kern, i) (a.phase + ((kern) * 4096 + blockIdx.x + blockIdx.y * gridDim.x) * 16 + (i))
 #else
 #define PHASE(kern, i) do {} while (0)
+#define PHASE_PTR(kern, i) nullptr
 #endif
 
 namespace chimere {
@@ -230,7 +232,8 @@ struct MoeArgs {
     float* wts;         // [M*K]
     int* plan;          // n_unique, uexp[128], u_ntok[128], u_pair[128][MAX_TOK]
     uint8_t* xq;        // [M][xq_stride]   Q8_1(x)
-    uint2* terms;       // [M*K + M][H][F/32]  down block terms (f32 scale bits, int32 sumi)
+    uint2* terms;       // F > 512: [M*K + M][H][F/32]  down block terms (f32 scale bits, int32 sumi)
+    float* lane_acc;    // F <= 512: [M*K + M][H][F/32]  lane j's finished accumulator (one block per lane)
     int64_t xq_stride;
     uint64_t* phase;    // debug timestamps (CHIMERE_PHASE_TIMING builds)
 };
@@ -248,6 +251,7 @@ struct Plan {
 };
 
 // K1: grid E (router rows) + has_gate (shared-expert gate row) + M (x quantizers).
+template <int NT>
 __global__ __launch_bounds__(256) void k_moe_route(MoeArgs a) {
     __shared__ float red[256];
     PHASE(0, 0);
@@ -267,9 +271,9 @@ __global__ __launch_bounds__(256) void k_moe_route(MoeArgs a) {
             });
         return;
     }
-    float v[MAX_TOK];
+    float v[NT];
     const float* A = row < a.E ? a.router + (int64_t)row * a.H : a.sh_gate_w;
-    f32_row_dot<MAX_TOK>(A, a.x, a.H, a.M, red, v);
+    f32_row_dot<NT>(A, a.x, a.H, a.M, red, v);
     if (threadIdx.x == 0) {
         for (int t = 0; t < a.M; t++) {
             if (row < a.E) a.logits[t * a.E + row] = a.bias ? v[t] + a.bias[row] : v[t];
@@ -300,21 +304,25 @@ __device__ __forceinline__ void load_down_blocks(RegBlk<T> (&rb)[EX_MAX_RPT], co
 }
 
 // Exact down-projection terms of block w for the thread's rows and every
-// token of the unit: terms[pair][r][w] = (f32(d_w) * f32(d_h), sumi).
+// token of the unit.  F <= 512 (NB <= 16): lane w of the L=16 order owns only
+// block w, so its finished accumulator fmaf(scale, sumi, 0) is stored
+// (lane_acc[pair][r][w]); otherwise the term itself (terms[pair][r][w] =
+// (f32(d_w) * f32(d_h), sumi)) for K3 to accumulate in order.
 template <int T>
 __device__ __forceinline__ void down_terms(const RegBlk<T> (&rb)[EX_MAX_RPT], const XLds* hx, const int* pairs,
-                                           int ntok, const uint32_t* grid, uint2* terms, int H, int NB, int w) {
+                                           int ntok, const uint32_t* grid, const MoeArgs& a, int NB, int w) {
 #pragma unroll
     for (int k = 0; k < EX_MAX_RPT; k++) {
         const int r = threadIdx.x + EX_THREADS * k;
-        if (r < H) {
+        if (r < a.H) {
             for (int t = 0; t < ntok; t++) {
                 XBlk xb;
                 xlds_to_blk(hx[t], xb);
                 float dw;
                 const int s = rb[k].dot(xb, grid, &dw);
-                terms[((int64_t)pairs[t] * H + r) * NB + w] =
-                    make_uint2(__builtin_bit_cast(uint32_t, dw * xb.d), (uint32_t)s);
+                const int64_t o = ((int64_t)pairs[t] * a.H + r) * NB + w;
+                if (NB <= SLOTS) a.lane_acc[o] = __builtin_fmaf(dw * xb.d, (float)s, 0.0f);
+                else a.terms[o] = make_uint2(__builtin_bit_cast(uint32_t, dw * xb.d), (uint32_t)s);
             }
         }
     }
@@ -336,14 +344,14 @@ __device__ __forceinline__ void down_terms(const RegBlk<T> (&rb)[EX_MAX_RPT], co
 // Work-groups are laid out so that the NB blocks of one unit run on one XCD
 // (work-group ids are dealt round-robin to the 8 XCDs), so the down slices
 // of an expert share that XCD's L2.
-template <int TE, int TS>
+template <int TE, int TS, int NT>
 __global__ __launch_bounds__(EX_THREADS) void k_moe_expert(MoeArgs a) {
     constexpr int CBE = ChunkGeom<TE>::BYTES, CBS = ChunkGeom<TS>::BYTES;
     constexpr int CB = CBE > CBS ? CBE : CBS;
     constexpr int ROUTE_BYTES = MAX_E * 4 + (int)sizeof(Plan);
     constexpr int TILE_BYTES = EX_RG * CB + 16 > ROUTE_BYTES ? EX_RG * CB + 16 : ROUTE_BYTES;
     __shared__ __attribute__((aligned(16))) uint8_t tile[TILE_BYTES];
-    __shared__ XLds xs[MAX_TOK][MAX_CHUNK_BLOCKS];
+    __shared__ XLds xs[NT][MAX_CHUNK_BLOCKS];
     __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
     __shared__ float hg[MAX_TOK][QK], hu[MAX_TOK][QK];
     __shared__ XLds hx[MAX_TOK];
@@ -367,23 +375,46 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert(MoeArgs a) {
     } else {
         const int wave = tid >> 6;
         if (wave < a.M) topk_wave_any(a.logits + wave * a.E, a.E, a.K, s_ids + wave * a.K, s_w + wave * a.K);
-        int* map = (int*)tile;
-        for (int e = tid; e < a.E; e += EX_THREADS) map[e] = -1;
+        // distinct-expert plan, built in parallel: the first pair (lowest
+        // t*K+k) selecting an expert numbers it by its rank among first pairs;
+        // the order of pairs inside an expert does not affect any result.
+        int* first = (int*)tile;    // [E]: lowest pair index selecting e
+        __shared__ int s_fcnt[2], s_cnt[MAX_TOK * MAX_K];
+        for (int e = tid; e < a.E; e += EX_THREADS) first[e] = 0x7fffffff;
+        if (tid < MAX_TOK * MAX_K) s_cnt[tid] = 0;
         __syncthreads();
         PHASE(1, 1);
-        if (tid == 0) {
-            int nu = 0;
-            for (int t = 0; t < a.M; t++)
-                for (int k = 0; k < a.K; k++) {
-                    const int e = s_ids[t * a.K + k];
-                    int uu = map[e];
-                    if (uu < 0) { uu = nu++; map[e] = uu; pl.uexp[uu] = e; pl.untok[uu] = 0; }
-                    const int n = pl.untok[uu]++;
-                    pl.upair[uu][n] = t * a.K + k;
-                    pl.utok[uu][n] = t;
-                }
-            pl.nu = nu;
+        const int MK = a.M * a.K;
+        if (tid < MK) atomicMin(&first[s_ids[tid]], tid);
+        __syncthreads();
+        int fp = 0;
+        bool isfirst = false;
+        if (tid < 128) {
+            fp = tid < MK ? first[s_ids[tid]] : -1;
+            isfirst = tid < MK && fp == tid;
+            const uint64_t m = __ballot(isfirst);
+            if ((tid & 63) == 0) s_fcnt[tid >> 6] = __popcll(m);
+            const int lrank = __popcll(m & ((1ull << (tid & 63)) - 1));
+            __syncthreads();
+            const int rank = lrank + ((tid >> 6) ? s_fcnt[0] : 0);
+            if (isfirst) { pl.uexp[rank] = s_ids[tid]; s_cnt[tid] = rank; }   // s_cnt: first pair -> unit
+            if (tid == 0) pl.nu = s_fcnt[0] + (MK > 64 ? s_fcnt[1] : 0);
+        } else {
+            __syncthreads();
         }
+        __syncthreads();
+        int uu = 0;
+        if (tid < MK) uu = s_cnt[fp];
+        __syncthreads();
+        if (tid < MAX_TOK * MAX_K) s_cnt[tid] = 0;
+        __syncthreads();
+        if (tid < MK) {
+            const int n = atomicAdd(&s_cnt[uu], 1);
+            pl.upair[uu][n] = tid;
+            pl.utok[uu][n] = tid / a.K;
+        }
+        __syncthreads();
+        if (tid < pl.nu) pl.untok[tid] = s_cnt[tid];
         __syncthreads();
         if (u == 0 && w == 0) {
             const int nu = pl.nu;
@@ -410,23 +441,23 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert(MoeArgs a) {
     const int64_t e = shared ? 0 : pl.uexp[u];
     RegBlk<TE> dbE[EX_MAX_RPT];
     RegBlk<TS> dbS[EX_MAX_RPT];
-    float acc[1][MAX_TOK];
+    float acc[1][NT];
     if (shared) {
         load_down_blocks<TS>(dbS, a.sh_down, row_bytes(TS, a.F), w, a.H);
         const int64_t rb = row_bytes(TS, a.H);
-        tile_gemv<TS, MAX_TOK, EX_RG, 1>(tile, xs, grid, a.sh_gate + r0 * rb, QK, a.sh_up + r0 * rb, QK, rb,
-                                         a.H, a.xq, a.xq_stride, toks, ntok, acc);
+        tile_gemv<TS, NT, EX_RG, 1>(tile, xs, grid, a.sh_gate + r0 * rb, QK, a.sh_up + r0 * rb, QK, rb,
+                                         a.H, a.xq, a.xq_stride, toks, ntok, acc, PHASE_PTR(1, 5));
     } else {
         load_down_blocks<TE>(dbE, a.down + e * a.sd, row_bytes(TE, a.F), w, a.H);
         const int64_t rb = row_bytes(TE, a.H);
-        tile_gemv<TE, MAX_TOK, EX_RG, 1>(tile, xs, grid, a.gate + e * a.sg + r0 * rb, QK,
+        tile_gemv<TE, NT, EX_RG, 1>(tile, xs, grid, a.gate + e * a.sg + r0 * rb, QK,
                                          a.up + e * a.su + r0 * rb, QK, rb, a.H, a.xq, a.xq_stride, toks, ntok,
-                                         acc);
+                                         acc, PHASE_PTR(1, 5));
     }
     PHASE(1, 3);
     const int g = tid >> 4, j = tid & 15;
 #pragma unroll
-    for (int t = 0; t < MAX_TOK; t++) {
+    for (int t = 0; t < NT; t++) {
         if (t < ntok) {
             const float v = slot_reduce16(acc[0][t]);
             if (j == 0) {
@@ -456,8 +487,9 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert(MoeArgs a) {
         if (i == 0) { hx[t].d = h2f(f2h(d)); hx[t].sumq = sq; }
     }
     __syncthreads();
-    if (shared) down_terms<TS>(dbS, hx, pairs, ntok, grid, a.terms, a.H, NB, w);
-    else down_terms<TE>(dbE, hx, pairs, ntok, grid, a.terms, a.H, NB, w);
+    PHASE(1, 7);
+    if (shared) down_terms<TS>(dbS, hx, pairs, ntok, grid, a, NB, w);
+    else down_terms<TE>(dbE, hx, pairs, ntok, grid, a, NB, w);
     PHASE(1, 4);
 }
 
@@ -466,7 +498,7 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert(MoeArgs a) {
 // exact block terms (acc = fmaf(scale_b, sumi_b, acc) over b = j, j+16, ...,
 // then the halving tree), then the router-weighted sum in k order plus the
 // shared expert.
-constexpr int CMB_CHUNK = 8;    // pairs whose terms are loaded together
+constexpr int CMB_CHUNK = 16;   // pairs whose terms are loaded together
 
 __global__ __launch_bounds__(GEMV_THREADS) void k_moe_combine(MoeArgs a) {
     __shared__ float s_w[MAX_TOK * MAX_K];
@@ -483,25 +515,37 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_combine(MoeArgs a) {
     const int np = MK + (a.has_shared ? a.M : 0);
     if (r < a.H) {
         for (int p0 = 0; p0 < np; p0 += CMB_CHUNK) {
-            // issue every term load of the chunk before using any
-            uint2 tv[CMB_CHUNK][EX_MAX_RPT];
+            float accs[CMB_CHUNK];
+            if (NB <= SLOTS) {
+                // one block per lane: the stored value is the lane's accumulator
 #pragma unroll
-            for (int c = 0; c < CMB_CHUNK; c++)
+                for (int c = 0; c < CMB_CHUNK; c++)
+                    accs[c] = (p0 + c < np && j < NB) ? a.lane_acc[((int64_t)(p0 + c) * a.H + r) * NB + j] : 0.0f;
+            } else {
+                // issue every term load of the chunk before using any
+                uint2 tv[CMB_CHUNK][EX_MAX_RPT];
 #pragma unroll
-                for (int q = 0; q < EX_MAX_RPT; q++) {
-                    const int b = j + SLOTS * q;
-                    tv[c][q] = (p0 + c < np && b < NB) ? a.terms[((int64_t)(p0 + c) * a.H + r) * NB + b]
-                                                       : make_uint2(0, 0);
-                }
+                for (int c = 0; c < CMB_CHUNK; c++)
 #pragma unroll
-            for (int c = 0; c < CMB_CHUNK; c++) {
-                if (p0 + c < np) {
+                    for (int q = 0; q < EX_MAX_RPT; q++) {
+                        const int b = j + SLOTS * q;
+                        tv[c][q] = (p0 + c < np && b < NB) ? a.terms[((int64_t)(p0 + c) * a.H + r) * NB + b]
+                                                           : make_uint2(0, 0);
+                    }
+#pragma unroll
+                for (int c = 0; c < CMB_CHUNK; c++) {
                     float acc = 0.0f;
 #pragma unroll
                     for (int q = 0; q < EX_MAX_RPT; q++)
                         if (j + SLOTS * q < NB)
                             acc = __builtin_fmaf(__builtin_bit_cast(float, tv[c][q].x), (float)(int)tv[c][q].y, acc);
-                    const float v = slot_reduce16(acc);
+                    accs[c] = acc;
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < CMB_CHUNK; c++) {
+                if (p0 + c < np) {
+                    const float v = slot_reduce16(accs[c]);
                     if (j == 0) dn[rr][p0 + c] = v;
                 }
             }
@@ -547,24 +591,31 @@ static WsPlan plan_ws(int H, int F, int E, int K, int M) {
     p.wts = o; o += al256((size_t)M * K * 4);
     p.plan = o; o += al256((size_t)PLAN_INTS * 4);
     p.xq = o; o += al256((size_t)M * p.xq_stride);
-    p.terms = o; o += al256((size_t)P * H * (F / QK) * 8);
+    p.terms = o; o += al256((size_t)P * H * (F / QK) * (F / QK <= SLOTS ? 4 : 8));
 #ifdef CHIMERE_PHASE_TIMING
-    p.phase = o; o += al256((size_t)3 * 4096 * 8 * 8);
+    p.phase = o; o += al256((size_t)3 * 4096 * 16 * 8);
 #endif
     p.total = o;
     return p;
 }
 
 // stage < 0: all three kernels; 0, 1, 2: only K1, K2 or K3
-template <int TE, int TS>
-static void launch_layer(const MoeArgs& a, int stage, hipStream_t s) {
+template <int TE, int TS, int NT>
+static void launch_layer_nt(const MoeArgs& a, int stage, hipStream_t s) {
     const int NB = a.F / QK, NU = a.M * a.K + 1;
     if (stage < 0 || stage == 0)
-        hipLaunchKernelGGL(k_moe_route, dim3(a.E + (a.sh_gate_w ? 1 : 0) + a.M), dim3(256), 0, s, a);
+        hipLaunchKernelGGL((k_moe_route<NT>), dim3(a.E + (a.sh_gate_w ? 1 : 0) + a.M), dim3(256), 0, s, a);
     if (stage < 0 || stage == 1)
-        hipLaunchKernelGGL((k_moe_expert<TE, TS>), dim3(8 * ((NU + 7) / 8) * NB), dim3(EX_THREADS), 0, s, a);
+        hipLaunchKernelGGL((k_moe_expert<TE, TS, NT>), dim3(8 * ((NU + 7) / 8) * NB), dim3(EX_THREADS), 0, s, a);
     if (stage < 0 || stage == 2)
         hipLaunchKernelGGL(k_moe_combine, dim3((a.H + TILE_ROWS - 1) / TILE_ROWS), dim3(GEMV_THREADS), 0, s, a);
+}
+
+// one token: instantiations without the 8-token loops
+template <int TE, int TS>
+static void launch_layer(const MoeArgs& a, int stage, hipStream_t s) {
+    if (a.M == 1) launch_layer_nt<TE, TS, 1>(a, stage, s);
+    else launch_layer_nt<TE, TS, MAX_TOK>(a, stage, s);
 }
 
 template <int TE>
@@ -681,7 +732,7 @@ static void moe_decode(const chimere_moe_layer* L, const float* x, float* out, i
     a.ids_out = ids_out; a.w_out = w_out;
     a.logits = (float*)(w + p.logits); a.glogit = (float*)(w + p.glogit);
     a.wts = (float*)(w + p.wts); a.plan = (int*)(w + p.plan);
-    a.xq = w + p.xq; a.terms = (uint2*)(w + p.terms);
+    a.xq = w + p.xq; a.terms = (uint2*)(w + p.terms); a.lane_acc = (float*)(w + p.terms);
     a.xq_stride = p.xq_stride;
     a.phase = (uint64_t*)(w + p.phase);
     dispatch_layer(L->expert_type, L->shared_type, a, stage, stream);

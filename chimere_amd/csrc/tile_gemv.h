@@ -50,7 +50,7 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds (*__r
                                           const uint8_t* base1, int n1, const uint8_t* base2, int n2,
                                           int64_t rb, int ncols, const uint8_t* __restrict__ X,
                                           int64_t x_tok_stride, const int* toks, int ntok,
-                                          float (&acc)[RPG][NT]) {
+                                          float (&acc)[RPG][NT], uint64_t* ph = nullptr) {
     constexpr int CBLK = ChunkGeom<T>::BLOCKS, NTH = RG * SLOTS;
     const int tid = threadIdx.x;
     const int g = tid >> 4, j = tid & 15;
@@ -78,8 +78,14 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds (*__r
             xs[t][b].d = xb.d;
             xs[t][b].sumq = xb.sumq;
         }
+#ifdef CHIMERE_PHASE_TIMING
+        if (ph && tid == 0) ph[0] = __builtin_amdgcn_s_memrealtime();
+#endif
         lds_copy_wait();
         __syncthreads();
+#ifdef CHIMERE_PHASE_TIMING
+        if (ph && tid == 0) ph[1] = __builtin_amdgcn_s_memrealtime();
+#endif
 #pragma unroll
         for (int r = 0; r < RPG; r++) {
             const int row_i = g + RG * r;
