@@ -41,6 +41,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--pmc", action="store_true", help="light mode for rocprofv3 --pmc runs")
+    ap.add_argument("--calib-copy-mb", type=int, default=0,
+                    help="run one device copy of this many MiB at the end (calibrates PMC byte counters)")
     return ap.parse_args()
 
 
@@ -61,9 +64,12 @@ def main():
 
     def qmat(t, rows, cols, n, g):
         out = torch.empty(n, rows * row_bytes(t, cols), dtype=torch.uint8, device=dev)
-        for i in range(n):   # chunked to bound the f32 staging memory
-            wf = torch.randn(rows, cols, generator=g, device=dev) * 0.02
-            G.quantize_weights(t, wf, out[i])
+        step = max(1, (1 << 28) // (rows * cols))   # experts per launch: 1 GiB of f32 staging at most
+        for i in range(0, n, step):
+            m = min(step, n - i)
+            wf = torch.randn(m * rows, cols, generator=g, device=dev) * 0.02
+            G.quantize_weights(t, wf, out[i:i + m])
+            del wf
         return out
 
     def make_layer(seed, t, st, E=256, H=2048, F=512, K=8, bias=None):
@@ -100,6 +106,25 @@ def main():
         return best, gr
 
     H, F, E, K = 2048, 512, 256, 8
+    if args.pmc:
+        # counter-collection mode (rocprofv3 --pmc serialises every dispatch):
+        # one layer, a few eager layer calls, then the calibration copy
+        print("bench.py --pmc: building one layer", flush=True)
+        L = make_layer(100, Q4_0, Q4_0)
+        xs = torch.randn(args.steps, 1, H, device=dev)
+        out = torch.empty(1, H, device=dev)
+        for i in range(args.steps):
+            L.forward(xs[i], out=out)
+        torch.cuda.synchronize()
+        print(f"bench.py --pmc: {args.steps} layer calls done", flush=True)
+        if args.calib_copy_mb:
+            src = torch.empty(args.calib_copy_mb << 18, dtype=torch.float32, device=dev).fill_(1.0)
+            dst = torch.empty_like(src)
+            torch.cuda.synchronize()
+            dst.copy_(src)
+            torch.cuda.synchronize()
+        print(json.dumps({"pmc_mode": True, "steps": args.steps, "calib_copy_mib": args.calib_copy_mb}), flush=True)
+        return
     sel_bytes = K * (2 * F * row_bytes(Q4_0, H) + H * row_bytes(Q4_0, F))       # 14,155,776
     expert_bytes = sel_bytes // K
     all_bytes = sel_bytes + expert_bytes + E * H * 4 + H * 4 * 2                  # + shared, router, x, out
@@ -167,9 +192,20 @@ def main():
                             "GBs": round(kbytes[name] / avg / 1e9, 1)}
     dom = max(per_kernel, key=lambda k: per_kernel[k]["us"])
     ach = per_kernel[dom]["GBs"]
+    # HBM traffic per launch of the dominant kernel, measured by the rocprofv3
+    # FETCH_SIZE / WRITE_SIZE passes summarised in profiles/ (bench.py cannot
+    # read hardware counters itself); null when no summary covers the kernel
+    traffic, traffic_src = None, None
+    tpath = os.path.join(ROOT, "profiles", "k_moe_expert_m1_q4_0_traffic.json")
+    if os.path.exists(tpath):
+        tj = json.load(open(tpath))
+        for kname, kv in tj["kernels"].items():
+            if kname.split("::")[-1].startswith(dom):
+                traffic = int(kv["read_bytes"] + kv["write_bytes"])
+                traffic_src = tj["source"]
     roofline = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom,
-                "alg_bytes_per_launch": kbytes[dom], "avg_launch_us": per_kernel[dom]["us"]}
+                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
+                "kernel": dom, "alg_bytes_per_launch": kbytes[dom], "avg_launch_us": per_kernel[dom]["us"]}
 
     extra = {"us_per_layer_m1": round(us_layer, 3), "us_per_layer_m1_eager": round(us_eager, 2),
              "GBs_selected_m1": round(value, 1), "GBs_all_bytes_m1": round(all_bytes / (t_step / args.steps) / 1e9, 1),
@@ -245,6 +281,14 @@ def main():
         cpu = {"value": round(sel_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
                "sample": f"{n} M=1 Q4_0 MoE layer calls of config 3 (oracle/oracle.c, OpenMP row-parallel), "
                          f"{dt * 1e6:.0f} us/layer"}
+
+    if args.calib_copy_mb:
+        src = torch.empty(args.calib_copy_mb << 18, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        extra["calib_copy_bytes_each_way"] = args.calib_copy_mb << 20
 
     line = {"metric": "MoE decode FFN effective HBM GB/s on selected-expert bytes (M=1, Q4_0, Qwen3.5-35B-A3B shape)",
             "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
