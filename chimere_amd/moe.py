@@ -76,6 +76,26 @@ class MoeLayer:
         check()
         return out
 
+    def prefill(self, x, out=None, ids=None, wts=None):
+        """x [T, H] f32, any T >= 1 -> out [T, H] through chimere_moe_prefill
+        (int8 matrix-core grouped GEMMs; Q4_0 / Q8_0 weights).  The prefill
+        workspace is allocated on first use and grown when T exceeds it."""
+        T = x.shape[0]
+        if out is None:
+            out = torch.empty_like(x)
+        if getattr(self, "pf_ntok", 0) < T:
+            self.pf_bytes = lib().chimere_moe_prefill_workspace_size(C.byref(self.c), T)
+            if self.pf_bytes == 0:
+                raise ValueError("chimere_moe_prefill_workspace_size rejected the layer shape")
+            self.pf_workspace = torch.empty(self.pf_bytes, dtype=torch.uint8, device=self.device)
+            self.pf_ntok = T
+        lib().chimere_moe_prefill(C.byref(self.c), C.c_void_p(x.data_ptr()), C.c_void_p(out.data_ptr()), T,
+                                  C.c_void_p(ids.data_ptr()) if ids is not None else None,
+                                  C.c_void_p(wts.data_ptr()) if wts is not None else None,
+                                  C.c_void_p(self.pf_workspace.data_ptr()), self.pf_bytes, G._stream())
+        check()
+        return out
+
     # ------------------------------------------------------------------
     def forward_moe_v3(self, x):
         """One token through the reference's 7-launch V3 sequence + shared expert."""

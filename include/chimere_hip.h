@@ -169,6 +169,22 @@ void chimere_moe_ffn_decode_stage(const chimere_moe_layer *layer, const float *x
                                   int ntok, void *workspace, size_t workspace_bytes, int stage,
                                   hipStream_t stream);
 
+/* Routed MoE layer for a chunk of ntok >= 1 tokens (prompt prefill).
+ * Replaces the reference's per-token loop over the decode MoE during prefill
+ * (src/qwen35_model/compute_graph.rs:1787-1800, moe_ffn.rs:1081-1768 per
+ * token): tokens are grouped by expert and the expert projections run as int8
+ * matrix-core GEMMs.  Same routing and arithmetic per token as
+ * chimere_moe_ffn_decode except the fp32 accumulation order of the quantized
+ * projections, which is ascending block order (one accumulator per row).
+ * Q4_0 / Q8_0 experts and shared expert only.  ids_out / w_out (both or
+ * neither) receive [ntok][top_k].  No allocation; workspace from
+ * chimere_moe_prefill_workspace_size(layer, >= ntok), 256-byte aligned, needs
+ * no initialisation. */
+size_t chimere_moe_prefill_workspace_size(const chimere_moe_layer *layer, int max_ntok);
+void chimere_moe_prefill(const chimere_moe_layer *layer, const float *x, float *out, int ntok,
+                         int *ids_out, float *w_out, void *workspace, size_t workspace_bytes,
+                         hipStream_t stream);
+
 /* ----------------------------------------------- weight quantizers (GPU) */
 /* Not part of the reference's ABI (its weights come pre-quantized from GGUF);
  * used to build synthetic weights on the device.  n multiple of 32 (IQ3_S:
