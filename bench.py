@@ -12,7 +12,8 @@ come from HBM and not from the 256 MB Infinity Cache.  Timed as one HIP graph
 of exactly K steps between events, after W warm-up steps.
 
 Also reported (extra): M=8 IQ3_S layer (config 4, uniform and Zipf routing),
-the Q4_0 151936x2048 head GEMV (config 2), the Q8_0 4096x2048 GEMV (config 1),
+the 512-token Q4_0 prefill chunk (config 5, int8 MFMA), the Q4_0 151936x2048
+head GEMV (config 2), the Q8_0 4096x2048 GEMV (config 1),
 per-kernel times and the roofline of the dominant kernel, and the CPU
 baseline (the C restatement in oracle/, timed on this host).
 """
@@ -239,6 +240,28 @@ def main():
                                          "GBs_unique_expert_bytes": round(ub / (us8 * 1e-6) / 1e9, 1)}
             del l8
             torch.cuda.empty_cache()
+
+        # ---------------- config 5: 512-token prefill chunk, Q4_0, two layer copies rotated
+        T = 512
+        lp = [make_layer(300 + r, Q4_0, Q4_0) for r in range(2)]
+        xp = torch.randn(T, H, generator=gx, device=dev)
+        op = torch.empty(T, H, device=dev)
+        ids = torch.empty(T, K, dtype=torch.int32, device=dev)
+        for lyr in lp:
+            lyr.prefill(xp, out=op, ids=ids, wts=torch.empty(T, K, device=dev))
+        ue = len(set(ids.cpu().numpy().reshape(-1).tolist()))
+        fns = [(lambda i=i: lp[i % 2].prefill(xp, out=op)) for i in range(16)]
+        tp, _ = graph_time(fns)
+        upf = tp / 16
+        pairs = T * K + T                                   # routed pairs + shared expert rows
+        ops = pairs * 2 * (2 * F * H + H * F)               # int8 MACs x2 of gate, up, down
+        pbytes = (ue + 1) * expert_bytes + E * H * 4 + 2 * T * H * 4
+        extra["prefill_q4_0_512"] = {
+            "us_per_chunk": round(upf * 1e6, 2), "tokens_per_s": round(T / upf, 1), "unique_experts": ue,
+            "GBs_unique_weight_bytes": round(pbytes / upf / 1e9, 1),
+            "int8_TOPs": round(ops / upf / 1e12, 2), "mfma_frac_of_int8_peak": round(ops / upf / 1e12 / 5000.0, 4)}
+        del lp
+        torch.cuda.empty_cache()
 
         # ---------------- config 2: Q4_0 head 151936 x 2048, three copies rotated
         V = 151936
