@@ -172,6 +172,84 @@ __device__ __forceinline__ int dot_iq3_s(const uint8_t* row, int off, int ib, co
                           grid, dw);
 }
 
+// ---- a weight block decoded once to 32 int8 values (8 words, element order
+// of the Q8_1 block), for reuse against several activation blocks.
+// wdot<T> gives the same exact sumi as the dot_* functions above (integer
+// sums are order-free).  Q4_0 values are the raw nibbles (0..15); the -8
+// term is applied with the activation's sum.  IQ3_S: signed grid levels and
+// the sub-block multiplier 1 + 2*scale.
+struct WBlk {
+    int v[8];
+    float dw;
+    int mult;
+};
+
+template <int T>
+__device__ __forceinline__ int wdot(const WBlk& w, const XBlk& x) {
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) s = dot4(w.v[i], x.q[i], s);
+    if constexpr (T == T_Q4_0) return s - 8 * x.sumq;
+    else if constexpr (T == T_IQ3_S) return s * w.mult;
+    else return s;
+}
+
+__device__ __forceinline__ void wdec_q8_0_core(uint32_t dbits, const uint32_t (&q)[8], WBlk& w) {
+    w.dw = h2f(dbits);
+    w.mult = 1;
+#pragma unroll
+    for (int i = 0; i < 8; i++) w.v[i] = (int)q[i];
+}
+
+__device__ __forceinline__ void wdec_q4_0_core(uint32_t dbits, const uint32_t (&qs)[4], WBlk& w) {
+    w.dw = h2f(dbits);
+    w.mult = 1;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        w.v[i] = (int)(qs[i] & 0x0F0F0F0Fu);
+        w.v[4 + i] = (int)((qs[i] >> 4) & 0x0F0F0F0Fu);
+    }
+}
+
+__device__ __forceinline__ void wdec_iq3_s_core(uint32_t dbits, uint32_t qs0, uint32_t qs1, uint32_t qh, uint32_t sg,
+                                                uint32_t nib, const uint32_t* grid, WBlk& w) {
+    w.dw = h2f(dbits);
+    w.mult = 1 + 2 * (int)nib;
+#pragma unroll
+    for (int l = 0; l < 4; l++) {
+        const uint32_t qsw = l < 2 ? qs0 : qs1;
+        const uint32_t i0 = ((qsw >> (16 * (l & 1))) & 0xFFu) | (((qh >> (2 * l)) & 1u) << 8);
+        const uint32_t i1 = ((qsw >> (16 * (l & 1) + 8)) & 0xFFu) | (((qh >> (2 * l + 1)) & 1u) << 8);
+        const uint32_t sb = (sg >> (8 * l)) & 0xFFu;
+        const uint32_t m0 = nib_mask(sb & 0xFu), m1 = nib_mask(sb >> 4);
+        w.v[2 * l] = (int)((grid[i0] ^ m0) + (m0 & 0x01010101u));
+        w.v[2 * l + 1] = (int)((grid[i1] ^ m1) + (m1 & 0x01010101u));
+    }
+}
+
+// Block b of a row chunk in LDS (layout as block_dot below), decoded.
+template <int T>
+__device__ __forceinline__ void block_decode(const uint8_t* row, int b, const uint32_t* grid, WBlk& w) {
+    if constexpr (T == T_Q8_0) {
+        const int off = b * 34;
+        uint32_t q[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) q[i] = lds_u32(row, off + 2 + 4 * i);
+        wdec_q8_0_core(lds_u16(row, off), q, w);
+    } else if constexpr (T == T_Q4_0) {
+        const int off = b * 18;
+        uint32_t qs[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) qs[i] = lds_u32(row, off + 2 + 4 * i);
+        wdec_q4_0_core(lds_u16(row, off), qs, w);
+    } else {
+        const int off = (b >> 3) * 110, ib = b & 7;
+        const uint32_t sc = row[off + 106 + (ib >> 1)];
+        wdec_iq3_s_core(lds_u16(row, off), lds_u32(row, off + 2 + 8 * ib), lds_u32(row, off + 6 + 8 * ib),
+                        row[off + 66 + ib], lds_u32(row, off + 74 + 4 * ib), (sc >> (4 * (ib & 1))) & 0xFu, grid, w);
+    }
+}
+
 // One weight block held in registers, read straight from global memory with
 // loads that never leave the block.  load() only issues the loads (the raw
 // words are kept as loaded, so no wait is forced there); dot() assembles the
@@ -188,8 +266,7 @@ template <> struct RegBlk<T_Q4_0> {
         if (!ph2) { v = *(const uint4*)blk; t = *(const uint16_t*)(blk + 16); }
         else { t = *(const uint16_t*)blk; v = *(const uint4*)(blk + 2); }
     }
-    __device__ __forceinline__ int dot(const XBlk& x, const uint32_t*, float* dw) const {
-        uint32_t d, qs[4];
+    __device__ __forceinline__ void fields(uint32_t& d, uint32_t (&qs)[4]) const {
         if (!ph2) {
             d = v.x & 0xFFFFu;
             qs[0] = (v.x >> 16) | (v.y << 16);
@@ -200,7 +277,16 @@ template <> struct RegBlk<T_Q4_0> {
             d = t;
             qs[0] = v.x; qs[1] = v.y; qs[2] = v.z; qs[3] = v.w;
         }
+    }
+    __device__ __forceinline__ int dot(const XBlk& x, const uint32_t*, float* dw) const {
+        uint32_t d, qs[4];
+        fields(d, qs);
         return dot_q4_0_core(d, qs, x, dw);
+    }
+    __device__ __forceinline__ void decode(const uint32_t*, WBlk& w) const {
+        uint32_t d, qs[4];
+        fields(d, qs);
+        wdec_q4_0_core(d, qs, w);
     }
 };
 template <> struct RegBlk<T_Q8_0> {
@@ -215,6 +301,15 @@ template <> struct RegBlk<T_Q8_0> {
     }
     __device__ __forceinline__ int dot(const XBlk& x, const uint32_t*, float* dw) const {
         uint32_t d, q[8];
+        fields(d, q);
+        return dot_q8_0_core(d, q, x, dw);
+    }
+    __device__ __forceinline__ void decode(const uint32_t*, WBlk& w) const {
+        uint32_t d, q[8];
+        fields(d, q);
+        wdec_q8_0_core(d, q, w);
+    }
+    __device__ __forceinline__ void fields(uint32_t& d, uint32_t (&q)[8]) const {
         if (!ph2) {
             const uint32_t w[9] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w, t};
             d = w[0] & 0xFFFFu;
@@ -225,7 +320,6 @@ template <> struct RegBlk<T_Q8_0> {
             q[0] = v0.x; q[1] = v0.y; q[2] = v0.z; q[3] = v0.w;
             q[4] = v1.x; q[5] = v1.y; q[6] = v1.z; q[7] = v1.w;
         }
-        return dot_q8_0_core(d, q, x, dw);
     }
 };
 template <> struct RegBlk<T_IQ3_S> {
@@ -244,6 +338,10 @@ template <> struct RegBlk<T_IQ3_S> {
     __device__ __forceinline__ int dot(const XBlk& x, const uint32_t* grid, float* dw) const {
         return dot_iq3_s_core(d, q0 | (q1 << 16), q2 | (q3 << 16), qh, s0 | (s1 << 16), (sc >> (4 * (ib & 1))) & 0xFu,
                               x, grid, dw);
+    }
+    __device__ __forceinline__ void decode(const uint32_t* grid, WBlk& w) const {
+        wdec_iq3_s_core(d, q0 | (q1 << 16), q2 | (q3 << 16), qh, s0 | (s1 << 16), (sc >> (4 * (ib & 1))) & 0xFu, grid,
+                        w);
     }
 };
 

@@ -69,6 +69,9 @@ struct MoeArgs {
     uint2* terms;       // F > 512: [M*K + M][H][F/32]  down block terms (f32 scale bits, int32 sumi)
     float* lane_acc;    // F <= 512: [M*K + M][H][F/32]  lane j's finished accumulator (one block per lane)
     int64_t xq_stride;
+    uint8_t* hq;        // M > 1: [M*K + M][hq_stride]  Q8_1(h) per pair
+    float* dn;          // M > 1: [M*K + M][H]  down-projection output per pair (aliases terms)
+    int64_t hq_stride;
     uint64_t* phase;    // debug timestamps (CHIMERE_PHASE_TIMING builds)
 };
 
@@ -149,145 +152,105 @@ __device__ __forceinline__ void down_terms(const RegBlk<T> (&rb)[EX_MAX_RPT], co
     for (int k = 0; k < EX_MAX_RPT; k++) {
         const int r = threadIdx.x + EX_THREADS * k;
         if (r < a.H) {
+            WBlk wb;
+            rb[k].decode(grid, wb);
             for (int t = 0; t < ntok; t++) {
                 XBlk xb;
                 xlds_to_blk(hx[t], xb);
-                float dw;
-                const int s = rb[k].dot(xb, grid, &dw);
+                const int s = wdot<T>(wb, xb);
                 const int64_t o = ((int64_t)pairs[t] * a.H + r) * NB + w;
-                if (NB <= SLOTS) a.lane_acc[o] = __builtin_fmaf(dw * xb.d, (float)s, 0.0f);
-                else a.terms[o] = make_uint2(__builtin_bit_cast(uint32_t, dw * xb.d), (uint32_t)s);
+                if (NB <= SLOTS) a.lane_acc[o] = __builtin_fmaf(wb.dw * xb.d, (float)s, 0.0f);
+                else a.terms[o] = make_uint2(__builtin_bit_cast(uint32_t, wb.dw * xb.d), (uint32_t)s);
             }
         }
     }
 }
 
-// K2: one work-group per (unit, w): unit = a distinct selected expert (or the
-// shared expert), w = a 32-row block of its F dimension.  1024 threads.
-//  1. Routing: waves 0..M-1 each run softmax/top-k for one token from the
-//     logits (registers only); thread 0 builds the distinct-expert plan.  No
-//     work-group waits on another: each recomputes it; work-group (0,0)
-//     publishes weights and plan for K3.
-//  2. Issues, together: the 32 gate + 32 up rows of block w (HBM -> LDS,
-//     asynchronous) and the block-w column slice of the down matrix (one
-//     weight block per down row, into registers).
-//  3. gate/up dots (group g < 32: gate row g, 32 + g: up row g), h =
-//     silu(gate)*up, Q8_1(h) for the 32-row block (ggml semantics).
-//  4. Exact down terms of block w for every down row (the L=16 order needs
-//     only these per-block (scale, sumi) pairs; K3 replays the order).
-// Work-groups are laid out so that the NB blocks of one unit run on one XCD
-// (work-group ids are dealt round-robin to the 8 XCDs), so the down slices
-// of an expert share that XCD's L2.
-template <int TE, int TS, int NT>
-__global__ __launch_bounds__(EX_THREADS) void k_moe_expert(MoeArgs a) {
-    constexpr int CBE = ChunkGeom<TE>::BYTES, CBS = ChunkGeom<TS>::BYTES;
-    constexpr int CB = CBE > CBS ? CBE : CBS;
-    constexpr int ROUTE_BYTES = MAX_E * 4 + (int)sizeof(Plan);
-    constexpr int TILE_BYTES = EX_RG * CB + 16 > ROUTE_BYTES ? EX_RG * CB + 16 : ROUTE_BYTES;
-    __shared__ __attribute__((aligned(16))) uint8_t tile[TILE_BYTES];
-    __shared__ XLds xs[NT][MAX_CHUNK_BLOCKS];
-    __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
-    __shared__ float hg[MAX_TOK][QK], hu[MAX_TOK][QK];
-    __shared__ XLds hx[MAX_TOK];
-    __shared__ int toks[MAX_TOK], pairs[MAX_TOK];
-    __shared__ int s_ids[MAX_TOK * MAX_K];
-    __shared__ float s_w[MAX_TOK * MAX_K];
-    Plan& pl = *(Plan*)(tile + MAX_E * 4);
-
-    const int NB = a.F / QK;
-    const int L = blockIdx.x, xcd = L & 7, li = L >> 3;
-    const int u = xcd + 8 * (li / NB), w = li % NB;
+// Routing for all M tokens and the distinct-expert plan, by a 1024-thread
+// work-group: waves 0..M-1 each run softmax/top-k for one token from the
+// logits (registers only); then the plan is built in parallel: the first
+// pair (lowest t*K+k) selecting an expert numbers it by its rank among first
+// pairs; the order of pairs inside an expert does not affect any result.
+// `first` is LDS scratch of E ints.  With `publish`, the routing weights
+// (and ids_out / w_out) and the plan are written to global memory.
+__device__ __forceinline__ void route_plan(const MoeArgs& a, int* first, Plan& pl, int* s_ids, float* s_w,
+                                           bool publish) {
     const int tid = threadIdx.x;
-    if (u > a.M * a.K) return;
-    const bool shared = u == a.M * a.K;
-    if (shared && !a.has_shared) return;
-    PHASE(1, 0);
-    int ntok;
-    if (shared) {
-        ntok = a.M;
-        if (tid < a.M) { toks[tid] = tid; pairs[tid] = a.M * a.K + tid; }
+    const int MK = a.M * a.K;
+
+    const int wave = tid >> 6;
+    if (wave < a.M) topk_wave_any(a.logits + wave * a.E, a.E, a.K, s_ids + wave * a.K, s_w + wave * a.K);
+    // distinct-expert plan, built in parallel: the first pair (lowest
+    // t*K+k) selecting an expert numbers it by its rank among first pairs;
+    // the order of pairs inside an expert does not affect any result.
+    __shared__ int s_fcnt[2], s_cnt[MAX_TOK * MAX_K];
+    for (int e = tid; e < a.E; e += EX_THREADS) first[e] = 0x7fffffff;
+    if (tid < MAX_TOK * MAX_K) s_cnt[tid] = 0;
+    __syncthreads();
+    if (tid < MK) atomicMin(&first[s_ids[tid]], tid);
+    __syncthreads();
+    int fp = 0;
+    bool isfirst = false;
+    if (tid < 128) {
+        fp = tid < MK ? first[s_ids[tid]] : -1;
+        isfirst = tid < MK && fp == tid;
+        const uint64_t m = __ballot(isfirst);
+        if ((tid & 63) == 0) s_fcnt[tid >> 6] = __popcll(m);
+        const int lrank = __popcll(m & ((1ull << (tid & 63)) - 1));
+        __syncthreads();
+        const int rank = lrank + ((tid >> 6) ? s_fcnt[0] : 0);
+        if (isfirst) { pl.uexp[rank] = s_ids[tid]; s_cnt[tid] = rank; }   // s_cnt: first pair -> unit
+        if (tid == 0) pl.nu = s_fcnt[0] + (MK > 64 ? s_fcnt[1] : 0);
     } else {
-        const int wave = tid >> 6;
-        if (wave < a.M) topk_wave_any(a.logits + wave * a.E, a.E, a.K, s_ids + wave * a.K, s_w + wave * a.K);
-        // distinct-expert plan, built in parallel: the first pair (lowest
-        // t*K+k) selecting an expert numbers it by its rank among first pairs;
-        // the order of pairs inside an expert does not affect any result.
-        int* first = (int*)tile;    // [E]: lowest pair index selecting e
-        __shared__ int s_fcnt[2], s_cnt[MAX_TOK * MAX_K];
-        for (int e = tid; e < a.E; e += EX_THREADS) first[e] = 0x7fffffff;
-        if (tid < MAX_TOK * MAX_K) s_cnt[tid] = 0;
         __syncthreads();
-        PHASE(1, 1);
-        const int MK = a.M * a.K;
-        if (tid < MK) atomicMin(&first[s_ids[tid]], tid);
-        __syncthreads();
-        int fp = 0;
-        bool isfirst = false;
-        if (tid < 128) {
-            fp = tid < MK ? first[s_ids[tid]] : -1;
-            isfirst = tid < MK && fp == tid;
-            const uint64_t m = __ballot(isfirst);
-            if ((tid & 63) == 0) s_fcnt[tid >> 6] = __popcll(m);
-            const int lrank = __popcll(m & ((1ull << (tid & 63)) - 1));
-            __syncthreads();
-            const int rank = lrank + ((tid >> 6) ? s_fcnt[0] : 0);
-            if (isfirst) { pl.uexp[rank] = s_ids[tid]; s_cnt[tid] = rank; }   // s_cnt: first pair -> unit
-            if (tid == 0) pl.nu = s_fcnt[0] + (MK > 64 ? s_fcnt[1] : 0);
-        } else {
-            __syncthreads();
-        }
-        __syncthreads();
-        int uu = 0;
-        if (tid < MK) uu = s_cnt[fp];
-        __syncthreads();
-        if (tid < MAX_TOK * MAX_K) s_cnt[tid] = 0;
-        __syncthreads();
-        if (tid < MK) {
-            const int n = atomicAdd(&s_cnt[uu], 1);
-            pl.upair[uu][n] = tid;
-            pl.utok[uu][n] = tid / a.K;
-        }
-        __syncthreads();
-        if (tid < pl.nu) pl.untok[tid] = s_cnt[tid];
-        __syncthreads();
-        if (u == 0 && w == 0) {
-            const int nu = pl.nu;
-            for (int i = tid; i < a.M * a.K; i += EX_THREADS) {
-                a.wts[i] = s_w[i];
-                if (a.ids_out) { a.ids_out[i] = s_ids[i]; a.w_out[i] = s_w[i]; }
-            }
-            int* P = a.plan;
-            if (tid == 0) P[0] = nu;
-            for (int i = tid; i < nu; i += EX_THREADS) {
-                P[PLAN_UEXP + i] = pl.uexp[i];
-                P[PLAN_UNTOK + i] = pl.untok[i];
-                for (int n = 0; n < pl.untok[i]; n++) P[PLAN_UPAIR + i * MAX_TOK + n] = pl.upair[i][n];
-            }
-        }
-        if (u >= pl.nu) return;
-        ntok = pl.untok[u];
-        if (tid < ntok) { toks[tid] = pl.utok[u][tid]; pairs[tid] = pl.upair[u][tid]; }
     }
-    if constexpr (TE == T_IQ3_S || TS == T_IQ3_S)
-        for (int i = tid; i < 512; i += EX_THREADS) grid[i] = c_iq3s_grid_moe[i];
-    PHASE(1, 2);
+    __syncthreads();
+    int uu = 0;
+    if (tid < MK) uu = s_cnt[fp];
+    __syncthreads();
+    if (tid < MAX_TOK * MAX_K) s_cnt[tid] = 0;
+    __syncthreads();
+    if (tid < MK) {
+        const int n = atomicAdd(&s_cnt[uu], 1);
+        pl.upair[uu][n] = tid;
+        pl.utok[uu][n] = tid / a.K;
+    }
+    __syncthreads();
+    if (tid < pl.nu) pl.untok[tid] = s_cnt[tid];
+    __syncthreads();
+    if (publish) {
+        const int nu = pl.nu;
+        for (int i = tid; i < MK; i += EX_THREADS) {
+            a.wts[i] = s_w[i];
+            if (a.ids_out) { a.ids_out[i] = s_ids[i]; a.w_out[i] = s_w[i]; }
+        }
+        int* P = a.plan;
+        if (tid == 0) P[0] = nu;
+        for (int i = tid; i < nu; i += EX_THREADS) {
+            P[PLAN_UEXP + i] = pl.uexp[i];
+            P[PLAN_UNTOK + i] = pl.untok[i];
+            for (int n = 0; n < pl.untok[i]; n++) P[PLAN_UPAIR + i * MAX_TOK + n] = pl.upair[i][n];
+        }
+    }
+
+}
+
+// One work item of K2 (see below): gate/up rows [32w, 32w+32) of one expert
+// (weights of type T at gate / up / down), h block w, and its down terms.
+template <int T, int NT, int CB>
+__device__ __forceinline__ void expert_item(const MoeArgs& a, uint8_t* tile, XLds (*xs)[MAX_CHUNK_BLOCKS],
+                                            const uint32_t* grid, float (*hg)[QK], float (*hu)[QK], XLds* hx,
+                                            const int* toks, const int* pairs, int ntok, int w, const uint8_t* gate,
+                                            const uint8_t* up, const uint8_t* down) {
+    const int tid = threadIdx.x;
+    const int NB = a.F / QK;
     const int r0 = w * QK;
-    const int64_t e = shared ? 0 : pl.uexp[u];
-    RegBlk<TE> dbE[EX_MAX_RPT];
-    RegBlk<TS> dbS[EX_MAX_RPT];
+    RegBlk<T> db[EX_MAX_RPT];
     float acc[1][NT];
-    if (shared) {
-        load_down_blocks<TS>(dbS, a.sh_down, row_bytes(TS, a.F), w, a.H);
-        const int64_t rb = row_bytes(TS, a.H);
-        tile_gemv<TS, NT, EX_RG, 1>(tile, xs, grid, a.sh_gate + r0 * rb, QK, a.sh_up + r0 * rb, QK, rb,
-                                         a.H, a.xq, a.xq_stride, toks, ntok, acc, PHASE_PTR(1, 5));
-    } else {
-        load_down_blocks<TE>(dbE, a.down + e * a.sd, row_bytes(TE, a.F), w, a.H);
-        const int64_t rb = row_bytes(TE, a.H);
-        tile_gemv<TE, NT, EX_RG, 1>(tile, xs, grid, a.gate + e * a.sg + r0 * rb, QK,
-                                         a.up + e * a.su + r0 * rb, QK, rb, a.H, a.xq, a.xq_stride, toks, ntok,
-                                         acc, PHASE_PTR(1, 5));
-    }
+    load_down_blocks<T>(db, down, row_bytes(T, a.F), w, a.H);
+    const int64_t rb = row_bytes(T, a.H);
+    tile_gemv<T, NT, EX_RG, 1>(tile, &xs[0][0], grid, gate + r0 * rb, QK, up + r0 * rb, QK, rb, a.H, a.xq, a.xq_stride, toks,
+                               ntok, acc, PHASE_PTR(1, 5));
     PHASE(1, 3);
     const int g = tid >> 4, j = tid & 15;
 #pragma unroll
@@ -301,8 +264,8 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert(MoeArgs a) {
         }
     }
     __syncthreads();
-    // one half-wave per token: Q8_1 of the 32-row block of h (ggml semantics),
-    // kept decoded in LDS for the down terms
+    // one half-wave per token: Q8_1 of the 32-row block of h (ggml
+    // semantics), kept decoded in LDS for the down terms
     if ((tid >> 5) < ntok) {
         const int t = tid >> 5, i = tid & 31;
         const float xi = det_silu(hg[t][i]) * hu[t][i];
@@ -322,9 +285,69 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert(MoeArgs a) {
     }
     __syncthreads();
     PHASE(1, 7);
-    if (shared) down_terms<TS>(dbS, hx, pairs, ntok, grid, a, NB, w);
-    else down_terms<TE>(dbE, hx, pairs, ntok, grid, a, NB, w);
-    PHASE(1, 4);
+    down_terms<T>(db, hx, pairs, ntok, grid, a, NB, w);
+}
+
+// K2: work items (unit, w): unit = a distinct selected expert (or the shared
+// expert), w = a 32-row block of its F dimension.  1024 threads; the grid is
+// at most one work-group per CU and each work-group loops over items
+// V = blockIdx.x, blockIdx.x + gridDim.x, ...
+//  1. Routing, once per work-group: waves 0..M-1 each run softmax/top-k for
+//     one token from the logits (registers only), then the distinct-expert
+//     plan.  No work-group waits on another: each recomputes it; work-group 0
+//     publishes weights and plan for K3.
+//  Per item:
+//  2. Issues, together: the 32 gate + 32 up rows of block w (HBM -> LDS,
+//     asynchronous) and the block-w column slice of the down matrix (one
+//     weight block per down row, into registers).
+//  3. gate/up dots (group g < 32: gate row g, 32 + g: up row g), h =
+//     silu(gate)*up, Q8_1(h) for the 32-row block (ggml semantics).
+//  4. Exact down terms of block w for every down row (the L=16 order needs
+//     only these per-block (scale, sumi) pairs; K3 replays the order).
+// Item V goes to XCD V & 7 (the grid is a multiple of 8 and work-group ids
+// are dealt round-robin to the 8 XCDs); consecutive units of an XCD's items
+// are 8 apart, so one expert's row blocks share that XCD's L2.
+template <int TE, int TS, int NT>
+__global__ __launch_bounds__(EX_THREADS) void k_moe_expert(MoeArgs a) {
+    constexpr int CBE = ChunkGeom<TE>::BYTES, CBS = ChunkGeom<TS>::BYTES;
+    constexpr int CB = CBE > CBS ? CBE : CBS;
+    constexpr int TILE_BYTES = EX_RG * CB + 16 > MAX_E * 4 ? EX_RG * CB + 16 : MAX_E * 4;
+    __shared__ __attribute__((aligned(16))) uint8_t tile[TILE_BYTES];
+    __shared__ XLds xs[NT][MAX_CHUNK_BLOCKS];
+    __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
+    __shared__ float hg[MAX_TOK][QK], hu[MAX_TOK][QK];
+    __shared__ XLds hx[MAX_TOK];
+    __shared__ int toks[MAX_TOK], pairs[MAX_TOK];
+    __shared__ int s_ids[MAX_TOK * MAX_K];
+    __shared__ float s_w[MAX_TOK * MAX_K];
+    __shared__ Plan pl;
+
+    const int NB = a.F / QK;
+    const int MK = a.M * a.K;
+    const int NI = 8 * ((MK + 1 + 7) / 8) * NB;
+    const int tid = threadIdx.x;
+    PHASE(1, 0);
+    route_plan(a, (int*)tile, pl, s_ids, s_w, blockIdx.x == 0);
+    if constexpr (TE == T_IQ3_S || TS == T_IQ3_S)
+        for (int i = tid; i < 512; i += EX_THREADS) grid[i] = c_iq3s_grid_moe[i];
+    PHASE(1, 2);
+    for (int V = blockIdx.x; V < NI; V += gridDim.x) {
+        const int li = V >> 3, u = (V & 7) + 8 * (li / NB), w = li % NB;
+        const bool shared = u == MK;
+        if (u > MK || (shared && !a.has_shared) || (!shared && u >= pl.nu)) continue;
+        const int ntok = shared ? a.M : pl.untok[u];
+        __syncthreads();   // the previous item's readers of toks / pairs / hx are done
+        if (tid < ntok) {
+            toks[tid] = shared ? tid : pl.utok[u][tid];
+            pairs[tid] = shared ? MK + tid : pl.upair[u][tid];
+        }
+        if (shared)
+            expert_item<TS, NT, CB>(a, tile, xs, grid, hg, hu, hx, toks, pairs, ntok, w, a.sh_gate, a.sh_up, a.sh_down);
+        else
+            expert_item<TE, NT, CB>(a, tile, xs, grid, hg, hu, hx, toks, pairs, ntok, w, a.gate + pl.uexp[u] * a.sg,
+                                    a.up + pl.uexp[u] * a.su, a.down + pl.uexp[u] * a.sd);
+        PHASE(1, 4);
+    }
 }
 
 // K3: grid (ceil(H/16)), 256 threads: 16 down rows per work-group, 16 lanes
@@ -406,11 +429,180 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_combine(MoeArgs a) {
     PHASE(2, 2);
 }
 
+// ------------------------------------------------ several tokens (M > 1)
+// With M > 1 the work per selected expert grows with its token count, so the
+// layer runs as five launches that each keep many work-groups in flight:
+// K1 router (as above), KP routing + plan (one work-group), KG gate/up + SiLU
+// + Q8_1(h) per (expert, 32-row block of F), KD down GEMV per (expert, 64-row
+// tile of H) with every h block of the expert's tokens (each output row
+// reduced in the L=16 order in place), KC router-weighted combine.
+
+__global__ __launch_bounds__(EX_THREADS) void k_moe_plan(MoeArgs a) {
+    __shared__ int first[MAX_E];
+    __shared__ Plan pl;
+    __shared__ int s_ids[MAX_TOK * MAX_K];
+    __shared__ float s_w[MAX_TOK * MAX_K];
+    route_plan(a, first, pl, s_ids, s_w, true);
+}
+
+// unit u of the published plan (u == M*K: the shared expert); false if none
+__device__ __forceinline__ bool load_unit(const MoeArgs& a, int u, int* pairs, int* toks, int& ntok, int64_t& e) {
+    const int MK = a.M * a.K;
+    if (u == MK) {
+        if (!a.has_shared) return false;
+        ntok = a.M;
+        e = -1;
+        if (threadIdx.x < a.M) { pairs[threadIdx.x] = MK + threadIdx.x; toks[threadIdx.x] = threadIdx.x; }
+        return true;
+    }
+    if (u >= a.plan[0]) return false;
+    ntok = a.plan[PLAN_UNTOK + u];
+    e = a.plan[PLAN_UEXP + u];
+    if (threadIdx.x < ntok) {
+        const int p = a.plan[PLAN_UPAIR + u * MAX_TOK + threadIdx.x];
+        pairs[threadIdx.x] = p;
+        toks[threadIdx.x] = p / a.K;
+    }
+    return true;
+}
+
+constexpr int KG_RG = 16;     // KG / KD: 256 threads, 64 rows per tile (4 per row group)
+// blocks per chunk: the tile and 8 tokens' blocks fit three work-groups per CU
+constexpr int KG_CHUNK = 32;
+template <int T>
+constexpr int kg_chunk() { return T == T_Q8_0 ? 16 : KG_CHUNK; }
+template <int T>
+constexpr int chunk_bytes(int blocks) { return T == T_IQ3_S ? blocks / 8 * 110 : blocks * QTraits<T>::BYTES; }
+
+// KG: grid 8*ceil((M*K+1)/8)*NB; item V -> XCD V & 7, unit (V & 7) + 8*(V/8/NB), block w = V/8 % NB.
+template <int TE, int TS>
+__global__ __launch_bounds__(GEMV_THREADS) void k_moe_gateup(MoeArgs a) {
+    constexpr int CBE = chunk_bytes<TE>(kg_chunk<TE>()), CBS = chunk_bytes<TS>(kg_chunk<TS>());
+    constexpr int CB = CBE > CBS ? CBE : CBS;
+    __shared__ __attribute__((aligned(16))) uint8_t tile[4 * KG_RG * CB + 16];
+    __shared__ XLds xs[MAX_TOK * KG_CHUNK];
+    __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
+    __shared__ float hg[MAX_TOK][QK], hu[MAX_TOK][QK];
+    __shared__ int toks[MAX_TOK], pairs[MAX_TOK];
+    const int NB = a.F / QK;
+    const int V = blockIdx.x, li = V >> 3, u = (V & 7) + 8 * (li / NB), w = li % NB;
+    if (u > a.M * a.K) return;
+    PHASE(1, 0);
+    int ntok;
+    int64_t e;
+    if (!load_unit(a, u, pairs, toks, ntok, e)) return;
+    const int tid = threadIdx.x;
+    if constexpr (TE == T_IQ3_S || TS == T_IQ3_S)
+        for (int i = tid; i < 512; i += GEMV_THREADS) grid[i] = c_iq3s_grid_moe[i];
+    PHASE(1, 1);
+    float acc[4][MAX_TOK];
+    const int r0 = w * QK;
+    if (e < 0) {
+        const int64_t rb = row_bytes(TS, a.H);
+        tile_gemv<TS, MAX_TOK, KG_RG, 4, kg_chunk<TS>()>(tile, xs, grid, a.sh_gate + r0 * rb, QK, a.sh_up + r0 * rb, QK, rb, a.H,
+                                         a.xq, a.xq_stride, toks, ntok, acc, PHASE_PTR(1, 5));
+    } else {
+        const int64_t rb = row_bytes(TE, a.H);
+        tile_gemv<TE, MAX_TOK, KG_RG, 4, kg_chunk<TE>()>(tile, xs, grid, a.gate + e * a.sg + r0 * rb, QK, a.up + e * a.su + r0 * rb,
+                                         QK, rb, a.H, a.xq, a.xq_stride, toks, ntok, acc, PHASE_PTR(1, 5));
+    }
+    PHASE(1, 2);
+    // group g holds tile rows g, g+16 (gate rows) and g+32, g+48 (up rows)
+    const int g = tid >> 4, j = tid & 15;
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int t = 0; t < MAX_TOK; t++) {
+            if (t < ntok) {
+                const float v = slot_reduce16(acc[r][t]);
+                if (j == 0) {
+                    const int row = g + KG_RG * r;
+                    if (row < QK) hg[t][row] = v;
+                    else hu[t][row - QK] = v;
+                }
+            }
+        }
+    __syncthreads();
+    // one half-wave per token: Q8_1 of the 32-row block w of h (ggml semantics)
+    for (int t = tid >> 5; t < ntok; t += GEMV_THREADS / 32) {
+        const int i = tid & 31;
+        const float xi = det_silu(hg[t][i]) * hu[t][i];
+        const float amax = bfly32_max(__builtin_fabsf(xi)), sum = bfly32_sum(xi);
+        const float d = amax / 127.0f;
+        const int q = amax == 0.0f ? 0 : (int)__builtin_roundf(xi / d);
+        uint8_t* o = a.hq + (int64_t)pairs[t] * a.hq_stride + w * Q8_1_BYTES;
+        o[4 + i] = (uint8_t)(int8_t)q;
+        if (i == 0) *(uint32_t*)o = f2h(d) | (f2h(sum) << 16);
+    }
+    PHASE(1, 3);
+}
+
+// KD: grid (H/64, M*K+1): unit blockIdx.y, down rows [64*blockIdx.x, +64).
+template <int TE, int TS>
+__global__ __launch_bounds__(GEMV_THREADS) void k_moe_down(MoeArgs a) {
+    constexpr int CBE = chunk_bytes<TE>(kg_chunk<TE>()), CBS = chunk_bytes<TS>(kg_chunk<TS>());
+    constexpr int CB = CBE > CBS ? CBE : CBS;
+    __shared__ __attribute__((aligned(16))) uint8_t tile[4 * KG_RG * CB + 16];
+    __shared__ XLds xs[MAX_TOK * KG_CHUNK];
+    __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
+    __shared__ int toks[MAX_TOK], pairs[MAX_TOK];
+    int ntok;
+    int64_t e;
+    PHASE(2, 0);
+    if (!load_unit(a, blockIdx.y, pairs, toks, ntok, e)) return;
+    const int tid = threadIdx.x;
+    PHASE(2, 1);
+    if constexpr (TE == T_IQ3_S || TS == T_IQ3_S)
+        for (int i = tid; i < 512; i += GEMV_THREADS) grid[i] = c_iq3s_grid_moe[i];
+    const int r0 = blockIdx.x * 4 * KG_RG, nr = min(4 * KG_RG, a.H - r0);
+    float acc[4][MAX_TOK];
+    // the h rows are indexed by pair
+    if (e < 0) {
+        const int64_t rb = row_bytes(TS, a.F);
+        tile_gemv<TS, MAX_TOK, KG_RG, 4, kg_chunk<TS>()>(tile, xs, grid, a.sh_down + r0 * rb, nr, nullptr, 0, rb, a.F, a.hq,
+                                         a.hq_stride, pairs, ntok, acc, PHASE_PTR(2, 5));
+    } else {
+        const int64_t rb = row_bytes(TE, a.F);
+        tile_gemv<TE, MAX_TOK, KG_RG, 4, kg_chunk<TE>()>(tile, xs, grid, a.down + e * a.sd + r0 * rb, nr, nullptr, 0, rb, a.F,
+                                         a.hq, a.hq_stride, pairs, ntok, acc, PHASE_PTR(2, 5));
+    PHASE(2, 2);
+    }
+    const int g = tid >> 4, j = tid & 15;
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int t = 0; t < MAX_TOK; t++) {
+            if (t < ntok) {
+                const float v = slot_reduce16(acc[r][t]);
+                const int row = g + KG_RG * r;
+                if (j == 0 && row < nr) a.dn[(int64_t)pairs[t] * a.H + r0 + row] = v;
+            }
+        }
+    PHASE(2, 3);
+}
+
+// KC: grid (ceil(H/256), M): out = sum_k fmaf(w_k, dn_k, acc) in k order (+ shared expert)
+__global__ __launch_bounds__(256) void k_moe_combine_dn(MoeArgs a) {
+    const int t = blockIdx.y, h = blockIdx.x * 256 + threadIdx.x;
+    if (h >= a.H) return;
+    const int MK = a.M * a.K;
+    float acc = 0.0f;
+    for (int k = 0; k < a.K; k++)
+        acc = __builtin_fmaf(a.wts[t * a.K + k], a.dn[(int64_t)(t * a.K + k) * a.H + h], acc);
+    float o = acc;
+    if (a.has_shared) {
+        const float sh = a.dn[(int64_t)(MK + t) * a.H + h];
+        if (a.sh_gate_w) o = __builtin_fmaf(sh, 1.0f / (1.0f + det_exp(-a.glogit[t])), acc);
+        else o = sh + acc;
+    }
+    a.out[(int64_t)t * a.H + h] = o;
+}
+
 // ------------------------------------------------------- workspace plan
 
 struct WsPlan {
-    size_t logits, glogit, wts, plan, xq, terms, phase, total;
-    int64_t xq_stride;
+    size_t logits, glogit, wts, plan, xq, terms, hq, phase, total;
+    int64_t xq_stride, hq_stride;
 };
 
 static size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -426,11 +618,26 @@ static WsPlan plan_ws(int H, int F, int E, int K, int M) {
     p.plan = o; o += al256((size_t)PLAN_INTS * 4);
     p.xq = o; o += al256((size_t)M * p.xq_stride);
     p.terms = o; o += al256((size_t)P * H * (F / QK) * (F / QK <= SLOTS ? 4 : 8));
+    p.hq_stride = pad_to(F, ROW_PAD) / QK * Q8_1_BYTES;
+    if (M > 1) { p.hq = o; o += al256((size_t)P * p.hq_stride); }
 #ifdef CHIMERE_PHASE_TIMING
     p.phase = o; o += al256((size_t)3 * 4096 * 16 * 8);
 #endif
     p.total = o;
     return p;
+}
+
+// K2 grid: all items, capped at one work-group per CU (a multiple of 8)
+static int expert_grid(int items) {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 8) n = 256;
+        cus[dev] = n / 8 * 8;
+    }
+    return items < cus[dev] ? items : cus[dev];
 }
 
 // stage < 0: all three kernels; 0, 1, 2: only K1, K2 or K3
@@ -440,16 +647,34 @@ static void launch_layer_nt(const MoeArgs& a, int stage, hipStream_t s) {
     if (stage < 0 || stage == 0)
         hipLaunchKernelGGL((k_moe_route<NT>), dim3(a.E + (a.sh_gate_w ? 1 : 0) + a.M), dim3(256), 0, s, a);
     if (stage < 0 || stage == 1)
-        hipLaunchKernelGGL((k_moe_expert<TE, TS, NT>), dim3(8 * ((NU + 7) / 8) * NB), dim3(EX_THREADS), 0, s, a);
+        hipLaunchKernelGGL((k_moe_expert<TE, TS, NT>), dim3(expert_grid(8 * ((NU + 7) / 8) * NB)), dim3(EX_THREADS), 0,
+                           s, a);
     if (stage < 0 || stage == 2)
         hipLaunchKernelGGL(k_moe_combine, dim3((a.H + TILE_ROWS - 1) / TILE_ROWS), dim3(GEMV_THREADS), 0, s, a);
 }
 
-// one token: instantiations without the 8-token loops
+// M > 1: five launches (stage 0: router + plan, 1: gate/up, 2: down + combine)
+template <int TE, int TS>
+static void launch_layer_multi(const MoeArgs& a, int stage, hipStream_t s) {
+    const int NB = a.F / QK, NU = a.M * a.K + 1;
+    if (stage < 0 || stage == 0) {
+        hipLaunchKernelGGL((k_moe_route<MAX_TOK>), dim3(a.E + (a.sh_gate_w ? 1 : 0) + a.M), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(k_moe_plan, dim3(1), dim3(EX_THREADS), 0, s, a);
+    }
+    if (stage < 0 || stage == 1)
+        hipLaunchKernelGGL((k_moe_gateup<TE, TS>), dim3(8 * ((NU + 7) / 8) * NB), dim3(GEMV_THREADS), 0, s, a);
+    if (stage < 0 || stage == 2) {
+        hipLaunchKernelGGL((k_moe_down<TE, TS>), dim3((a.H + 4 * KG_RG - 1) / (4 * KG_RG), NU), dim3(GEMV_THREADS), 0,
+                           s, a);
+        hipLaunchKernelGGL(k_moe_combine_dn, dim3((a.H + 255) / 256, a.M), dim3(256), 0, s, a);
+    }
+}
+
+// one token: the fused three-launch layer
 template <int TE, int TS>
 static void launch_layer(const MoeArgs& a, int stage, hipStream_t s) {
     if (a.M == 1) launch_layer_nt<TE, TS, 1>(a, stage, s);
-    else launch_layer_nt<TE, TS, MAX_TOK>(a, stage, s);
+    else launch_layer_multi<TE, TS>(a, stage, s);
 }
 
 template <int TE>
@@ -568,6 +793,7 @@ static void moe_decode(const chimere_moe_layer* L, const float* x, float* out, i
     a.wts = (float*)(w + p.wts); a.plan = (int*)(w + p.plan);
     a.xq = w + p.xq; a.terms = (uint2*)(w + p.terms); a.lane_acc = (float*)(w + p.terms);
     a.xq_stride = p.xq_stride;
+    a.hq = w + p.hq; a.dn = (float*)(w + p.terms); a.hq_stride = p.hq_stride;
     a.phase = (uint64_t*)(w + p.phase);
     dispatch_layer(L->expert_type, L->shared_type, a, stage, stream);
     check_launch("moe_ffn_decode");

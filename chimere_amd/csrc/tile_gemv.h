@@ -44,14 +44,17 @@ __device__ __forceinline__ void xlds_to_blk(const XLds& s, XBlk& x) {
 // at X + tok(i) * x_tok_stride with tok(i) = toks ? toks[i] : i.
 // acc[r][t]: partial sum of the group's r-th row (tile row g + RG*r) for
 // token t; reduce with slot_reduce16.  Contains __syncthreads().
-template <int T, int NT, int RG, int RPG>
-__device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds (*__restrict__ xs)[MAX_CHUNK_BLOCKS],
+// CBLK: blocks per chunk (default ChunkGeom<T>::BLOCKS; a multiple of 16,
+// and of 8 for IQ3_S); xs holds NT * CBLK decoded blocks (token-major).
+template <int T, int NT, int RG, int RPG, int CBLK = ChunkGeom<T>::BLOCKS>
+__device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds* __restrict__ xs,
                                           const uint32_t* __restrict__ grid,
                                           const uint8_t* base1, int n1, const uint8_t* base2, int n2,
                                           int64_t rb, int ncols, const uint8_t* __restrict__ X,
                                           int64_t x_tok_stride, const int* toks, int ntok,
                                           float (&acc)[RPG][NT], uint64_t* ph = nullptr) {
-    constexpr int CBLK = ChunkGeom<T>::BLOCKS, NTH = RG * SLOTS;
+    constexpr int NTH = RG * SLOTS;
+    static_assert(CBLK % SLOTS == 0 && (T != T_IQ3_S || CBLK % 8 == 0) && CBLK <= MAX_CHUNK_BLOCKS, "chunk");
     const int tid = threadIdx.x;
     const int g = tid >> 4, j = tid & 15;
     const int nr = n1 + n2;
@@ -73,10 +76,11 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds (*__r
             const int tk = toks ? toks[t] : t;
             XBlk xb;
             load_xblk(X + tk * x_tok_stride + (int64_t)(b0 + b) * Q8_1_BYTES, xb);
+            XLds& o = xs[t * CBLK + b];
 #pragma unroll
-            for (int k = 0; k < 8; k++) xs[t][b].q[k] = xb.q[k];
-            xs[t][b].d = xb.d;
-            xs[t][b].sumq = xb.sumq;
+            for (int k = 0; k < 8; k++) o.q[k] = xb.q[k];
+            o.d = xb.d;
+            o.sumq = xb.sumq;
         }
 #ifdef CHIMERE_PHASE_TIMING
         if (ph && tid == 0) ph[0] = __builtin_amdgcn_s_memrealtime();
@@ -92,14 +96,15 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds (*__r
             if (row_i < nr) {
                 const uint8_t* row = tile + row_i * seg;
                 for (int b = j; b < cb; b += SLOTS) {
+                    WBlk wb;   // decoded once, used for every token
+                    block_decode<T>(row, b, grid, wb);
 #pragma unroll
                     for (int t = 0; t < NT; t++) {
                         if (t < ntok) {
                             XBlk xb;
-                            xlds_to_blk(xs[t][b], xb);
-                            float dw;
-                            const int s = block_dot<T>(row, b, xb, grid, &dw);
-                            acc[r][t] = __builtin_fmaf(dw * xb.d, (float)s, acc[r][t]);
+                            xlds_to_blk(xs[t * CBLK + b], xb);
+                            const int s = wdot<T>(wb, xb);
+                            acc[r][t] = __builtin_fmaf(wb.dw * xb.d, (float)s, acc[r][t]);
                         }
                     }
                 }
