@@ -19,11 +19,11 @@
 namespace chimere {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int PF_CHUNK = 8;      // 32-element blocks per K chunk staged in LDS
-constexpr int PF_TILE = 32;      // (token, k) pairs per MFMA tile (the M dimension)
+constexpr int PF_TILE = 16;      // (token, k) pairs per tile: the M dimension of v_mfma_i32_16x16x32_i8
 constexpr int PF_THREADS = 256;  // 4 waves
+constexpr int PF_RT = 16, PF_RE = 8;   // router tile: tokens x rows per work-group
 
 struct PfArgs {
     int H, F, E, K, T, has_shared;
@@ -43,7 +43,6 @@ struct PfArgs {
     int* ids;        // [T*K]
     float* wts;      // [T*K]
     uint8_t* xq;     // [T][xq_stride]
-    int* off;        // [E+2] start of each expert's pairs in spairs
     int* spairs;     // [T*K + T] pairs grouped by expert (shared expert last)
     int* tiles;      // [max_tiles][3] (expert, start, count)
     int* ntiles;     // [1]
@@ -53,19 +52,69 @@ struct PfArgs {
     int max_tiles;
 };
 
-// P1: grid (E + has_gate, ceil(T/8)): router logits for 8 tokens per work-group.
+// P1: grid (ceil((E + has_gate) / 8), ceil(T / 16)), 256 threads: logits of 16
+// tokens x 8 router rows.  Every output keeps the reference's order
+// (elementwise.rs:186-221 launched with 256 threads): thread j accumulates
+// columns j, j+256, ... with fma, then the 256 partials are summed by the
+// halving tree (pairs j, j+m for m = 128, ..., 1).  Thread j owns partial j
+// of all 128 outputs of the tile; the tree runs in LDS for 32 outputs at a
+// time: 8 threads per output, thread q first reduces the 32 partials
+// j = q (mod 8) (tree levels m = 128 .. 8), then levels 4, 2, 1 run across
+// the 8 lanes.
 __global__ __launch_bounds__(256) void k_pf_router(PfArgs a) {
-    __shared__ float red[256];
-    const int row = blockIdx.x, t0 = blockIdx.y * MAX_TOK;
-    const int nt = min(MAX_TOK, a.T - t0);
-    float v[MAX_TOK];
-    const float* A = row < a.E ? a.router + (int64_t)row * a.H : a.sh_gate_w;
-    f32_row_dot<MAX_TOK>(A, a.x + (int64_t)t0 * a.H, a.H, nt, red, v);
-    if (threadIdx.x == 0)
-        for (int t = 0; t < nt; t++) {
-            if (row < a.E) a.logits[(int64_t)(t0 + t) * a.E + row] = a.bias ? v[t] + a.bias[row] : v[t];
-            else a.glogit[t0 + t] = v[t];
+    __shared__ float red[32][257];
+    const int tid = threadIdx.x;
+    const int NR = a.E + (a.sh_gate_w ? 1 : 0);
+    const int e0 = blockIdx.x * PF_RE, t0 = blockIdx.y * PF_RT;
+    const float* rows[PF_RE];
+#pragma unroll
+    for (int e = 0; e < PF_RE; e++) {
+        const int r = min(e0 + e, NR - 1);
+        rows[e] = r < a.E ? a.router + (int64_t)r * a.H : a.sh_gate_w;
+    }
+    float acc[PF_RT][PF_RE];
+#pragma unroll
+    for (int t = 0; t < PF_RT; t++)
+#pragma unroll
+        for (int e = 0; e < PF_RE; e++) acc[t][e] = 0.0f;
+    for (int h = tid; h < a.H; h += 256) {
+        float rv[PF_RE], xv[PF_RT];
+#pragma unroll
+        for (int e = 0; e < PF_RE; e++) rv[e] = rows[e][h];
+#pragma unroll
+        for (int t = 0; t < PF_RT; t++) xv[t] = a.x[(int64_t)min(t0 + t, a.T - 1) * a.H + h];
+#pragma unroll
+        for (int t = 0; t < PF_RT; t++)
+#pragma unroll
+            for (int e = 0; e < PF_RE; e++) acc[t][e] = __builtin_fmaf(rv[e], xv[t], acc[t][e]);
+    }
+    const int o = tid >> 3, q = tid & 7;
+#pragma unroll
+    for (int rnd = 0; rnd < PF_RT * PF_RE / 32; rnd++) {
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            const int oo = rnd * 32 + i;
+            red[i][tid] = acc[oo / PF_RE][oo % PF_RE];
         }
+        __syncthreads();
+        float v[32];
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = red[o][q + 8 * i];
+#pragma unroll
+        for (int m = 16; m >= 1; m >>= 1)
+#pragma unroll
+            for (int i = 0; i < m; i++) v[i] = v[i] + v[i + m];
+        float w = v[0];
+        w = w + xlane<4>(w);
+        w = w + xlane<2>(w);
+        w = w + xlane<1>(w);
+        const int oo = rnd * 32 + o, t = t0 + oo / PF_RE, e = e0 + oo % PF_RE;
+        if (q == 0 && t < a.T && e < NR) {
+            if (e < a.E) a.logits[(int64_t)t * a.E + e] = a.bias ? w + a.bias[e] : w;
+            else a.glogit[t] = w;
+        }
+    }
 }
 
 // P2: one wave per token
@@ -74,147 +123,220 @@ __global__ __launch_bounds__(64) void k_pf_topk(PfArgs a) {
     topk_wave_any(a.logits + (int64_t)t * a.E, a.E, a.K, a.ids + t * a.K, a.wts + t * a.K);
 }
 
-// P3: one work-group.  Counting sort of the T*K pairs by expert (the order of
-// pairs inside an expert does not affect any result: every pair's output row
-// is computed on its own), the shared expert as expert E with all T tokens,
-// and the list of 32-pair tiles.
+// exclusive prefix sum of one int per thread over a 1024-thread group
+__device__ __forceinline__ int excl_scan1024(int v, int* wsum, int* total) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    int x = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d);
+        if (lane >= d) x += y;
+    }
+    if (lane == 63) wsum[w] = x;
+    __syncthreads();
+    if (w == 0) {
+        const int t = lane < 16 ? wsum[lane] : 0;
+        int sc = t;
+#pragma unroll
+        for (int d = 1; d < 16; d <<= 1) {
+            const int y = __shfl_up(sc, d);
+            if (lane >= d) sc += y;
+        }
+        __syncthreads();   // pairs with the barrier below for the other waves
+        if (lane < 16) wsum[lane] = sc - t;
+        if (lane == 15) *total = sc;
+    } else {
+        __syncthreads();
+    }
+    __syncthreads();
+    return x - v + wsum[w];
+}
+
+// P3: one 1024-thread work-group.  Counting sort of the T*K pairs by expert
+// (the order of pairs inside an expert does not affect any result: every
+// pair's output row is computed on its own), the shared expert as expert E
+// with all T tokens, and the list of 16-pair tiles.  Thread i owns experts
+// 2i and 2i+1 in the scans.
 __global__ __launch_bounds__(1024) void k_pf_plan(PfArgs a) {
-    __shared__ int cnt[MAX_E + 1], fill[MAX_E + 1], off[MAX_E + 2];
+    __shared__ int cnt[2 * 1024], fill[MAX_E + 1];
+    __shared__ int wsum[16], tot[2];
     const int tid = threadIdx.x, TK = a.T * a.K, NE = a.E + 1;
-    for (int e = tid; e < NE; e += 1024) { cnt[e] = 0; fill[e] = 0; }
+    for (int e = tid; e < 2 * 1024; e += 1024) cnt[e] = 0;
+    for (int e = tid; e < NE; e += 1024) fill[e] = 0;
     __syncthreads();
     for (int p = tid; p < TK; p += 1024) atomicAdd(&cnt[a.ids[p]], 1);
     if (tid == 0) cnt[a.E] = a.has_shared ? a.T : 0;
     __syncthreads();
-    if (tid == 0) {
-        int o = 0, nt = 0;
-        for (int e = 0; e < NE; e++) {
-            off[e] = o;
-            for (int s = 0; s < cnt[e]; s += PF_TILE) {
-                a.tiles[nt * 3] = e;
-                a.tiles[nt * 3 + 1] = o + s;
-                a.tiles[nt * 3 + 2] = min(PF_TILE, cnt[e] - s);
-                nt++;
-            }
-            o += cnt[e];
-        }
-        off[NE] = o;
-        *a.ntiles = nt;
-    }
+    const int c0 = cnt[2 * tid], c1 = cnt[2 * tid + 1];
+    const int n0 = (c0 + PF_TILE - 1) / PF_TILE, n1 = (c1 + PF_TILE - 1) / PF_TILE;
+    const int po = excl_scan1024(c0 + c1, wsum, &tot[0]);
+    const int to = excl_scan1024(n0 + n1, wsum, &tot[1]);
     __syncthreads();
-    for (int e = tid; e <= NE; e += 1024) a.off[e] = off[e];
+    cnt[2 * tid] = po;                 // cnt now holds each expert's first position
+    cnt[2 * tid + 1] = po + c0;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int e = 2 * tid + h, c = h ? c1 : c0, base = h ? po + c0 : po, tb = h ? to + n0 : to;
+        for (int s = 0; s * PF_TILE < c; s++) {
+            a.tiles[(tb + s) * 3] = e;
+            a.tiles[(tb + s) * 3 + 1] = base + s * PF_TILE;
+            a.tiles[(tb + s) * 3 + 2] = min(PF_TILE, c - s * PF_TILE);
+        }
+    }
+    if (tid == 0) *a.ntiles = tot[1];
+    __syncthreads();
     for (int p = tid; p < TK; p += 1024) {
         const int e = a.ids[p];
-        a.spairs[off[e] + atomicAdd(&fill[e], 1)] = p;
+        a.spairs[cnt[e] + atomicAdd(&fill[e], 1)] = p;
         if (a.ids_out) { a.ids_out[p] = e; a.w_out[p] = a.wts[p]; }
     }
     if (a.has_shared)
-        for (int t = tid; t < a.T; t += 1024) a.spairs[off[a.E] + t] = TK + t;
+        for (int t = tid; t < a.T; t += 1024) a.spairs[cnt[a.E] + t] = TK + t;
 }
 
-// ---- MFMA fragments.  v_mfma_i32_32x32x32_i8 layout: lane l supplies row
-// l%32 of A and column l%32 of B, elements 16*(l/32) .. +16 of the K=32
-// block; result D[i] at lane l is (row 8*(i/4) + 4*(l/32) + i%4, col l%32).
+// ---- grouped GEMM on v_mfma_i32_16x16x32_i8.  Layout: lane l supplies row
+// l%16 of A and column l%16 of B, elements 8*(l/16) .. +8 of the K = 32
+// block; result D[i] at lane l is (row 4*(l/16) + i, column l%16).  A = the
+// tile's 16 Q8_1 activation rows (pairs), B = 16 weight rows; one 32-element
+// quantization block per instruction, so each result is the exact int32
+// block dot.  Q4_0 enters as the unsigned nibbles and the accumulator starts
+// at -8 * sum(q_x) of the pair's block, which makes the result
+// sum((nib - 8) * q_x).
 
-// 16 activation quants of a decoded Q8_1 block in LDS (q bytes at +4)
-__device__ __forceinline__ v4i a_frag(const uint8_t* blk, int half) {
-    const uint32_t* w = (const uint32_t*)(blk + 4 + 16 * half);
-    v4i r;
-    r.x = (int)w[0]; r.y = (int)w[1]; r.z = (int)w[2]; r.w = (int)w[3];
-    return r;
-}
-
-// 16 weight values of a block row in LDS, as int8; Q4_0 gives the unsigned
-// nibbles (0..15), corrected by -8 * sum(q_x) after the MFMA
 template <int T>
-__device__ __forceinline__ v4i b_frag(const uint8_t* row, int b, int half, float* dw) {
-    v4i r;
+constexpr int pf_row_chunk_bytes() { return PF_CHUNK * QTraits<T>::BYTES; }
+
+// 8 weight values of block b of an LDS row as int8, and f32(d)
+template <int T>
+__device__ __forceinline__ long pf_b_frag(const uint8_t* row, int b, int q, float* dw) {
+    uint32_t lo, hi;
     if constexpr (T == T_Q4_0) {
         const int off = b * 18;
         *dw = h2f(lds_u16(row, off));
-        const int sh = 4 * half;
-        r.x = (int)((lds_u32(row, off + 2) >> sh) & 0x0F0F0F0Fu);
-        r.y = (int)((lds_u32(row, off + 6) >> sh) & 0x0F0F0F0Fu);
-        r.z = (int)((lds_u32(row, off + 10) >> sh) & 0x0F0F0F0Fu);
-        r.w = (int)((lds_u32(row, off + 14) >> sh) & 0x0F0F0F0Fu);
+        const int o = off + 2 + 8 * (q & 1), sh = 4 * (q >> 1);
+        lo = (lds_u32(row, o) >> sh) & 0x0F0F0F0Fu;
+        hi = (lds_u32(row, o + 4) >> sh) & 0x0F0F0F0Fu;
     } else {
         const int off = b * 34;
         *dw = h2f(lds_u16(row, off));
-        const int q = off + 2 + 16 * half;
-        r.x = (int)lds_u32(row, q);
-        r.y = (int)lds_u32(row, q + 4);
-        r.z = (int)lds_u32(row, q + 8);
-        r.w = (int)lds_u32(row, q + 12);
+        lo = lds_u32(row, off + 2 + 8 * q);
+        hi = lds_u32(row, off + 6 + 8 * q);
     }
-    return r;
+    return (long)(((uint64_t)hi << 32) | lo);
 }
 
-// Stages, for one K chunk: `nrows` weight rows (global stride rb, chunk bytes
-// cbytes at goff) into wlds, and the chunk of the tile's Q8_1 rows (src row
-// stride xstride, 36*PF_CHUNK bytes at xoff) into xlds.
-__device__ __forceinline__ void pf_stage(uint8_t* wlds, const uint8_t* w, int64_t rb, int nrows, int cbytes,
-                                         uint8_t* xlds, const uint8_t* xsrc, const int* xrows, int64_t xstride,
+// Per-block metadata of the staged activation blocks (PF_TILE pairs x
+// PF_CHUNK blocks, pair-major, 36 bytes each): xd[b][m] = f32(d),
+// xs8[b][m] = -8 * sum(q) (Q4_0 correction; the MFMA accumulator's start)
+__device__ __forceinline__ void pf_xmeta(const uint8_t* xl, float* xd, int* xs8) {
+    const int i = threadIdx.x;
+    if (i < PF_TILE * PF_CHUNK) {
+        const int m = i / PF_CHUNK, b = i % PF_CHUNK;
+        const uint8_t* blk = xl + i * 36;
+        int s = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) s = dot4(*(const int*)(blk + 4 + 4 * k), 0x01010101, s);
+        xs8[b * PF_TILE + m] = -8 * s;
+        xd[b * PF_TILE + m] = h2f(*(const uint16_t*)blk);
+    }
+}
+
+// Issues (asynchronously) one K chunk: `nrows` weight rows of `cbytes`
+// bytes (global stride rb) and the tile's PF_TILE activation rows (row
+// xrows[m] of src, stride xstride, chunk at byte xoff).
+__device__ __forceinline__ void pf_issue(uint8_t* wl, const uint8_t* w, int64_t rb, int nrows, int cbytes,
+                                         uint8_t* xl, const uint8_t* xsrc, const int* xrows, int64_t xstride,
                                          int64_t xoff) {
-    stage_rows(wlds, w, rb, nrows, cbytes, threadIdx.x, PF_THREADS);
-    // Q8_1 rows of the tile: 288 bytes each (18 pieces of 16 B), row index per pair
+    stage_rows(wl, w, rb, nrows, cbytes, threadIdx.x, PF_THREADS);
     constexpr int PER = 36 * PF_CHUNK / 16;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int c0 = wave * 64; c0 < PF_TILE * PER; c0 += 4 * 64) {
+    for (int c0 = wave * 64; c0 < PF_TILE * PER; c0 += PF_THREADS) {
         const int c = c0 + lane;
         if (c < PF_TILE * PER) {
             const int r = c / PER, col = c - r * PER;
             __builtin_amdgcn_global_load_lds((const glb_void_t*)(xsrc + xrows[r] * xstride + xoff + col * 16),
-                                             (lds_void_t*)(xlds + c0 * 16), 16, 0, 0);
+                                             (lds_void_t*)(xl + c0 * 16), 16, 0, 0);
         }
     }
 }
 
-// 8 * sum of the 32 quants and f32(d) of every Q8_1 block in xlds
-__device__ __forceinline__ void pf_xmeta(const uint8_t* xlds, int* xs8, float* xd) {
-    const int i = threadIdx.x;   // PF_TILE * PF_CHUNK = 256 blocks, one per thread
-    const uint8_t* blk = xlds + i * 36;
-    int s = 0;
-#pragma unroll
-    for (int k = 0; k < 8; k++) s = dot4(*(const int*)(blk + 4 + 4 * k), 0x01010101, s);
-    xs8[i] = 8 * s;
-    xd[i] = h2f(*(const uint16_t*)blk);
-}
-
-// One K chunk of a wave's 32x32 output tile: rows = pairs (A from xlds),
-// columns = its 32 weight rows (B from wrows, row stride cbytes).
-template <int T>
-__device__ __forceinline__ void pf_mma_chunk(const uint8_t* xlds, const int* xs8, const float* xd,
-                                             const uint8_t* wrows, int cbytes, int nb, float (&acc)[16]) {
-    const int lane = threadIdx.x & 63, half = lane >> 5, col = lane & 31;
-    const uint8_t* wrow = wrows + col * cbytes;
+// One staged K chunk for a wave's NTN 16-row column tiles (weight rows
+// wrows + 16*n, LDS row stride cbytes): acc[n][i] = output (pair 4*(l/16)+i,
+// row 16n + l%16), updated per block as fmaf(f32(d_w)*f32(d_x), sumi, acc).
+template <int T, int NTN>
+__device__ __forceinline__ void pf_mma_chunk(const uint8_t* xl, const float* xd, const int* xs8,
+                                             const uint8_t* wrows, int cbytes, int nb, float (&acc)[NTN][4]) {
+    const int lane = threadIdx.x & 63, q = lane >> 4, c = lane & 15;
     for (int b = 0; b < nb; b++) {
-        float dw;
-        const v4i bf = b_frag<T>(wrow, b, half, &dw);
-        const v4i af = a_frag(xlds + ((lane & 31) * PF_CHUNK + b) * 36, half);
-        v16i c = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-        c = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf, c, 0, 0, 0);
+        const uint8_t* ab = xl + (c * PF_CHUNK + b) * 36 + 4 + 8 * q;
+        const long af = (long)(((uint64_t) * (const uint32_t*)(ab + 4) << 32) | *(const uint32_t*)ab);
+        const float4 dx = *(const float4*)(xd + b * PF_TILE + 4 * q);
+        v4i c0 = {0, 0, 0, 0};
+        if constexpr (T == T_Q4_0) c0 = *(const v4i*)(xs8 + b * PF_TILE + 4 * q);
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int m = 8 * (i >> 2) + 4 * half + (i & 3);
-            int s = c[i];
-            if constexpr (T == T_Q4_0) s -= xs8[m * PF_CHUNK + b];
-            acc[i] = __builtin_fmaf(dw * xd[m * PF_CHUNK + b], (float)s, acc[i]);
+        for (int n = 0; n < NTN; n++) {
+            float dw;
+            const long bf = pf_b_frag<T>(wrows + (16 * n + c) * cbytes, b, q, &dw);
+            const v4i r = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bf, c0, 0, 0, 0);
+            acc[n][0] = __builtin_fmaf(dw * dx.x, (float)r[0], acc[n][0]);
+            acc[n][1] = __builtin_fmaf(dw * dx.y, (float)r[1], acc[n][1]);
+            acc[n][2] = __builtin_fmaf(dw * dx.z, (float)r[2], acc[n][2]);
+            acc[n][3] = __builtin_fmaf(dw * dx.w, (float)r[3], acc[n][3]);
         }
     }
 }
 
-// P4: grid (F/64, max_tiles).  Waves 0,1: gate/up rows f0..f0+31; waves 2,3:
-// gate/up rows f0+32..f0+63; then h = silu(gate)*up and Q8_1 of its two
-// 32-row blocks per pair.
+// Double-buffered K loop of one work-group: nwrows weight rows starting at
+// w0 (and w1 for the second half when split, see callers), activation rows
+// xrows of xsrc; wave `wave` computes NTN 16-row tiles at LDS row wrow0.
+template <int T, int NTN>
+__device__ __forceinline__ void pf_gemm(uint8_t* wl, uint8_t* xl, float* xd, int* xs8, const uint8_t* w0, int n0,
+                                        const uint8_t* w1, int n1, int64_t rb, int nbk, const uint8_t* xsrc,
+                                        const int* xrows, int64_t xstride, int wrow0, float (&acc)[NTN][4]) {
+    constexpr int CB = pf_row_chunk_bytes<T>();
+    const int nrows = n0 + n1;
+    const int WST = nrows * CB + 16, XST = PF_TILE * PF_CHUNK * 36;
+#pragma unroll
+    for (int n = 0; n < NTN; n++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[n][i] = 0.0f;
+    const int nc = nbk / PF_CHUNK;
+    auto issue = [&](int c, int buf) {
+        const int64_t goff = (int64_t)c * CB;
+        uint8_t* wb = wl + buf * WST;
+        stage_rows(wb, w0 + goff, rb, n0, CB, threadIdx.x, PF_THREADS);
+        pf_issue(wb + n0 * CB, w1 + goff, rb, n1, CB, xl + buf * XST, xsrc, xrows, xstride,
+                 (int64_t)c * PF_CHUNK * 36);
+    };
+    issue(0, 0);
+    for (int c = 0; c < nc; c++) {
+        const int buf = c & 1;
+        lds_copy_wait();
+        __syncthreads();   // chunk c landed; every wave is done with chunk c-1
+        pf_xmeta(xl + buf * XST, xd + buf * PF_TILE * PF_CHUNK, xs8 + buf * PF_TILE * PF_CHUNK);
+        if (c + 1 < nc) issue(c + 1, buf ^ 1);
+        __syncthreads();
+        pf_mma_chunk<T, NTN>(xl + buf * XST, xd + buf * PF_TILE * PF_CHUNK, xs8 + buf * PF_TILE * PF_CHUNK,
+                             wl + buf * WST + wrow0 * CB, CB, PF_CHUNK, acc);
+    }
+}
+
+template <int T>
+constexpr int pf_wst(int nrows) { return nrows * pf_row_chunk_bytes<T>() + 16; }
+constexpr int PF_XST = PF_TILE * PF_CHUNK * 36;
+
+// P4: grid (F/64, max_tiles).  Waves 0, 1: gate rows f0 + [0,32), up rows
+// f0 + [0,32); waves 2, 3: the same for f0 + [32, 64) (two 16-row tiles per
+// wave); then h = silu(gate) * up and Q8_1 of its two 32-row blocks per pair.
 template <int TE, int TS>
 __global__ __launch_bounds__(PF_THREADS) void k_pf_gate_up(PfArgs a) {
-    constexpr int WB = (QTraits<TE>::BYTES > QTraits<TS>::BYTES ? QTraits<TE>::BYTES : QTraits<TS>::BYTES);
-    __shared__ __attribute__((aligned(16))) uint8_t wlds[128 * PF_CHUNK * WB + 16];
-    __shared__ __attribute__((aligned(16))) uint8_t xlds[PF_TILE * PF_CHUNK * 36 + 16];
-    __shared__ int xs8[PF_TILE * PF_CHUNK];
-    __shared__ float xd[PF_TILE * PF_CHUNK];
+    constexpr int WS = pf_wst<TE>(128) > pf_wst<TS>(128) ? pf_wst<TE>(128) : pf_wst<TS>(128);
+    __shared__ __attribute__((aligned(16))) uint8_t wl[2 * WS];
+    __shared__ __attribute__((aligned(16))) uint8_t xl[2 * PF_XST];
+    __shared__ __attribute__((aligned(16))) float xd[2 * PF_TILE * PF_CHUNK];
+    __shared__ __attribute__((aligned(16))) int xs8[2 * PF_TILE * PF_CHUNK];
     __shared__ int prs[PF_TILE], xrows[PF_TILE];
-    __shared__ float gu[2][PF_TILE][64];
+    __shared__ float gu[2][PF_TILE][65];
     const int ti = blockIdx.y;
     if (ti >= *a.ntiles) return;
     const int e = a.tiles[ti * 3], start = a.tiles[ti * 3 + 1], n = a.tiles[ti * 3 + 2];
@@ -224,31 +346,18 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_gate_up(PfArgs a) {
         prs[tid] = p;
         xrows[tid] = p < TK ? p / a.K : p - TK;
     }
+    __syncthreads();
     const bool sh = e == a.E;
     const int f0 = blockIdx.x * 64;
     const int wave = tid >> 6, mat = wave & 1, rh = wave >> 1;
-    float acc[16];
-#pragma unroll
-    for (int i = 0; i < 16; i++) acc[i] = 0.0f;
-    const int nbk = a.H / QK;
+    float acc[2][4];
     auto run = [&](auto tag) {
         constexpr int T = decltype(tag)::value;
         const int64_t rb = row_bytes(T, a.H);
         const uint8_t* g = sh ? a.sh_gate : a.gate + (int64_t)e * a.sg;
         const uint8_t* u = sh ? a.sh_up : a.up + (int64_t)e * a.su;
-        const int cbytes = PF_CHUNK * QTraits<T>::BYTES;
-        for (int b0 = 0; b0 < nbk; b0 += PF_CHUNK) {
-            __syncthreads();
-            const int64_t goff = (int64_t)b0 * QTraits<T>::BYTES;
-            stage_rows(wlds, g + f0 * rb + goff, rb, 64, cbytes, tid, PF_THREADS);
-            pf_stage(wlds + 64 * cbytes, u + f0 * rb + goff, rb, 64, cbytes, xlds, a.xq, xrows, a.xq_stride,
-                     (int64_t)b0 * 36);
-            lds_copy_wait();
-            __syncthreads();
-            pf_xmeta(xlds, xs8, xd);
-            __syncthreads();
-            pf_mma_chunk<T>(xlds, xs8, xd, wlds + (mat * 64 + rh * 32) * cbytes, cbytes, PF_CHUNK, acc);
-        }
+        pf_gemm<T, 2>(wl, xl, xd, xs8, g + f0 * rb, 64, u + f0 * rb, 64, rb, a.H / QK, a.xq, xrows, a.xq_stride,
+                      mat * 64 + rh * 32, acc);
     };
     if (sh) {
         if constexpr (TS == T_Q4_0) run(std::integral_constant<int, T_Q4_0>{});
@@ -258,14 +367,16 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_gate_up(PfArgs a) {
         else run(std::integral_constant<int, T_Q8_0>{});
     }
     {
-        const int lane = tid & 63, half = lane >> 5, col = lane & 31;
+        const int lane = tid & 63, q = lane >> 4, c = lane & 15;
 #pragma unroll
-        for (int i = 0; i < 16; i++) gu[mat][8 * (i >> 2) + 4 * half + (i & 3)][rh * 32 + col] = acc[i];
+        for (int nn = 0; nn < 2; nn++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) gu[mat][4 * q + i][rh * 32 + 16 * nn + c] = acc[nn][i];
     }
     __syncthreads();
     // Q8_1(h) of the two 32-row blocks for each pair: one half-wave per (pair, block)
-    for (int q = tid >> 5; q < 2 * n; q += PF_THREADS / 32) {
-        const int m = q >> 1, blk = q & 1, i = tid & 31;
+    for (int qq = tid >> 5; qq < 2 * n; qq += PF_THREADS / 32) {
+        const int m = qq >> 1, blk = qq & 1, i = tid & 31;
         const float xi = det_silu(gu[0][m][blk * 32 + i]) * gu[1][m][blk * 32 + i];
         const float amax = bfly32_max(__builtin_fabsf(xi)), sum = bfly32_sum(xi);
         const float d = amax / 127.0f;
@@ -276,43 +387,31 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_gate_up(PfArgs a) {
     }
 }
 
-// P5: grid (H/128, max_tiles).  Wave w: down rows r0 + 32w .. +31 for the
-// tile's 32 pairs; K = F.
+// P5: grid (H/128, max_tiles).  Wave w: down rows r0 + 32w .. +31 (two
+// 16-row tiles) for the tile's 16 pairs; K = F.
 template <int TE, int TS>
 __global__ __launch_bounds__(PF_THREADS) void k_pf_down(PfArgs a) {
-    constexpr int WB = (QTraits<TE>::BYTES > QTraits<TS>::BYTES ? QTraits<TE>::BYTES : QTraits<TS>::BYTES);
-    __shared__ __attribute__((aligned(16))) uint8_t wlds[128 * PF_CHUNK * WB + 16];
-    __shared__ __attribute__((aligned(16))) uint8_t xlds[PF_TILE * PF_CHUNK * 36 + 16];
-    __shared__ int xs8[PF_TILE * PF_CHUNK];
-    __shared__ float xd[PF_TILE * PF_CHUNK];
+    constexpr int WS = pf_wst<TE>(128) > pf_wst<TS>(128) ? pf_wst<TE>(128) : pf_wst<TS>(128);
+    __shared__ __attribute__((aligned(16))) uint8_t wl[2 * WS];
+    __shared__ __attribute__((aligned(16))) uint8_t xl[2 * PF_XST];
+    __shared__ __attribute__((aligned(16))) float xd[2 * PF_TILE * PF_CHUNK];
+    __shared__ __attribute__((aligned(16))) int xs8[2 * PF_TILE * PF_CHUNK];
     __shared__ int prs[PF_TILE];
     const int ti = blockIdx.y;
     if (ti >= *a.ntiles) return;
     const int e = a.tiles[ti * 3], start = a.tiles[ti * 3 + 1], n = a.tiles[ti * 3 + 2];
     const int tid = threadIdx.x;
     if (tid < PF_TILE) prs[tid] = a.spairs[start + min(tid, n - 1)];
+    __syncthreads();
     const bool sh = e == a.E;
     const int r0 = blockIdx.x * 128, wave = tid >> 6;
-    float acc[16];
-#pragma unroll
-    for (int i = 0; i < 16; i++) acc[i] = 0.0f;
-    const int nbk = a.F / QK;
+    float acc[2][4];
     auto run = [&](auto tag) {
         constexpr int T = decltype(tag)::value;
         const int64_t rb = row_bytes(T, a.F);
         const uint8_t* d = sh ? a.sh_down : a.down + (int64_t)e * a.sd;
-        for (int b0 = 0; b0 < nbk; b0 += PF_CHUNK) {
-            const int cb = min(PF_CHUNK, nbk - b0);
-            const int cbytes = cb * QTraits<T>::BYTES;
-            __syncthreads();
-            pf_stage(wlds, d + r0 * rb + (int64_t)b0 * QTraits<T>::BYTES, rb, 128, cbytes, xlds, a.hq, prs,
-                     a.hq_stride, (int64_t)b0 * 36);
-            lds_copy_wait();
-            __syncthreads();
-            pf_xmeta(xlds, xs8, xd);
-            __syncthreads();
-            pf_mma_chunk<T>(xlds, xs8, xd, wlds + wave * 32 * cbytes, cbytes, cb, acc);
-        }
+        pf_gemm<T, 2>(wl, xl, xd, xs8, d + r0 * rb, 128, d, 0, rb, a.F / QK, a.hq, prs, a.hq_stride, wave * 32,
+                      acc);
     };
     if (sh) {
         if constexpr (TS == T_Q4_0) run(std::integral_constant<int, T_Q4_0>{});
@@ -321,12 +420,14 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_down(PfArgs a) {
         if constexpr (TE == T_Q4_0) run(std::integral_constant<int, T_Q4_0>{});
         else run(std::integral_constant<int, T_Q8_0>{});
     }
-    const int lane = tid & 63, half = lane >> 5, col = lane & 31;
+    const int lane = tid & 63, q = lane >> 4, c = lane & 15;
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const int m = 8 * (i >> 2) + 4 * half + (i & 3);
-        if (m < n) a.dn[(int64_t)prs[m] * a.H + r0 + wave * 32 + col] = acc[i];
-    }
+    for (int nn = 0; nn < 2; nn++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = 4 * q + i;
+            if (m < n) a.dn[(int64_t)prs[m] * a.H + r0 + wave * 32 + 16 * nn + c] = acc[nn][i];
+        }
 }
 
 // P6: grid (ceil(H/256), T): out = sum_k fmaf(w_k, dn_k, acc) (+ shared expert)
@@ -349,7 +450,7 @@ void launch_quantize_q8_1(const float* x, void* out, int64_t ncols, int64_t ncol
                           hipStream_t s);
 
 struct PfPlan {
-    size_t logits, glogit, ids, wts, xq, off, spairs, tiles, ntiles, hq, dn, total;
+    size_t logits, glogit, ids, wts, xq, spairs, tiles, ntiles, hq, dn, total;
     int64_t xq_stride, hq_stride;
     int max_tiles;
 };
@@ -368,7 +469,6 @@ static PfPlan plan_pf(int H, int F, int E, int K, int T) {
     p.ids = o; o += al256p((size_t)T * K * 4);
     p.wts = o; o += al256p((size_t)T * K * 4);
     p.xq = o; o += al256p((size_t)T * p.xq_stride);
-    p.off = o; o += al256p((size_t)(E + 2) * 4);
     p.spairs = o; o += al256p(P * 4);
     p.tiles = o; o += al256p((size_t)p.max_tiles * 3 * 4);
     p.ntiles = o; o += al256p(4);
@@ -380,8 +480,8 @@ static PfPlan plan_pf(int H, int F, int E, int K, int T) {
 
 template <int TE, int TS>
 static void launch_pf(const PfArgs& a, const PfPlan& p, hipStream_t s) {
-    hipLaunchKernelGGL(k_pf_router, dim3(a.E + (a.sh_gate_w ? 1 : 0), (a.T + MAX_TOK - 1) / MAX_TOK), dim3(256), 0, s,
-                       a);
+    hipLaunchKernelGGL(k_pf_router, dim3((a.E + (a.sh_gate_w ? 1 : 0) + PF_RE - 1) / PF_RE, (a.T + PF_RT - 1) / PF_RT),
+                       dim3(256), 0, s, a);
     launch_quantize_q8_1(a.x, a.xq, a.H, p.xq_stride / Q8_1_BYTES * QK, a.T, s);
     hipLaunchKernelGGL(k_pf_topk, dim3(a.T), dim3(64), 0, s, a);
     hipLaunchKernelGGL(k_pf_plan, dim3(1), dim3(1024), 0, s, a);
@@ -440,7 +540,7 @@ void chimere_moe_prefill(const chimere_moe_layer* L, const float* x, float* out,
     a.ids_out = ids_out; a.w_out = w_out;
     a.logits = (float*)(w + p.logits); a.glogit = (float*)(w + p.glogit);
     a.ids = (int*)(w + p.ids); a.wts = (float*)(w + p.wts);
-    a.xq = w + p.xq; a.off = (int*)(w + p.off); a.spairs = (int*)(w + p.spairs);
+    a.xq = w + p.xq; a.spairs = (int*)(w + p.spairs);
     a.tiles = (int*)(w + p.tiles); a.ntiles = (int*)(w + p.ntiles);
     a.hq = w + p.hq; a.dn = (float*)(w + p.dn);
     a.xq_stride = p.xq_stride; a.hq_stride = p.hq_stride; a.max_tiles = p.max_tiles;
