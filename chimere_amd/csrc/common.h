@@ -444,6 +444,19 @@ __device__ __forceinline__ float xlane(float v) {
     return __builtin_bit_cast(float, xlane<M>(__builtin_bit_cast(int, v)));
 }
 
+// Maximum of a non-negative int over the wave, returned wave-uniform: DPP
+// prefix maximum (row_shr 1, 2, 4, 8 inside each 16-lane row, then
+// row_bcast 15 / 31 across rows) leaves the total in lane 63.
+__device__ __forceinline__ int wave_max_nonneg(int v) {
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false));   // row_shr:1
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false));   // row_shr:2
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false));   // row_shr:4
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false));   // row_shr:8
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false));   // row_bcast:15
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false));   // row_bcast:31
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
 // Sum over the 16 lanes of a row group in the halving-tree order
 // (xor 8, 4, 2, 1); every lane of the group ends with the same value.
 __device__ __forceinline__ float slot_reduce16(float v) {

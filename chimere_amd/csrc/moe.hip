@@ -180,44 +180,57 @@ __device__ __forceinline__ void route_plan(const MoeArgs& a, int* first, Plan& p
 
     const int wave = tid >> 6;
     if (wave < a.M) topk_wave_any(a.logits + wave * a.E, a.E, a.K, s_ids + wave * a.K, s_w + wave * a.K);
-    // distinct-expert plan, built in parallel: the first pair (lowest
-    // t*K+k) selecting an expert numbers it by its rank among first pairs;
-    // the order of pairs inside an expert does not affect any result.
-    __shared__ int s_fcnt[2], s_cnt[MAX_TOK * MAX_K];
-    for (int e = tid; e < a.E; e += EX_THREADS) first[e] = 0x7fffffff;
-    if (tid < MAX_TOK * MAX_K) s_cnt[tid] = 0;
-    __syncthreads();
-    if (tid < MK) atomicMin(&first[s_ids[tid]], tid);
-    __syncthreads();
-    int fp = 0;
-    bool isfirst = false;
-    if (tid < 128) {
-        fp = tid < MK ? first[s_ids[tid]] : -1;
-        isfirst = tid < MK && fp == tid;
-        const uint64_t m = __ballot(isfirst);
-        if ((tid & 63) == 0) s_fcnt[tid >> 6] = __popcll(m);
-        const int lrank = __popcll(m & ((1ull << (tid & 63)) - 1));
+    if (a.M == 1) {
+        // one token: its K experts are distinct; unit k = the k-th selected
         __syncthreads();
-        const int rank = lrank + ((tid >> 6) ? s_fcnt[0] : 0);
-        if (isfirst) { pl.uexp[rank] = s_ids[tid]; s_cnt[tid] = rank; }   // s_cnt: first pair -> unit
-        if (tid == 0) pl.nu = s_fcnt[0] + (MK > 64 ? s_fcnt[1] : 0);
+        if (tid < MK) {
+            pl.uexp[tid] = s_ids[tid];
+            pl.untok[tid] = 1;
+            pl.upair[tid][0] = tid;
+            pl.utok[tid][0] = 0;
+        }
+        if (tid == 0) pl.nu = MK;
+        __syncthreads();
     } else {
+        // distinct-expert plan, built in parallel: the first pair (lowest
+        // t*K+k) selecting an expert numbers it by its rank among first pairs;
+        // the order of pairs inside an expert does not affect any result.
+        __shared__ int s_fcnt[2], s_cnt[MAX_TOK * MAX_K];
+        for (int e = tid; e < a.E; e += EX_THREADS) first[e] = 0x7fffffff;
+        if (tid < MAX_TOK * MAX_K) s_cnt[tid] = 0;
+        __syncthreads();
+        if (tid < MK) atomicMin(&first[s_ids[tid]], tid);
+        __syncthreads();
+        int fp = 0;
+        bool isfirst = false;
+        if (tid < 128) {
+            fp = tid < MK ? first[s_ids[tid]] : -1;
+            isfirst = tid < MK && fp == tid;
+            const uint64_t m = __ballot(isfirst);
+            if ((tid & 63) == 0) s_fcnt[tid >> 6] = __popcll(m);
+            const int lrank = __popcll(m & ((1ull << (tid & 63)) - 1));
+            __syncthreads();
+            const int rank = lrank + ((tid >> 6) ? s_fcnt[0] : 0);
+            if (isfirst) { pl.uexp[rank] = s_ids[tid]; s_cnt[tid] = rank; }   // s_cnt: first pair -> unit
+            if (tid == 0) pl.nu = s_fcnt[0] + (MK > 64 ? s_fcnt[1] : 0);
+        } else {
+            __syncthreads();
+        }
+        __syncthreads();
+        int uu = 0;
+        if (tid < MK) uu = s_cnt[fp];
+        __syncthreads();
+        if (tid < MAX_TOK * MAX_K) s_cnt[tid] = 0;
+        __syncthreads();
+        if (tid < MK) {
+            const int n = atomicAdd(&s_cnt[uu], 1);
+            pl.upair[uu][n] = tid;
+            pl.utok[uu][n] = tid / a.K;
+        }
+        __syncthreads();
+        if (tid < pl.nu) pl.untok[tid] = s_cnt[tid];
         __syncthreads();
     }
-    __syncthreads();
-    int uu = 0;
-    if (tid < MK) uu = s_cnt[fp];
-    __syncthreads();
-    if (tid < MAX_TOK * MAX_K) s_cnt[tid] = 0;
-    __syncthreads();
-    if (tid < MK) {
-        const int n = atomicAdd(&s_cnt[uu], 1);
-        pl.upair[uu][n] = tid;
-        pl.utok[uu][n] = tid / a.K;
-    }
-    __syncthreads();
-    if (tid < pl.nu) pl.untok[tid] = s_cnt[tid];
-    __syncthreads();
     if (publish) {
         const int nu = pl.nu;
         for (int i = tid; i < MK; i += EX_THREADS) {
@@ -247,11 +260,14 @@ __device__ __forceinline__ void expert_item(const MoeArgs& a, uint8_t* tile, XLd
     const int r0 = w * QK;
     RegBlk<T> db[EX_MAX_RPT];
     float acc[1][NT];
-    load_down_blocks<T>(db, down, row_bytes(T, a.F), w, a.H);
     const int64_t rb = row_bytes(T, a.H);
     tile_gemv<T, NT, EX_RG, 1>(tile, &xs[0][0], grid, gate + r0 * rb, QK, up + r0 * rb, QK, rb, a.H, a.xq, a.xq_stride, toks,
                                ntok, acc, PHASE_PTR(1, 5));
     PHASE(1, 3);
+    // the down column slice is requested only now, behind the gate/up rows
+    // (its pieces are prefetched into L2 by the idle work-groups of this XCD)
+    load_down_blocks<T>(db, down, row_bytes(T, a.F), w, a.H);
+    PHASE(1, 8);
     const int g = tid >> 4, j = tid & 15;
 #pragma unroll
     for (int t = 0; t < NT; t++) {
@@ -324,17 +340,40 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert(MoeArgs a) {
 
     const int NB = a.F / QK;
     const int MK = a.M * a.K;
-    const int NI = 8 * ((MK + 1 + 7) / 8) * NB;
     const int tid = threadIdx.x;
     PHASE(1, 0);
     route_plan(a, (int*)tile, pl, s_ids, s_w, blockIdx.x == 0);
     if constexpr (TE == T_IQ3_S || TS == T_IQ3_S)
         for (int i = tid; i < 512; i += EX_THREADS) grid[i] = c_iq3s_grid_moe[i];
     PHASE(1, 2);
-    for (int V = blockIdx.x; V < NI; V += gridDim.x) {
-        const int li = V >> 3, u = (V & 7) + 8 * (li / NB), w = li % NB;
-        const bool shared = u == MK;
-        if (u > MK || (shared && !a.has_shared) || (!shared && u >= pl.nu)) continue;
+    // Items of XCD x (work-groups b with b % 8 == x): the row blocks of the
+    // routed units u = x, x+8, ... then the shared unit's blocks w = x, x+8, ...
+    // Work-groups without an item prefetch the down matrices those items read
+    // (their column slices are scattered 18..34-byte pieces: from L2 they cost
+    // only the per-request issue time, from HBM a full memory latency each).
+    const int x = blockIdx.x & 7, lb = blockIdx.x >> 3, G8 = gridDim.x >> 3;
+    const int nr = pl.nu > x ? (pl.nu - 1 - x) / 8 + 1 : 0;
+    const int ns = a.has_shared ? (NB > x ? (NB - 1 - x) / 8 + 1 : 0) : 0;
+    const int nx = nr * NB + ns;
+    if (lb >= nx) {
+        const int nh = G8 - nx, hb = lb - nx;
+        const int64_t mb = (int64_t)a.H * row_bytes(TE, a.F), sb = (int64_t)a.H * row_bytes(TS, a.F);
+        const int64_t total = nr * mb + (ns ? sb : 0);
+        const int64_t c0 = total * hb / nh, c1 = total * (hb + 1) / nh;
+        uint32_t sink = 0;
+        for (int64_t o = c0 + 64 * (int64_t)tid; o < c1; o += 64 * EX_THREADS) {   // one 2-byte load per 64 bytes
+            const int m = (int)(o / mb);
+            const uint8_t* base = m < nr ? a.down + (int64_t)pl.uexp[x + 8 * m] * a.sd : a.sh_down;
+            const int64_t off = m < nr ? o - (int64_t)m * mb : o - (int64_t)nr * mb;
+            sink += *(const uint16_t*)(base + (off & ~(int64_t)1));   // weights are 2-byte aligned
+        }
+        if (a.H < 0) a.plan[0] = (int)sink;   // never taken: keeps the loads
+        return;
+    }
+    for (int i = lb; i < nx; i += G8) {
+        const bool shared = i >= nr * NB;
+        const int u = shared ? MK : x + 8 * (i / NB);
+        const int w = shared ? x + 8 * (i - nr * NB) : i % NB;
         const int ntok = shared ? a.M : pl.untok[u];
         __syncthreads();   // the previous item's readers of toks / pairs / hx are done
         if (tid < ntok) {
@@ -643,12 +682,10 @@ static int expert_grid(int items) {
 // stage < 0: all three kernels; 0, 1, 2: only K1, K2 or K3
 template <int TE, int TS, int NT>
 static void launch_layer_nt(const MoeArgs& a, int stage, hipStream_t s) {
-    const int NB = a.F / QK, NU = a.M * a.K + 1;
     if (stage < 0 || stage == 0)
         hipLaunchKernelGGL((k_moe_route<NT>), dim3(a.E + (a.sh_gate_w ? 1 : 0) + a.M), dim3(256), 0, s, a);
     if (stage < 0 || stage == 1)
-        hipLaunchKernelGGL((k_moe_expert<TE, TS, NT>), dim3(expert_grid(8 * ((NU + 7) / 8) * NB)), dim3(EX_THREADS), 0,
-                           s, a);
+        hipLaunchKernelGGL((k_moe_expert<TE, TS, NT>), dim3(expert_grid(256)), dim3(EX_THREADS), 0, s, a);
     if (stage < 0 || stage == 2)
         hipLaunchKernelGGL(k_moe_combine, dim3((a.H + TILE_ROWS - 1) / TILE_ROWS), dim3(GEMV_THREADS), 0, s, a);
 }

@@ -70,13 +70,12 @@ __device__ __forceinline__ void f32_row_dot(const float* __restrict__ a, const f
 // 512..64 pair values inside a lane, strides 32..1 pair lanes; padding adds
 // +0, which leaves the non-negative partial sums unchanged).
 // Selection: the reference takes k rounds of arg-max by probability with ties
-// to the lowest index, i.e. the K largest keys (p, -index).  Here the K-th
-// largest key is found by a radix select over 41-bit keys
-// (f32 bits of p << 11 | 1024 - index) with ballot counts, then each selected
-// entry's rank is the number of larger keys -- same set, same order, no
-// cross-lane shuffles in the loop.  Weights are renormalised by the
-// sequential sum of the selected probabilities (rank order).  Lane k < K
-// writes entry k.  Requires E <= 1024, K <= E.
+// to the lowest index; so does this, in registers: a round takes the wave
+// maximum of the keys f32bits(p) + 1 (0 marks a taken or padding entry; p >= 0
+// so the key order is the order of p; keys < 2^31) by a DPP scan, the lowest index
+// holding it (ballots over l, l+64, ...), and clears that entry.  Weights are
+// renormalised by the sequential sum of the selected probabilities (round
+// order).  Lane k < K writes entry k.  Requires E <= 1024, K <= min(E, 64).
 template <int NV>
 __device__ __forceinline__ void topk_wave(const float* __restrict__ logits, int E, int K,
                                           int* __restrict__ idx_out, float* __restrict__ w_out) {
@@ -102,42 +101,32 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ logits, int 
     float s = p[0];
     s = bfly32_sum(s + xlane<32>(s));
     // s equals lane 0's value of the halving tree on every lane
-    uint64_t key[NV];
+    uint32_t key[NV];
 #pragma unroll
     for (int i = 0; i < NV; i++) {
         const int j = lane + 64 * i;
         p[i] = s > 0.0f ? ev[i] / s : 1.0f / (float)E;
-        key[i] = j < E ? (((uint64_t)__builtin_bit_cast(uint32_t, p[i])) << 11) | (uint64_t)(1024 - j) : 0;
+        key[i] = j < E ? __builtin_bit_cast(uint32_t, p[i]) + 1u : 0u;
     }
-    // radix select of the K-th largest key (p <= 1, so the f32 bits fit in 30 bits)
-    // (stops as soon as exactly K keys reach the candidate: the set is fixed then)
-    uint64_t T = 0;
-    for (int b = 40; b >= 0; b--) {
-        const uint64_t cand = T | (1ull << b);
-        int cnt = 0;
-#pragma unroll
-        for (int i = 0; i < NV; i++) cnt += __popcll(__ballot(key[i] >= cand));
-        if (cnt >= K) T = cand;
-        if (cnt == K) break;
-    }
-    // rank each selected entry: rank = number of keys larger than it
     int my_idx = 0;
     float my_w = 0.0f;
+    for (int k = 0; k < K; k++) {
+        int m = (int)key[0];
 #pragma unroll
-    for (int i = 0; i < NV; i++) {
-        uint64_t m = __ballot(key[i] >= T);
-        while (m) {
-            const int src = __builtin_ctzll(m);
-            m &= m - 1;
-            const uint32_t klo = __builtin_amdgcn_readlane((uint32_t)key[i], src);
-            const uint32_t khi = __builtin_amdgcn_readlane((uint32_t)(key[i] >> 32), src);
-            const uint64_t kx = ((uint64_t)khi << 32) | klo;
-            const float px = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p[i]), src));
-            int r = 0;
+        for (int i = 1; i < NV; i++) m = max(m, (int)key[i]);
+        m = wave_max_nonneg(m);
+        int win = -1;
 #pragma unroll
-            for (int i2 = 0; i2 < NV; i2++) r += __popcll(__ballot(key[i2] > kx));
-            if (lane == r) { my_idx = src + 64 * i; my_w = px; }
+        for (int i = 0; i < NV; i++) {
+            const uint64_t bm = __ballot(key[i] == (uint32_t)m);
+            if (win < 0 && bm) win = __builtin_ctzll(bm) + 64 * i;
         }
+        if ((win & 63) == lane) {
+#pragma unroll
+            for (int i = 0; i < NV; i++)
+                if (i == (win >> 6)) key[i] = 0u;
+        }
+        if (lane == k) { my_idx = win; my_w = __builtin_bit_cast(float, (uint32_t)m - 1u); }
     }
     float ws = 0.0f;
     for (int k = 0; k < K; k++)

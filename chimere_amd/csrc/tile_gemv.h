@@ -71,6 +71,9 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds* __re
         // rows are packed with stride seg (== CB except in a ragged last chunk)
         if (n1) stage_rows(tile, base1 + goff, rb, n1, seg, tid, NTH);
         if (n2) stage_rows(tile + n1 * seg, base2 + goff, rb, n2, seg, tid, NTH);
+#ifdef CHIMERE_PHASE_TIMING
+        if (ph && tid == 0) ph[4] = __builtin_amdgcn_s_memrealtime();
+#endif
         for (int i = tid; i < ntok * cb; i += NTH) {
             const int t = i / cb, b = i - t * cb;
             const int tk = toks ? toks[t] : t;
