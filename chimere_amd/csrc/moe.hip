@@ -356,16 +356,33 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert(MoeArgs a) {
     const int ns = a.has_shared ? (NB > x ? (NB - 1 - x) / 8 + 1 : 0) : 0;
     const int nx = nr * NB + ns;
     if (lb >= nx) {
+        // helper: first the up rows of this XCD's items (requested by the items
+        // right behind their gate rows), then the down matrices; each helper
+        // takes an equal contiguous share of both, one 2-byte load per 64 bytes
+        // (weights are 2-byte aligned)
         const int nh = G8 - nx, hb = lb - nx;
+        uint32_t sink = 0;
+        const int64_t LE = QK * row_bytes(TE, a.H), LS = QK * row_bytes(TS, a.H);
+        const int64_t ua = (int64_t)nr * NB * LE + ns * LS;
+        for (int64_t o = ua * hb / nh + 64 * (int64_t)tid, e1 = ua * (hb + 1) / nh; o < e1; o += 64 * EX_THREADS) {
+            const int64_t rl = (int64_t)nr * NB * LE;
+            const uint8_t* p;
+            if (o < rl) {
+                const int i = (int)(o / LE);
+                p = a.up + (int64_t)pl.uexp[x + 8 * (i / NB)] * a.su + (int64_t)(i % NB) * LE + (o - (int64_t)i * LE);
+            } else {
+                const int j = (int)((o - rl) / LS);
+                p = a.sh_up + (int64_t)(x + 8 * j) * LS + (o - rl - (int64_t)j * LS);
+            }
+            sink += *(const uint16_t*)((uintptr_t)p & ~(uintptr_t)1);
+        }
         const int64_t mb = (int64_t)a.H * row_bytes(TE, a.F), sb = (int64_t)a.H * row_bytes(TS, a.F);
         const int64_t total = nr * mb + (ns ? sb : 0);
-        const int64_t c0 = total * hb / nh, c1 = total * (hb + 1) / nh;
-        uint32_t sink = 0;
-        for (int64_t o = c0 + 64 * (int64_t)tid; o < c1; o += 64 * EX_THREADS) {   // one 2-byte load per 64 bytes
+        for (int64_t o = total * hb / nh + 64 * (int64_t)tid, e1 = total * (hb + 1) / nh; o < e1; o += 64 * EX_THREADS) {
             const int m = (int)(o / mb);
             const uint8_t* base = m < nr ? a.down + (int64_t)pl.uexp[x + 8 * m] * a.sd : a.sh_down;
             const int64_t off = m < nr ? o - (int64_t)m * mb : o - (int64_t)nr * mb;
-            sink += *(const uint16_t*)(base + (off & ~(int64_t)1));   // weights are 2-byte aligned
+            sink += *(const uint16_t*)(base + (off & ~(int64_t)1));
         }
         if (a.H < 0) a.plan[0] = (int)sink;   // never taken: keeps the loads
         return;
