@@ -66,8 +66,8 @@ struct MoeArgs {
     float* wts;         // [M*K]
     int* plan;          // n_unique, uexp[128], u_ntok[128], u_pair[128][MAX_TOK]
     uint8_t* xq;        // [M][xq_stride]   Q8_1(x)
-    uint2* terms;       // F > 512: [M*K + M][H][F/32]  down block terms (f32 scale bits, int32 sumi)
-    float* lane_acc;    // F <= 512: [M*K + M][H][F/32]  lane j's finished accumulator (one block per lane)
+    uint2* terms;       // F > 512: [M*K + M][F/32][H]  down block terms (f32 scale bits, int32 sumi)
+    float* lane_acc;    // F <= 512: [M*K + M][F/32][H]  lane j's finished accumulator (one block per lane)
     int64_t xq_stride;
     uint8_t* hq;        // M > 1: [M*K + M][hq_stride]  Q8_1(h) per pair
     float* dn;          // M > 1: [M*K + M][H]  down-projection output per pair (aliases terms)
@@ -143,7 +143,7 @@ __device__ __forceinline__ void load_down_blocks(RegBlk<T> (&rb)[EX_MAX_RPT], co
 // Exact down-projection terms of block w for the thread's rows and every
 // token of the unit.  F <= 512 (NB <= 16): lane w of the L=16 order owns only
 // block w, so its finished accumulator fmaf(scale, sumi, 0) is stored
-// (lane_acc[pair][r][w]); otherwise the term itself (terms[pair][r][w] =
+// (lane_acc[pair][w][r]); otherwise the term itself (terms[pair][w][r] =
 // (f32(d_w) * f32(d_h), sumi)) for K3 to accumulate in order.
 template <int T>
 __device__ __forceinline__ void down_terms(const RegBlk<T> (&rb)[EX_MAX_RPT], const XLds* hx, const int* pairs,
@@ -158,7 +158,7 @@ __device__ __forceinline__ void down_terms(const RegBlk<T> (&rb)[EX_MAX_RPT], co
                 XBlk xb;
                 xlds_to_blk(hx[t], xb);
                 const int s = wdot<T>(wb, xb);
-                const int64_t o = ((int64_t)pairs[t] * a.H + r) * NB + w;
+                const int64_t o = ((int64_t)pairs[t] * NB + w) * a.H + r;   // one contiguous run per block w
                 if (NB <= SLOTS) a.lane_acc[o] = __builtin_fmaf(wb.dw * xb.d, (float)s, 0.0f);
                 else a.terms[o] = make_uint2(__builtin_bit_cast(uint32_t, wb.dw * xb.d), (uint32_t)s);
             }
@@ -433,7 +433,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_combine(MoeArgs a) {
                 // one block per lane: the stored value is the lane's accumulator
 #pragma unroll
                 for (int c = 0; c < CMB_CHUNK; c++)
-                    accs[c] = (p0 + c < np && j < NB) ? a.lane_acc[((int64_t)(p0 + c) * a.H + r) * NB + j] : 0.0f;
+                    accs[c] = (p0 + c < np && j < NB) ? a.lane_acc[((int64_t)(p0 + c) * NB + j) * a.H + r] : 0.0f;
             } else {
                 // issue every term load of the chunk before using any
                 uint2 tv[CMB_CHUNK][EX_MAX_RPT];
@@ -442,7 +442,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_combine(MoeArgs a) {
 #pragma unroll
                     for (int q = 0; q < EX_MAX_RPT; q++) {
                         const int b = j + SLOTS * q;
-                        tv[c][q] = (p0 + c < np && b < NB) ? a.terms[((int64_t)(p0 + c) * a.H + r) * NB + b]
+                        tv[c][q] = (p0 + c < np && b < NB) ? a.terms[((int64_t)(p0 + c) * NB + b) * a.H + r]
                                                            : make_uint2(0, 0);
                     }
 #pragma unroll

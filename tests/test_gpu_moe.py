@@ -141,3 +141,12 @@ def test_moe_repeat_calls_reuse_workspace(dev):
     for _ in range(20):
         layer.forward(x[:1])
         assert (host(layer.forward(x)) == first).all()
+
+
+@pytest.mark.parametrize("et,M", [(O.Q4_0, 1), (O.Q8_0, 1), (O.IQ3_S, 3)])
+def test_moe_wide_ffn(dev, et, M):
+    """F = 1024 (more than 16 blocks per down row: the per-block term path)."""
+    print(f"moe wide ffn et={et} M={M}", flush=True)
+    layer = build(dev, 300 + et + M, H=1024, F=1024, E=32, K=4, et=et, st=O.Q8_0, gate_vec=True)
+    g = torch.Generator(device=dev).manual_seed(9)
+    run_and_check(layer, torch.randn(M, 1024, generator=g, device=dev))
