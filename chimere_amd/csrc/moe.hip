@@ -420,7 +420,10 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_combine(MoeArgs a) {
     PHASE(2, 0);
     const int tid = threadIdx.x;
     const int rr = tid >> 4, j = tid & 15;
-    const int r = blockIdx.x * TILE_ROWS + rr;
+    // neighbouring 16-row tiles on one XCD (work-group b runs on XCD b % 8):
+    // they share the 128-byte lines of the block-major terms
+    const int tile_i = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
+    const int r = tile_i * TILE_ROWS + rr;
     const int NB = a.F / QK;
     const int MK = a.M * a.K;
     for (int i = tid; i < MK; i += GEMV_THREADS) s_w[i] = a.wts[i];
@@ -469,7 +472,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_combine(MoeArgs a) {
     // combine: one thread per (row, token)
     if (tid < TILE_ROWS * a.M) {
         const int row = tid % TILE_ROWS, t = tid / TILE_ROWS;
-        const int rg = blockIdx.x * TILE_ROWS + row;
+        const int rg = tile_i * TILE_ROWS + row;
         if (rg < a.H) {
             float acc = 0.0f;
             for (int k = 0; k < a.K; k++) acc = __builtin_fmaf(s_w[t * a.K + k], dn[row][t * a.K + k], acc);
