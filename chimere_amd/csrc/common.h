@@ -69,9 +69,14 @@ __device__ __forceinline__ float det_silu(float g) { return g / (1.0f + det_exp(
 __device__ __forceinline__ int dot4(int a, int b, int c) {   // v_dot4_i32_i8
     return __builtin_amdgcn_sdot4(a, b, c, false);
 }
+// byte i = bit i of the 4-bit nibble (0x00 / 0x01)
+__device__ __forceinline__ uint32_t nib_bits(uint32_t nib) {
+    return (nib * 0x00204081u) & 0x01010101u;   // 24-bit multiply: nib < 16
+}
 // bytes 0xFF where the corresponding bit of the 4-bit nibble is set
+// (v_perm_b32 selector 12 yields 0x00, 13 yields 0xFF)
 __device__ __forceinline__ uint32_t nib_mask(uint32_t nib) {
-    return ((nib * 0x00204081u) & 0x01010101u) * 0xFFu;
+    return __builtin_amdgcn_perm(0u, 0u, nib_bits(nib) | 0x0C0C0C0Cu);
 }
 // (hi:lo) >> 8*s, s in 0..3
 __device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t s) {
@@ -147,7 +152,7 @@ __device__ __forceinline__ int dot_iq3_s_core(uint32_t dbits, uint32_t qs0, uint
         s = dot4((int)v0, x.q[2 * l], s);
         s = dot4((int)v1, x.q[2 * l + 1], s);
     }
-    return s * mult;
+    return __mul24(s, mult);
 }
 
 __device__ __forceinline__ int dot_q8_0(const uint8_t* row, int off, const XBlk& x, float* dw) {
@@ -190,7 +195,7 @@ __device__ __forceinline__ int wdot(const WBlk& w, const XBlk& x) {
 #pragma unroll
     for (int i = 0; i < 8; i++) s = dot4(w.v[i], x.q[i], s);
     if constexpr (T == T_Q4_0) return s - 8 * x.sumq;
-    else if constexpr (T == T_IQ3_S) return s * w.mult;
+    else if constexpr (T == T_IQ3_S) return __mul24(s, w.mult);   // |s| < 2^23, mult <= 31
     else return s;
 }
 
@@ -221,9 +226,12 @@ __device__ __forceinline__ void wdec_iq3_s_core(uint32_t dbits, uint32_t qs0, ui
         const uint32_t i0 = ((qsw >> (16 * (l & 1))) & 0xFFu) | (((qh >> (2 * l)) & 1u) << 8);
         const uint32_t i1 = ((qsw >> (16 * (l & 1) + 8)) & 0xFFu) | (((qh >> (2 * l + 1)) & 1u) << 8);
         const uint32_t sb = (sg >> (8 * l)) & 0xFFu;
-        const uint32_t m0 = nib_mask(sb & 0xFu), m1 = nib_mask(sb >> 4);
-        w.v[2 * l] = (int)((grid[i0] ^ m0) + (m0 & 0x01010101u));
-        w.v[2 * l + 1] = (int)((grid[i1] ^ m1) + (m1 & 0x01010101u));
+        const uint32_t b0 = nib_bits(sb & 0xFu), b1 = nib_bits(sb >> 4);
+        const uint32_t m0 = __builtin_amdgcn_perm(0u, 0u, b0 | 0x0C0C0C0Cu);
+        const uint32_t m1 = __builtin_amdgcn_perm(0u, 0u, b1 | 0x0C0C0C0Cu);
+        // signed levels: (g ^ m) + (m & 1): per-byte negation, no carry since g >= 1
+        w.v[2 * l] = (int)((grid[i0] ^ m0) + b0);
+        w.v[2 * l + 1] = (int)((grid[i1] ^ m1) + b1);
     }
 }
 
@@ -358,11 +366,12 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void glb_void_t;
 
 // Copy `nrows` row segments of `seg` bytes (global row stride `gstride`) into
-// LDS, packed with row stride `seg`.  When every piece is 16-byte aligned the
-// copy uses the asynchronous global->LDS loads (global_load_lds_dwordx4: lane
-// l of a wave deposits its 16 bytes at a wave-uniform LDS base + 16*l), so all
-// loads of a phase are in flight together; otherwise all pieces are loaded to
-// registers before any is stored.  The caller completes the copy with
+// LDS, packed with row stride `seg`.  When every piece is 16-byte (4-byte)
+// aligned the copy uses the asynchronous global->LDS loads
+// (global_load_lds_dwordx4 / _dword: lane l of a wave deposits its 16 (4)
+// bytes at a wave-uniform LDS base + 16*l (4*l)), so all loads of a phase are
+// in flight together; otherwise all pieces are loaded to registers before any
+// is stored.  The caller completes the copy with
 // lds_copy_wait() + __syncthreads().
 __device__ __forceinline__ void stage_rows(uint8_t* __restrict__ lds, const uint8_t* __restrict__ g,
                                            int64_t gstride, int nrows, int seg, int tid, int nthreads) {
@@ -387,9 +396,22 @@ __device__ __forceinline__ void stage_rows(uint8_t* __restrict__ lds, const uint
                 }
             }
         }
+    } else if ((al & 3) == 0) {
+        // 4-byte aligned (e.g. IQ3_S chunks of 2 or 4 superblocks): the same
+        // asynchronous copy in dword pieces (global_load_lds_dword)
+        const int per = seg >> 2, tot = per * nrows;
+        const int lane = tid & 63, wave = tid >> 6, nw = nthreads >> 6;
+        for (int c0 = wave * 64; c0 < tot; c0 += nw * 64) {
+            const int c = c0 + lane;
+            if (c < tot) {
+                const int r = c / per, col = c - r * per;
+                __builtin_amdgcn_global_load_lds((const glb_void_t*)(g + r * gstride + col * 4),
+                                                 (lds_void_t*)(lds + c0 * 4), 4, 0, 0);
+            }
+        }
     } else {
         // rare unaligned case: whole-dword or byte pieces, up to 8 in flight per thread
-        const bool w4 = (al & 3) == 0;
+        const bool w4 = false;
         const int unit = w4 ? 4 : 1, per = seg / unit, tot = per * nrows;
         for (int i0 = 0; i0 < tot; i0 += 8 * nthreads) {
             uint32_t v[8];

@@ -90,7 +90,7 @@ struct Plan {
 // K1: grid E (router rows) + has_gate (shared-expert gate row) + M (x quantizers).
 template <int NT>
 __global__ __launch_bounds__(256) void k_moe_route(MoeArgs a) {
-    __shared__ float red[256];
+    __shared__ float red[NT * 256];
     PHASE(0, 0);
     const int row = blockIdx.x;
     const int ng = a.sh_gate_w ? 1 : 0;
@@ -530,22 +530,63 @@ constexpr int KG_RG = 16;     // KG / KD: 256 threads, 64 rows per tile (4 per r
 constexpr int KG_CHUNK = 32;
 template <int T>
 constexpr int kg_chunk() { return T == T_Q8_0 ? 16 : KG_CHUNK; }
+// KG: K chunks of 16 blocks, double-buffered where two 64-row buffers fit in
+// KG_BUF * 2 bytes (Q4_0, IQ3_S); Q8_0 rows use the same space single-buffered
+constexpr int KG_BLK = 16;
+constexpr int KG_BUF = 64 * 16 * 18 + 16;
 template <int T>
-constexpr int chunk_bytes(int blocks) { return T == T_IQ3_S ? blocks / 8 * 110 : blocks * QTraits<T>::BYTES; }
+constexpr bool kg_db() { return 64 * chunk_bytes<T>(KG_BLK) + 16 <= KG_BUF; }
 
-// KG: grid 8*ceil((M*K+1)/8)*NB; item V -> XCD V & 7, unit (V & 7) + 8*(V/8/NB), block w = V/8 % NB.
+template <int T>
+__device__ __forceinline__ void kg_tile(uint8_t* tile, XLds* xs, uint8_t* xraw, const uint32_t* grid, const uint8_t* g,
+                                        const uint8_t* u, int64_t rb, const MoeArgs& a, const int* toks, int ntok,
+                                        float (&acc)[4][MAX_TOK]) {
+    if (ntok == 1) {   // most experts of a decode batch serve one token: no token loop
+        float a1[4][1];
+        if constexpr (kg_db<T>())
+            tile_gemv_db<T, 1, KG_RG, 4, KG_BLK>(tile, KG_BUF, xraw, grid, g, QK, u, QK, rb, a.H, a.xq, a.xq_stride,
+                                                 toks, 1, a1);
+        else
+            tile_gemv<T, 1, KG_RG, 4, KG_BLK>(tile, xs, grid, g, QK, u, QK, rb, a.H, a.xq, a.xq_stride, toks, 1, a1);
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[r][0] = a1[r][0];
+        return;
+    }
+    if constexpr (kg_db<T>())
+        tile_gemv_db<T, MAX_TOK, KG_RG, 4, KG_BLK>(tile, KG_BUF, xraw, grid, g, QK, u, QK, rb, a.H, a.xq, a.xq_stride,
+                                                   toks, ntok, acc);
+    else
+        tile_gemv<T, MAX_TOK, KG_RG, 4, KG_BLK>(tile, xs, grid, g, QK, u, QK, rb, a.H, a.xq, a.xq_stride, toks, ntok,
+                                                acc);
+}
+
+// KG: grid NB + 8*ceil(M*K/8)*NB.  The first NB work-groups take the shared
+// expert (all M tokens: the heaviest items, dispatched first, block w on XCD
+// w & 7); then item V' = V - NB -> unit (V' & 7) + 8*(V'/8/NB), block
+// V'/8 % NB (a routed expert's blocks on one XCD, V & 7 == V' & 7 for NB % 8 == 0).
 template <int TE, int TS>
 __global__ __launch_bounds__(GEMV_THREADS) void k_moe_gateup(MoeArgs a) {
-    constexpr int CBE = chunk_bytes<TE>(kg_chunk<TE>()), CBS = chunk_bytes<TS>(kg_chunk<TS>());
-    constexpr int CB = CBE > CBS ? CBE : CBS;
-    __shared__ __attribute__((aligned(16))) uint8_t tile[4 * KG_RG * CB + 16];
-    __shared__ XLds xs[MAX_TOK * KG_CHUNK];
+    static_assert(64 * chunk_bytes<T_Q8_0>(KG_BLK) + 16 <= 2 * KG_BUF, "tile");
+    __shared__ __attribute__((aligned(16))) uint8_t tile[2 * KG_BUF];
+    // raw Q8_1 blocks (double-buffered path) or decoded blocks (single-buffered path)
+    static_assert(MAX_TOK * KG_BLK * sizeof(XLds) <= 2 * MAX_TOK * KG_BLK * Q8_1_BYTES, "xbuf");
+    __shared__ __attribute__((aligned(16))) uint8_t xraw[2 * MAX_TOK * KG_BLK * Q8_1_BYTES];
+    XLds* xs = (XLds*)xraw;
     __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
     __shared__ float hg[MAX_TOK][QK], hu[MAX_TOK][QK];
     __shared__ int toks[MAX_TOK], pairs[MAX_TOK];
     const int NB = a.F / QK;
-    const int V = blockIdx.x, li = V >> 3, u = (V & 7) + 8 * (li / NB), w = li % NB;
-    if (u > a.M * a.K) return;
+    const int MK = a.M * a.K;
+    int u, w;
+    if ((int)blockIdx.x < NB) {
+        u = MK;
+        w = blockIdx.x;
+    } else {
+        const int V = blockIdx.x - NB, li = V >> 3;
+        u = (V & 7) + 8 * (li / NB);
+        w = li % NB;
+        if (u >= MK) return;
+    }
     PHASE(1, 0);
     int ntok;
     int64_t e;
@@ -558,12 +599,11 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_gateup(MoeArgs a) {
     const int r0 = w * QK;
     if (e < 0) {
         const int64_t rb = row_bytes(TS, a.H);
-        tile_gemv<TS, MAX_TOK, KG_RG, 4, kg_chunk<TS>()>(tile, xs, grid, a.sh_gate + r0 * rb, QK, a.sh_up + r0 * rb, QK, rb, a.H,
-                                         a.xq, a.xq_stride, toks, ntok, acc, PHASE_PTR(1, 5));
+        kg_tile<TS>(tile, xs, xraw, grid, a.sh_gate + r0 * rb, a.sh_up + r0 * rb, rb, a, toks, ntok, acc);
     } else {
         const int64_t rb = row_bytes(TE, a.H);
-        tile_gemv<TE, MAX_TOK, KG_RG, 4, kg_chunk<TE>()>(tile, xs, grid, a.gate + e * a.sg + r0 * rb, QK, a.up + e * a.su + r0 * rb,
-                                         QK, rb, a.H, a.xq, a.xq_stride, toks, ntok, acc, PHASE_PTR(1, 5));
+        kg_tile<TE>(tile, xs, xraw, grid, a.gate + e * a.sg + r0 * rb, a.up + e * a.su + r0 * rb, rb, a, toks, ntok,
+                    acc);
     }
     PHASE(1, 2);
     // group g holds tile rows g, g+16 (gate rows) and g+32, g+48 (up rows)
@@ -596,7 +636,23 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_gateup(MoeArgs a) {
     PHASE(1, 3);
 }
 
-// KD: grid (H/64, M*K+1): unit blockIdx.y, down rows [64*blockIdx.x, +64).
+template <int T>
+__device__ __forceinline__ void kd_tile(uint8_t* tile, XLds* xs, const uint32_t* grid,
+                                        const uint8_t* rows, int nr, int64_t rb, const MoeArgs& a, const int* pairs,
+                                        int ntok, float (&acc)[4][MAX_TOK]) {
+    if (ntok == 1) {
+        float a1[4][1];
+        tile_gemv<T, 1, KG_RG, 4, kg_chunk<T>()>(tile, xs, grid, rows, nr, nullptr, 0, rb, a.F, a.hq, a.hq_stride,
+                                                 pairs, 1, a1);
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[r][0] = a1[r][0];
+        return;
+    }
+    tile_gemv<T, MAX_TOK, KG_RG, 4, kg_chunk<T>()>(tile, xs, grid, rows, nr, nullptr, 0, rb, a.F, a.hq,
+                                                   a.hq_stride, pairs, ntok, acc);
+}
+
+// KD: grid (H/64, M*K+1): down rows [64*blockIdx.x, +64) of unit blockIdx.y - 1 (y = 0: shared expert).
 template <int TE, int TS>
 __global__ __launch_bounds__(GEMV_THREADS) void k_moe_down(MoeArgs a) {
     constexpr int CBE = chunk_bytes<TE>(kg_chunk<TE>()), CBS = chunk_bytes<TS>(kg_chunk<TS>());
@@ -608,7 +664,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_down(MoeArgs a) {
     int ntok;
     int64_t e;
     PHASE(2, 0);
-    if (!load_unit(a, blockIdx.y, pairs, toks, ntok, e)) return;
+    // unit blockIdx.y - 1; y = 0: the shared expert (heaviest, dispatched first)
+    if (!load_unit(a, blockIdx.y == 0 ? a.M * a.K : (int)blockIdx.y - 1, pairs, toks, ntok, e)) return;
     const int tid = threadIdx.x;
     PHASE(2, 1);
     if constexpr (TE == T_IQ3_S || TS == T_IQ3_S)
@@ -618,14 +675,12 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_down(MoeArgs a) {
     // the h rows are indexed by pair
     if (e < 0) {
         const int64_t rb = row_bytes(TS, a.F);
-        tile_gemv<TS, MAX_TOK, KG_RG, 4, kg_chunk<TS>()>(tile, xs, grid, a.sh_down + r0 * rb, nr, nullptr, 0, rb, a.F, a.hq,
-                                         a.hq_stride, pairs, ntok, acc, PHASE_PTR(2, 5));
+        kd_tile<TS>(tile, xs, grid, a.sh_down + r0 * rb, nr, rb, a, pairs, ntok, acc);
     } else {
         const int64_t rb = row_bytes(TE, a.F);
-        tile_gemv<TE, MAX_TOK, KG_RG, 4, kg_chunk<TE>()>(tile, xs, grid, a.down + e * a.sd + r0 * rb, nr, nullptr, 0, rb, a.F,
-                                         a.hq, a.hq_stride, pairs, ntok, acc, PHASE_PTR(2, 5));
-    PHASE(2, 2);
+        kd_tile<TE>(tile, xs, grid, a.down + e * a.sd + r0 * rb, nr, rb, a, pairs, ntok, acc);
     }
+    PHASE(2, 2);
     const int g = tid >> 4, j = tid & 15;
 #pragma unroll
     for (int r = 0; r < 4; r++)
@@ -719,7 +774,7 @@ static void launch_layer_multi(const MoeArgs& a, int stage, hipStream_t s) {
         hipLaunchKernelGGL(k_moe_plan, dim3(1), dim3(EX_THREADS), 0, s, a);
     }
     if (stage < 0 || stage == 1)
-        hipLaunchKernelGGL((k_moe_gateup<TE, TS>), dim3(8 * ((NU + 7) / 8) * NB), dim3(GEMV_THREADS), 0, s, a);
+        hipLaunchKernelGGL((k_moe_gateup<TE, TS>), dim3(NB + 8 * ((NU - 1 + 7) / 8) * NB), dim3(GEMV_THREADS), 0, s, a);
     if (stage < 0 || stage == 2) {
         hipLaunchKernelGGL((k_moe_down<TE, TS>), dim3((a.H + 4 * KG_RG - 1) / (4 * KG_RG), NU), dim3(GEMV_THREADS), 0,
                            s, a);

@@ -32,7 +32,8 @@ __device__ __forceinline__ float tree_sum256(float v, float* red) {
 
 // f32 row dot of `a` (H) against NT tokens of x (token stride H), in the
 // reference's order: thread t accumulates columns t, t+256, ... with fused
-// multiply-add, then tree_sum256.  Results valid in thread 0.
+// multiply-add, then tree_sum256 (NT > 1: the NT trees side by side, red of
+// NT * 256 floats).  Results valid in thread 0.
 template <int NT>
 __device__ __forceinline__ void f32_row_dot(const float* __restrict__ a, const float* __restrict__ x,
                                             int H, int ntok, float* red, float (&out)[NT]) {
@@ -41,24 +42,45 @@ __device__ __forceinline__ void f32_row_dot(const float* __restrict__ a, const f
 #pragma unroll
     for (int t = 0; t < NT; t++) acc[t] = 0.0f;
     for (int j0 = threadIdx.x; j0 < H; j0 += 256 * U) {
-        float av[U];
+        // every load of the step is issued before any is used (tokens past
+        // ntok re-read the last token; their sums are not returned)
+        float av[U], xv[NT][U];
 #pragma unroll
         for (int u = 0; u < U; u++) av[u] = j0 + 256 * u < H ? a[j0 + 256 * u] : 0.0f;
 #pragma unroll
         for (int t = 0; t < NT; t++) {
-            if (t < ntok) {
-                float xv[U];
+            const int64_t tt = t < ntok ? t : ntok - 1;
 #pragma unroll
-                for (int u = 0; u < U; u++) xv[u] = j0 + 256 * u < H ? x[(int64_t)t * H + j0 + 256 * u] : 0.0f;
+            for (int u = 0; u < U; u++) xv[t][u] = j0 + 256 * u < H ? x[tt * H + j0 + 256 * u] : 0.0f;
+        }
 #pragma unroll
-                for (int u = 0; u < U; u++)
-                    if (j0 + 256 * u < H) acc[t] = __builtin_fmaf(av[u], xv[u], acc[t]);
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int u = 0; u < U; u++)
+                if (j0 + 256 * u < H) acc[t] = __builtin_fmaf(av[u], xv[t][u], acc[t]);
+    }
+    if constexpr (NT == 1) {
+        out[0] = tree_sum256(acc[0], red);
+    } else {
+        // the NT trees side by side: red holds NT * 256 floats
+        const int tid = threadIdx.x;
+#pragma unroll
+        for (int t = 0; t < NT; t++) red[t * 256 + tid] = acc[t];
+        __syncthreads();
+        if (tid < 128)
+#pragma unroll
+            for (int t = 0; t < NT; t++) red[t * 256 + tid] = red[t * 256 + tid] + red[t * 256 + tid + 128];
+        __syncthreads();
+        if (tid < 64) {
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                float w = red[t * 256 + tid] + red[t * 256 + tid + 64];
+                w = w + xlane<32>(w);
+                out[t] = bfly32_sum(w);
             }
         }
+        __syncthreads();
     }
-#pragma unroll
-    for (int t = 0; t < NT; t++)
-        if (t < ntok) out[t] = tree_sum256(acc[t], red);
 }
 
 // ---------------------------------------------------------------- top-k

@@ -117,3 +117,102 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds* __re
 }
 
 }  // namespace chimere
+
+namespace chimere {
+
+// Bytes of `blocks` 32-element blocks of a type-T row (IQ3_S: whole superblocks).
+template <int T>
+__host__ __device__ constexpr int chunk_bytes(int blocks) {
+    return T == T_IQ3_S ? blocks / 8 * 110 : blocks * QTraits<T>::BYTES;
+}
+
+// Q8_1 block from raw bytes in LDS (36 bytes, 4-byte aligned); the sum of the
+// quants only where the weight type needs it (Q4_0).
+template <int T>
+__device__ __forceinline__ void raw_xblk(const uint8_t* p, XBlk& x) {
+    const uint32_t* w = (const uint32_t*)p;
+    x.d = h2f(w[0] & 0xFFFFu);
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        x.q[i] = (int)w[1 + i];
+        if constexpr (T == T_Q4_0) s = dot4(x.q[i], 0x01010101, s);
+    }
+    x.sumq = s;
+}
+
+// tile_gemv with double-buffered K chunks: chunk c+1 (weight rows and the
+// tokens' raw Q8_1 blocks, both by asynchronous global->LDS copies) is in
+// flight while chunk c is computed.  tile: 2 buffers of TB bytes (TB >=
+// (n1+n2) * chunk_bytes<T>(CBLK)); xraw: 2 buffers of NT * CBLK * 36 bytes.
+// Needs 16-byte aligned row starts and chunk offsets (rb, X, x_tok_stride
+// multiples of 16; ncols a multiple of 128).  Same fp32 order as tile_gemv.
+template <int T, int NT, int RG, int RPG, int CBLK>
+__device__ __forceinline__ void tile_gemv_db(uint8_t* __restrict__ tile, int TB, uint8_t* __restrict__ xraw,
+                                             const uint32_t* __restrict__ grid, const uint8_t* base1, int n1,
+                                             const uint8_t* base2, int n2, int64_t rb, int ncols,
+                                             const uint8_t* __restrict__ X, int64_t x_tok_stride, const int* toks,
+                                             int ntok, float (&acc)[RPG][NT]) {
+    constexpr int NTH = RG * SLOTS, XB = NT * CBLK * Q8_1_BYTES;
+    static_assert(CBLK % SLOTS == 0 && (T != T_IQ3_S || CBLK % 8 == 0) && CBLK <= MAX_CHUNK_BLOCKS, "chunk");
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = tid >> 4, j = tid & 15;
+    const int nr = n1 + n2;
+    const int nb = ncols / QK, nc = (nb + CBLK - 1) / CBLK;
+#pragma unroll
+    for (int r = 0; r < RPG; r++)
+#pragma unroll
+        for (int t = 0; t < NT; t++) acc[r][t] = 0.0f;
+    auto issue = [&](int c, int buf) {
+        const int b0 = c * CBLK, cb = min(CBLK, nb - b0);
+        const int seg = chunk_bytes<T>(cb);
+        const int64_t goff = T == T_IQ3_S ? (int64_t)b0 / 8 * 110 : (int64_t)b0 * QTraits<T>::BYTES;
+        uint8_t* tb = tile + buf * TB;
+        if (n1) stage_rows(tb, base1 + goff, rb, n1, seg, tid, NTH);
+        if (n2) stage_rows(tb + n1 * seg, base2 + goff, rb, n2, seg, tid, NTH);
+        // token t's cb blocks at xraw + buf*XB + t*cb*36 (16-byte pieces)
+        const int per = cb * Q8_1_BYTES / 16, tot = ntok * per;
+        uint8_t* xb = xraw + buf * XB;
+        for (int c0 = wave * 64; c0 < tot; c0 += NTH) {
+            const int cc = c0 + lane;
+            if (cc < tot) {
+                const int t = cc / per, col = cc - t * per;
+                const int tk = toks ? toks[t] : t;
+                __builtin_amdgcn_global_load_lds(
+                    (const glb_void_t*)(X + tk * x_tok_stride + (int64_t)b0 * Q8_1_BYTES + col * 16),
+                    (lds_void_t*)(xb + c0 * 16), 16, 0, 0);
+            }
+        }
+    };
+    issue(0, 0);
+    for (int c = 0; c < nc; c++) {
+        const int buf = c & 1, cb = min(CBLK, nb - c * CBLK), seg = chunk_bytes<T>(cb);
+        lds_copy_wait();
+        __syncthreads();   // chunk c landed; every wave is done with chunk c-1
+        if (c + 1 < nc) issue(c + 1, buf ^ 1);
+        const uint8_t* tb = tile + buf * TB;
+        const uint8_t* xb = xraw + buf * XB;
+#pragma unroll
+        for (int r = 0; r < RPG; r++) {
+            const int row_i = g + RG * r;
+            if (row_i < nr) {
+                const uint8_t* row = tb + row_i * seg;
+                for (int b = j; b < cb; b += SLOTS) {
+                    WBlk wb;
+                    block_decode<T>(row, b, grid, wb);
+#pragma unroll
+                    for (int t = 0; t < NT; t++) {
+                        if (t < ntok) {
+                            XBlk x;
+                            raw_xblk<T>(xb + (t * cb + b) * Q8_1_BYTES, x);
+                            const int s = wdot<T>(wb, x);
+                            acc[r][t] = __builtin_fmaf(wb.dw * x.d, (float)s, acc[r][t]);
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+}  // namespace chimere
