@@ -366,13 +366,14 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void glb_void_t;
 
 // Copy `nrows` row segments of `seg` bytes (global row stride `gstride`) into
-// LDS, packed with row stride `seg`.  When every piece is 16-byte (4-byte)
-// aligned the copy uses the asynchronous global->LDS loads
+// LDS, packed with row stride `seg`.  When every piece is 16-byte (with DW:
+// 4-byte) aligned the copy uses the asynchronous global->LDS loads
 // (global_load_lds_dwordx4 / _dword: lane l of a wave deposits its 16 (4)
 // bytes at a wave-uniform LDS base + 16*l (4*l)), so all loads of a phase are
 // in flight together; otherwise all pieces are loaded to registers before any
 // is stored.  The caller completes the copy with
 // lds_copy_wait() + __syncthreads().
+template <bool DW = false>
 __device__ __forceinline__ void stage_rows(uint8_t* __restrict__ lds, const uint8_t* __restrict__ g,
                                            int64_t gstride, int nrows, int seg, int tid, int nthreads) {
     const uintptr_t al = (uintptr_t)g | (uintptr_t)gstride | (uintptr_t)seg | (uintptr_t)lds;
@@ -396,7 +397,7 @@ __device__ __forceinline__ void stage_rows(uint8_t* __restrict__ lds, const uint
                 }
             }
         }
-    } else if ((al & 3) == 0) {
+    } else if (DW && (al & 3) == 0) {
         // 4-byte aligned (e.g. IQ3_S chunks of 2 or 4 superblocks): the same
         // asynchronous copy in dword pieces (global_load_lds_dword)
         const int per = seg >> 2, tot = per * nrows;
@@ -411,7 +412,7 @@ __device__ __forceinline__ void stage_rows(uint8_t* __restrict__ lds, const uint
         }
     } else {
         // rare unaligned case: whole-dword or byte pieces, up to 8 in flight per thread
-        const bool w4 = false;
+        const bool w4 = !DW && (al & 3) == 0;
         const int unit = w4 ? 4 : 1, per = seg / unit, tot = per * nrows;
         for (int i0 = 0; i0 < tot; i0 += 8 * nthreads) {
             uint32_t v[8];

@@ -69,8 +69,8 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds* __re
         const int64_t goff = T == T_IQ3_S ? (int64_t)b0 / 8 * 110 : (int64_t)b0 * QTraits<T>::BYTES;
         __syncthreads();   // previous users of tile / xs are done
         // rows are packed with stride seg (== CB except in a ragged last chunk)
-        if (n1) stage_rows(tile, base1 + goff, rb, n1, seg, tid, NTH);
-        if (n2) stage_rows(tile + n1 * seg, base2 + goff, rb, n2, seg, tid, NTH);
+        if (n1) stage_rows<T == T_IQ3_S>(tile, base1 + goff, rb, n1, seg, tid, NTH);
+        if (n2) stage_rows<T == T_IQ3_S>(tile + n1 * seg, base2 + goff, rb, n2, seg, tid, NTH);
 #ifdef CHIMERE_PHASE_TIMING
         if (ph && tid == 0) ph[4] = __builtin_amdgcn_s_memrealtime();
 #endif
@@ -168,8 +168,8 @@ __device__ __forceinline__ void tile_gemv_db(uint8_t* __restrict__ tile, int TB,
         const int seg = chunk_bytes<T>(cb);
         const int64_t goff = T == T_IQ3_S ? (int64_t)b0 / 8 * 110 : (int64_t)b0 * QTraits<T>::BYTES;
         uint8_t* tb = tile + buf * TB;
-        if (n1) stage_rows(tb, base1 + goff, rb, n1, seg, tid, NTH);
-        if (n2) stage_rows(tb + n1 * seg, base2 + goff, rb, n2, seg, tid, NTH);
+        if (n1) stage_rows<T == T_IQ3_S>(tb, base1 + goff, rb, n1, seg, tid, NTH);
+        if (n2) stage_rows<T == T_IQ3_S>(tb + n1 * seg, base2 + goff, rb, n2, seg, tid, NTH);
         // token t's cb blocks at xraw + buf*XB + t*cb*36 (16-byte pieces)
         const int per = cb * Q8_1_BYTES / 16, tot = ntok * per;
         uint8_t* xb = xraw + buf * XB;
