@@ -362,6 +362,10 @@ __device__ __forceinline__ int block_dot(const uint8_t* row, int b, const XBlk& 
     else return dot_iq3_s(row, (b >> 3) * 110, b & 7, x, grid, dw);
 }
 
+// cache policy of global->LDS weight copies: non-temporal (each weight byte is
+// read once per call)
+constexpr int CPOL_STREAM = 2;
+
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void glb_void_t;
 
@@ -373,7 +377,7 @@ typedef __attribute__((address_space(1))) void glb_void_t;
 // in flight together; otherwise all pieces are loaded to registers before any
 // is stored.  The caller completes the copy with
 // lds_copy_wait() + __syncthreads().
-template <bool DW = false>
+template <bool DW = false, int CPOL = 0>
 __device__ __forceinline__ void stage_rows(uint8_t* __restrict__ lds, const uint8_t* __restrict__ g,
                                            int64_t gstride, int nrows, int seg, int tid, int nthreads) {
     const uintptr_t al = (uintptr_t)g | (uintptr_t)gstride | (uintptr_t)seg | (uintptr_t)lds;
@@ -385,7 +389,7 @@ __device__ __forceinline__ void stage_rows(uint8_t* __restrict__ lds, const uint
                 const int c = c0 + lane;
                 if (c < tot)
                     __builtin_amdgcn_global_load_lds((const glb_void_t*)(g + c * 16), (lds_void_t*)(lds + c0 * 16),
-                                                     16, 0, 0);
+                                                     16, 0, CPOL);
             }
         } else {
             for (int c0 = wave * 64; c0 < tot; c0 += nw * 64) {
@@ -393,7 +397,7 @@ __device__ __forceinline__ void stage_rows(uint8_t* __restrict__ lds, const uint
                 if (c < tot) {
                     const int r = c / per, col = c - r * per;
                     __builtin_amdgcn_global_load_lds((const glb_void_t*)(g + r * gstride + col * 16),
-                                                     (lds_void_t*)(lds + c0 * 16), 16, 0, 0);
+                                                     (lds_void_t*)(lds + c0 * 16), 16, 0, CPOL);
                 }
             }
         }
@@ -407,7 +411,7 @@ __device__ __forceinline__ void stage_rows(uint8_t* __restrict__ lds, const uint
             if (c < tot) {
                 const int r = c / per, col = c - r * per;
                 __builtin_amdgcn_global_load_lds((const glb_void_t*)(g + r * gstride + col * 4),
-                                                 (lds_void_t*)(lds + c0 * 4), 4, 0, 0);
+                                                 (lds_void_t*)(lds + c0 * 4), 4, 0, CPOL);
             }
         }
     } else {

@@ -544,19 +544,19 @@ __device__ __forceinline__ void kg_tile(uint8_t* tile, XLds* xs, uint8_t* xraw, 
     if (ntok == 1) {   // most experts of a decode batch serve one token: no token loop
         float a1[4][1];
         if constexpr (kg_db<T>())
-            tile_gemv_db<T, 1, KG_RG, 4, KG_BLK>(tile, KG_BUF, xraw, grid, g, QK, u, QK, rb, a.H, a.xq, a.xq_stride,
+            tile_gemv_db<T, 1, KG_RG, 4, KG_BLK, CPOL_STREAM>(tile, KG_BUF, xraw, grid, g, QK, u, QK, rb, a.H, a.xq, a.xq_stride,
                                                  toks, 1, a1);
         else
-            tile_gemv<T, 1, KG_RG, 4, KG_BLK>(tile, xs, grid, g, QK, u, QK, rb, a.H, a.xq, a.xq_stride, toks, 1, a1);
+            tile_gemv<T, 1, KG_RG, 4, KG_BLK, CPOL_STREAM>(tile, xs, grid, g, QK, u, QK, rb, a.H, a.xq, a.xq_stride, toks, 1, a1);
 #pragma unroll
         for (int r = 0; r < 4; r++) acc[r][0] = a1[r][0];
         return;
     }
     if constexpr (kg_db<T>())
-        tile_gemv_db<T, MAX_TOK, KG_RG, 4, KG_BLK>(tile, KG_BUF, xraw, grid, g, QK, u, QK, rb, a.H, a.xq, a.xq_stride,
+        tile_gemv_db<T, MAX_TOK, KG_RG, 4, KG_BLK, CPOL_STREAM>(tile, KG_BUF, xraw, grid, g, QK, u, QK, rb, a.H, a.xq, a.xq_stride,
                                                    toks, ntok, acc);
     else
-        tile_gemv<T, MAX_TOK, KG_RG, 4, KG_BLK>(tile, xs, grid, g, QK, u, QK, rb, a.H, a.xq, a.xq_stride, toks, ntok,
+        tile_gemv<T, MAX_TOK, KG_RG, 4, KG_BLK, CPOL_STREAM>(tile, xs, grid, g, QK, u, QK, rb, a.H, a.xq, a.xq_stride, toks, ntok,
                                                 acc);
 }
 
@@ -642,13 +642,13 @@ __device__ __forceinline__ void kd_tile(uint8_t* tile, XLds* xs, const uint32_t*
                                         int ntok, float (&acc)[4][MAX_TOK]) {
     if (ntok == 1) {
         float a1[4][1];
-        tile_gemv<T, 1, KG_RG, 4, kg_chunk<T>()>(tile, xs, grid, rows, nr, nullptr, 0, rb, a.F, a.hq, a.hq_stride,
+        tile_gemv<T, 1, KG_RG, 4, kg_chunk<T>(), CPOL_STREAM>(tile, xs, grid, rows, nr, nullptr, 0, rb, a.F, a.hq, a.hq_stride,
                                                  pairs, 1, a1);
 #pragma unroll
         for (int r = 0; r < 4; r++) acc[r][0] = a1[r][0];
         return;
     }
-    tile_gemv<T, MAX_TOK, KG_RG, 4, kg_chunk<T>()>(tile, xs, grid, rows, nr, nullptr, 0, rb, a.F, a.hq,
+    tile_gemv<T, MAX_TOK, KG_RG, 4, kg_chunk<T>(), CPOL_STREAM>(tile, xs, grid, rows, nr, nullptr, 0, rb, a.F, a.hq,
                                                    a.hq_stride, pairs, ntok, acc);
 }
 

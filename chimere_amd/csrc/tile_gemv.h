@@ -46,7 +46,9 @@ __device__ __forceinline__ void xlds_to_blk(const XLds& s, XBlk& x) {
 // token t; reduce with slot_reduce16.  Contains __syncthreads().
 // CBLK: blocks per chunk (default ChunkGeom<T>::BLOCKS; a multiple of 16,
 // and of 8 for IQ3_S); xs holds NT * CBLK decoded blocks (token-major).
-template <int T, int NT, int RG, int RPG, int CBLK = ChunkGeom<T>::BLOCKS>
+// CPOL: cache policy of the weight copies (2 = non-temporal: weights are
+// streamed once per call).
+template <int T, int NT, int RG, int RPG, int CBLK = ChunkGeom<T>::BLOCKS, int CPOL = 0>
 __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds* __restrict__ xs,
                                           const uint32_t* __restrict__ grid,
                                           const uint8_t* base1, int n1, const uint8_t* base2, int n2,
@@ -69,8 +71,8 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds* __re
         const int64_t goff = T == T_IQ3_S ? (int64_t)b0 / 8 * 110 : (int64_t)b0 * QTraits<T>::BYTES;
         __syncthreads();   // previous users of tile / xs are done
         // rows are packed with stride seg (== CB except in a ragged last chunk)
-        if (n1) stage_rows<T == T_IQ3_S>(tile, base1 + goff, rb, n1, seg, tid, NTH);
-        if (n2) stage_rows<T == T_IQ3_S>(tile + n1 * seg, base2 + goff, rb, n2, seg, tid, NTH);
+        if (n1) stage_rows<T == T_IQ3_S, CPOL>(tile, base1 + goff, rb, n1, seg, tid, NTH);
+        if (n2) stage_rows<T == T_IQ3_S, CPOL>(tile + n1 * seg, base2 + goff, rb, n2, seg, tid, NTH);
 #ifdef CHIMERE_PHASE_TIMING
         if (ph && tid == 0) ph[4] = __builtin_amdgcn_s_memrealtime();
 #endif
@@ -147,7 +149,7 @@ __device__ __forceinline__ void raw_xblk(const uint8_t* p, XBlk& x) {
 // (n1+n2) * chunk_bytes<T>(CBLK)); xraw: 2 buffers of NT * CBLK * 36 bytes.
 // Needs 16-byte aligned row starts and chunk offsets (rb, X, x_tok_stride
 // multiples of 16; ncols a multiple of 128).  Same fp32 order as tile_gemv.
-template <int T, int NT, int RG, int RPG, int CBLK>
+template <int T, int NT, int RG, int RPG, int CBLK, int CPOL = 0>
 __device__ __forceinline__ void tile_gemv_db(uint8_t* __restrict__ tile, int TB, uint8_t* __restrict__ xraw,
                                              const uint32_t* __restrict__ grid, const uint8_t* base1, int n1,
                                              const uint8_t* base2, int n2, int64_t rb, int ncols,
@@ -168,8 +170,8 @@ __device__ __forceinline__ void tile_gemv_db(uint8_t* __restrict__ tile, int TB,
         const int seg = chunk_bytes<T>(cb);
         const int64_t goff = T == T_IQ3_S ? (int64_t)b0 / 8 * 110 : (int64_t)b0 * QTraits<T>::BYTES;
         uint8_t* tb = tile + buf * TB;
-        if (n1) stage_rows<T == T_IQ3_S>(tb, base1 + goff, rb, n1, seg, tid, NTH);
-        if (n2) stage_rows<T == T_IQ3_S>(tb + n1 * seg, base2 + goff, rb, n2, seg, tid, NTH);
+        if (n1) stage_rows<T == T_IQ3_S, CPOL>(tb, base1 + goff, rb, n1, seg, tid, NTH);
+        if (n2) stage_rows<T == T_IQ3_S, CPOL>(tb + n1 * seg, base2 + goff, rb, n2, seg, tid, NTH);
         // token t's cb blocks at xraw + buf*XB + t*cb*36 (16-byte pieces)
         const int per = cb * Q8_1_BYTES / 16, tot = ntok * per;
         uint8_t* xb = xraw + buf * XB;
