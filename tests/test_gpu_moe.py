@@ -125,11 +125,24 @@ def test_moe_edge_cases(dev, et, st, gate_vec, K, E, M):
     run_and_check(layer, torch.randn(M, 1024, generator=g, device=dev))
 
 
-def test_moe_zero_input_finite(dev):
+@pytest.mark.parametrize("M", [1, 2])
+def test_moe_zero_input_finite(dev, M):
+    """All logits equal: every probability ties, the lowest indices win."""
     layer = build(dev, 9, H=1024, F=256, E=32, K=4)
-    x = torch.zeros(2, 1024, device=dev)
+    x = torch.zeros(M, 1024, device=dev)
     og, ig, wg = run_and_check(layer, x)
     assert np.isfinite(og).all() and (ig == np.arange(4)).all()
+
+
+def test_moe_m1_tied_logits(dev):
+    """Router rows repeated in pairs: tied probabilities straddle the top-k boundary."""
+    layer = build(dev, 21, H=1024, F=256, E=64, K=7)
+    r = layer.tensors[0]
+    r[1::2] = r[0::2]            # experts 2i and 2i+1 get identical logits
+    g = torch.Generator(device=dev).manual_seed(4)
+    for _ in range(3):
+        og, ig, wg = run_and_check(layer, torch.randn(1, 1024, generator=g, device=dev))
+        assert len(set(ig[0])) == 7
 
 
 def test_moe_repeat_calls_reuse_workspace(dev):
