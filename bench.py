@@ -43,6 +43,8 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--pmc", action="store_true", help="light mode for rocprofv3 --pmc runs")
+    ap.add_argument("--pmc-workload", choices=["m1", "m8", "prefill", "head"], default="m1",
+                    help="workload of the --pmc light mode")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="run one device copy of this many MiB at the end (calibrates PMC byte counters)")
     return ap.parse_args()
@@ -110,14 +112,29 @@ def main():
     if args.pmc:
         # counter-collection mode (rocprofv3 --pmc serialises every dispatch):
         # one layer, a few eager layer calls, then the calibration copy
-        print("bench.py --pmc: building one layer", flush=True)
-        L = make_layer(100, Q4_0, Q4_0)
-        xs = torch.randn(args.steps, 1, H, device=dev)
-        out = torch.empty(1, H, device=dev)
-        for i in range(args.steps):
-            L.forward(xs[i], out=out)
+        wl = args.pmc_workload
+        print(f"bench.py --pmc: building the {wl} workload", flush=True)
+        if wl == "head":
+            V = 151936
+            g = torch.Generator(device=dev).manual_seed(2)
+            head = qmat(Q4_0, V, H, 1, g)[0]
+            xq = torch.empty(G.q8_1_row_bytes(H), dtype=torch.uint8, device=dev)
+            G.ggml_gpu_quantize_q8_1(torch.randn(H, generator=g, device=dev), xq, H)
+            y = torch.empty(V, device=dev)
+            for i in range(args.steps):
+                G.ggml_gpu_gemv_q4_0_q8(head, xq, y, V, H)
+        else:
+            L = make_layer(100, *((IQ3_S, Q8_0) if wl == "m8" else (Q4_0, Q4_0)))
+            M = {"m1": 1, "m8": 8, "prefill": 512}[wl]
+            xs = torch.randn(args.steps, M, H, device=dev)
+            out = torch.empty(M, H, device=dev)
+            for i in range(args.steps):
+                if wl == "prefill":
+                    L.prefill(xs[i], out=out)
+                else:
+                    L.forward(xs[i], out=out)
         torch.cuda.synchronize()
-        print(f"bench.py --pmc: {args.steps} layer calls done", flush=True)
+        print(f"bench.py --pmc: {args.steps} {wl} calls done", flush=True)
         if args.calib_copy_mb:
             src = torch.empty(args.calib_copy_mb << 18, dtype=torch.float32, device=dev).fill_(1.0)
             dst = torch.empty_like(src)
