@@ -31,6 +31,9 @@ SIGNATURES = [
     ("chimere_mmvq_q8_0_batched", None, [vp, vp, vp, vp, i32, i32, i32, i64, i64, i32, vp]),
     ("chimere_mmvq_q4_0_batched", None, [vp, vp, vp, vp, i32, i32, i32, i64, i64, i32, vp]),
     ("chimere_mmvq_multi", None, [i32, vp, vp, vp, i32, i32, i32, i32, vp]),
+    ("chimere_mmvq_q4_0_multi", None, [vp, vp, vp, i32, i32, i32, i32, vp]),
+    ("chimere_mmvq_q8_0_multi", None, [vp, vp, vp, i32, i32, i32, i32, vp]),
+    ("chimere_mmvq_iq3s_multi", None, [vp, vp, vp, i32, i32, i32, i32, vp]),
     ("chimere_f32_gemv", None, [vp, vp, vp, i32, i32, vp]),
     ("chimere_topk_softmax", None, [vp, vp, vp, i32, i32, i32, vp]),
     ("chimere_silu_mul_inplace", None, [vp, vp, i32, vp]),

@@ -219,6 +219,19 @@ void chimere_mmvq_multi(int type, const void* w, const void* x, float* y, int nc
     gemv_entry("mmvq_multi", type, w, x, y, ncols, nrows, nyp, ntok, s);
 }
 
+void chimere_mmvq_q4_0_multi(const void* w, const void* x, float* y, int ncols, int nrows, int nyp, int ntok,
+                             hipStream_t s) {
+    gemv_entry("mmvq_q4_0_multi", T_Q4_0, w, x, y, ncols, nrows, nyp, ntok, s);
+}
+void chimere_mmvq_q8_0_multi(const void* w, const void* x, float* y, int ncols, int nrows, int nyp, int ntok,
+                             hipStream_t s) {
+    gemv_entry("mmvq_q8_0_multi", T_Q8_0, w, x, y, ncols, nrows, nyp, ntok, s);
+}
+void chimere_mmvq_iq3s_multi(const void* w, const void* x, float* y, int ncols, int nrows, int nyp, int ntok,
+                             hipStream_t s) {
+    gemv_entry("mmvq_iq3s_multi", T_IQ3_S, w, x, y, ncols, nrows, nyp, ntok, s);
+}
+
 void chimere_dbg_block_dots(int type, const void* w, const void* x, int32_t* out, int ncols,
                             int nrows, hipStream_t s) {
     if (!out || !check_gemv("dbg_block_dots", type, w, x, (const float*)out, ncols, nrows, ncols / 32, 1))

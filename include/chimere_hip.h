@@ -102,6 +102,13 @@ void chimere_mmvq_q4_0_batched(const void *all_weights, const void *input_q8, fl
  * input at input_q8 + t*nrows_y_padded*36, output[t*nrows + r]. */
 void chimere_mmvq_multi(int type, const void *weights, const void *input_q8, float *output,
                         int ncols, int nrows, int nrows_y_padded, int ntok, hipStream_t stream);
+/* The same per weight type (the per-type names of the boundary's additions). */
+void chimere_mmvq_q4_0_multi(const void *weights, const void *input_q8, float *output, int ncols,
+                             int nrows, int nrows_y_padded, int ntok, hipStream_t stream);
+void chimere_mmvq_q8_0_multi(const void *weights, const void *input_q8, float *output, int ncols,
+                             int nrows, int nrows_y_padded, int ntok, hipStream_t stream);
+void chimere_mmvq_iq3s_multi(const void *weights, const void *input_q8, float *output, int ncols,
+                             int nrows, int nrows_y_padded, int ntok, hipStream_t stream);
 
 /* ------------------------------------------------------- routing / glue */
 /* f32 GEMV, y[r] = sum_c A[r*cols+c] x[c]  (src/kernels/elementwise.rs:186-221,

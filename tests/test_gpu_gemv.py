@@ -121,6 +121,16 @@ def test_gemv_multi_token(dev, t, ntok):
     G.gemv_multi(t, dev_t(w, dev), dev_t(xq, dev), y, nrows, ncols, ntok)
     yo = O.gemv(t, w, xq, ncols, nrows, ntok=ntok, xq_stride=xq.shape[1])
     assert (host(y).reshape(ntok, nrows).view(np.uint32) == np.asarray(yo).reshape(ntok, nrows).view(np.uint32)).all()
+    # the per-type entry point gives the same bits
+    import ctypes as C
+    from chimere_amd._lib import check, lib
+    fn = {O.Q4_0: "chimere_mmvq_q4_0_multi", O.Q8_0: "chimere_mmvq_q8_0_multi", O.IQ3_S: "chimere_mmvq_iq3s_multi"}[t]
+    y2 = torch.zeros_like(y)
+    wd, xd = dev_t(w, dev), dev_t(xq, dev)
+    getattr(lib(), fn)(C.c_void_p(wd.data_ptr()), C.c_void_p(xd.data_ptr()), C.c_void_p(y2.data_ptr()), ncols, nrows,
+                       xq.shape[1] // 36, ntok, G._stream())
+    check()
+    assert (host(y2).view(np.uint32) == host(y).view(np.uint32)).all()
 
 
 def test_gemv_synth251_fixture(dev):
