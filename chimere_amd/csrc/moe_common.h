@@ -95,7 +95,7 @@ __device__ __forceinline__ void f32_row_dot(const float* __restrict__ a, const f
 // to the lowest index; so does this, in registers: a round takes the wave
 // maximum of the keys f32bits(p) + 1 (0 marks a taken or padding entry; p >= 0
 // so the key order is the order of p; keys < 2^31) by a DPP scan, the lowest index
-// holding it (ballots over l, l+64, ...), and clears that entry.  Weights are
+// holding it (a second DPP scan), and clears that entry.  Weights are
 // renormalised by the sequential sum of the selected probabilities (round
 // order).  Lane k < K writes entry k.  Requires E <= 1024, K <= min(E, 64).
 template <int NV>
@@ -137,17 +137,15 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ logits, int 
 #pragma unroll
         for (int i = 1; i < NV; i++) m = max(m, (int)key[i]);
         m = wave_max_nonneg(m);
-        int win = -1;
+        // the lowest index holding m: a second DPP maximum, of (2^31-1 - index)
+        int c = 0;
 #pragma unroll
-        for (int i = 0; i < NV; i++) {
-            const uint64_t bm = __ballot(key[i] == (uint32_t)m);
-            if (win < 0 && bm) win = __builtin_ctzll(bm) + 64 * i;
-        }
-        if ((win & 63) == lane) {
+        for (int i = NV - 1; i >= 0; i--)
+            if (key[i] == (uint32_t)m) c = 0x7fffffff - (lane + 64 * i);
+        const int win = 0x7fffffff - wave_max_nonneg(c);
 #pragma unroll
-            for (int i = 0; i < NV; i++)
-                if (i == (win >> 6)) key[i] = 0u;
-        }
+        for (int i = 0; i < NV; i++)
+            if (lane + 64 * i == win) key[i] = 0u;
         if (lane == k) { my_idx = win; my_w = __builtin_bit_cast(float, (uint32_t)m - 1u); }
     }
     float ws = 0.0f;
