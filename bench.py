@@ -301,6 +301,21 @@ def main():
         b1 = 4096 * row_bytes(Q8_0, H) + 4096 * 4 + (H // 32) * 36
         extra["dense_q8_0_4096x2048"] = {"us": round(t1 / 256 * 1e6, 2), "GBs": round(b1 / (t1 / 256) / 1e9, 1)}
         del q8w
+        # ---------------- ggml K-quant / MXFP4 GEMV, 16384 x 4096, four copies rotated (timing
+        # only: random block bytes)
+        Rk, Ck = 16384, 4096
+        xk = torch.empty(G.q8_1_row_bytes(Ck), dtype=torch.uint8, device=dev)
+        G.ggml_gpu_quantize_q8_1(torch.randn(Ck, generator=g, device=dev), xk, Ck)
+        yk = torch.empty(Rk, device=dev)
+        for name, fn, rbk in (("q4k", G.ggml_gpu_gemv_q4k_q8, Ck // 256 * 144), ("q5k", G.ggml_gpu_gemv_q5k_q8, Ck // 256 * 176),
+                              ("q6k", G.ggml_gpu_gemv_q6k_q8, Ck // 256 * 210), ("mxfp4", G.ggml_gpu_gemv_mxfp4_q8, Ck // 32 * 17)):
+            wk = torch.randint(0, 256, (4, Rk * rbk), dtype=torch.uint8, device=dev, generator=g)
+            fns = [(lambda i=i, fn=fn, wk=wk: fn(wk[i % 4], xk, yk, Rk, Ck)) for i in range(32)]
+            tk, _ = graph_time(fns)
+            bk = Rk * rbk + Rk * 4 + (Ck // 32) * 36
+            extra[f"{name}_{Rk}x{Ck}"] = {"us": round(tk / 32 * 1e6, 2), "GBs": round(bk / (tk / 32) / 1e9, 1),
+                                          "frac": round(bk / (tk / 32) / 1e9 / HBM_PEAK_GBS, 4)}
+            del wk
 
     # ---------------- CPU baseline: the oracle (C restatement, OpenMP) on this host, M=1 Q4_0 layer
     cpu = None

@@ -9,8 +9,8 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libchimere_hip.so")
 
-Q4_0, Q8_0, IQ3_S = 2, 8, 21
-TYPE_NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", IQ3_S: "iq3s"}
+Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, IQ3_S, MXFP4 = 2, 8, 12, 13, 14, 21, 39
+TYPE_NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", IQ3_S: "iq3s", Q4_K: "q4k", Q5_K: "q5k", Q6_K: "q6k", MXFP4: "mxfp4"}
 
 vp, i32, i64, f32p, szt = C.c_void_p, C.c_int, C.c_int64, C.c_void_p, C.c_size_t
 
@@ -27,6 +27,15 @@ SIGNATURES = [
     ("chimere_mmvq_iq3s_f32", None, [vp, vp, vp, i32, i32, i32, vp, vp]),
     ("chimere_mmvq_q8_0_f32", None, [vp, vp, vp, i32, i32, i32, vp, vp]),
     ("chimere_mmvq_q4_0_f32", None, [vp, vp, vp, i32, i32, i32, vp, vp]),
+    ("chimere_mmvq_q5k", None, [vp, vp, vp, i32, i32, i32, vp]),
+    ("chimere_mmvq_q4k", None, [vp, vp, vp, i32, i32, i32, vp]),
+    ("chimere_mmvq_q6k", None, [vp, vp, vp, i32, i32, i32, vp]),
+    ("chimere_mmvq_mxfp4", None, [vp, vp, vp, i32, i32, i32, vp]),
+    ("chimere_mmvq_q5k_f32", None, [vp, vp, vp, i32, i32, i32, vp, vp]),
+    ("chimere_mmvq_q4k_f32", None, [vp, vp, vp, i32, i32, i32, vp, vp]),
+    ("chimere_mmvq_q6k_f32", None, [vp, vp, vp, i32, i32, i32, vp, vp]),
+    ("chimere_mmvq_mxfp4_f32", None, [vp, vp, vp, vp, i32, i32, i32, vp]),
+    ("chimere_mmvq_mxfp4_batched", None, [vp, vp, vp, vp, i32, i32, i32, i64, i64, i32, vp]),
     ("chimere_mmvq_iq3s_batched", None, [vp, vp, vp, vp, i32, i32, i32, i64, i64, i32, vp]),
     ("chimere_mmvq_q8_0_batched", None, [vp, vp, vp, vp, i32, i32, i32, i64, i64, i32, vp]),
     ("chimere_mmvq_q4_0_batched", None, [vp, vp, vp, vp, i32, i32, i32, i64, i64, i32, vp]),

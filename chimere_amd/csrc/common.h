@@ -14,7 +14,7 @@
 namespace chimere {
 
 // ggml type ids
-enum : int { T_Q4_0 = 2, T_Q8_0 = 8, T_IQ3_S = 21 };
+enum : int { T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ3_S = 21, T_MXFP4 = 39 };
 
 constexpr int QK = 32;             // elements per Q8_0 / Q4_0 / Q8_1 block
 constexpr int Q8_1_BYTES = 36;     // [f16 d][f16 s][i8 q[32]]
@@ -30,9 +30,29 @@ template <int T> struct QTraits;
 template <> struct QTraits<T_Q8_0>  { static constexpr int BYTES = 34;  static constexpr int ELEMS = 32; };
 template <> struct QTraits<T_Q4_0>  { static constexpr int BYTES = 18;  static constexpr int ELEMS = 32; };
 template <> struct QTraits<T_IQ3_S> { static constexpr int BYTES = 110; static constexpr int ELEMS = 256; };
+template <> struct QTraits<T_Q4_K>  { static constexpr int BYTES = 144; static constexpr int ELEMS = 256; };
+template <> struct QTraits<T_Q5_K>  { static constexpr int BYTES = 176; static constexpr int ELEMS = 256; };
+template <> struct QTraits<T_Q6_K>  { static constexpr int BYTES = 210; static constexpr int ELEMS = 256; };
+template <> struct QTraits<T_MXFP4> { static constexpr int BYTES = 17;  static constexpr int ELEMS = 32; };
 
+// Block bytes / elements per block of a type id (0 for an unknown type).
+__host__ __device__ inline int type_block_bytes(int type) {
+    switch (type) {
+    case T_Q8_0: return 34;
+    case T_Q4_0: return 18;
+    case T_IQ3_S: return 110;
+    case T_Q4_K: return 144;
+    case T_Q5_K: return 176;
+    case T_Q6_K: return 210;
+    case T_MXFP4: return 17;
+    default: return 0;
+    }
+}
+__host__ __device__ inline int type_block_elems(int type) {
+    return type == T_IQ3_S || type == T_Q4_K || type == T_Q5_K || type == T_Q6_K ? 256 : 32;
+}
 __host__ __device__ inline int64_t row_bytes(int type, int64_t ncols) {
-    return type == T_Q8_0 ? ncols / 32 * 34 : type == T_Q4_0 ? ncols / 32 * 18 : ncols / 256 * 110;
+    return ncols / type_block_elems(type) * type_block_bytes(type);
 }
 
 __device__ __forceinline__ float h2f(uint32_t h) {
@@ -183,21 +203,51 @@ __device__ __forceinline__ int dot_iq3_s(const uint8_t* row, int off, int ib, co
 // sums are order-free).  Q4_0 values are the raw nibbles (0..15); the -8
 // term is applied with the activation's sum.  IQ3_S: signed grid levels and
 // the sub-block multiplier 1 + 2*scale.
+// Q4_K / Q5_K: unsigned quants 0..15 / 0..31, mult = 6-bit sub-block scale,
+// plus the min term (dm = f32(dmin), mmin = 6-bit sub-block min).  Q6_K:
+// signed quants q-32, mult / mult2 = the int8 scales of elements 0..15 /
+// 16..31.  MXFP4: signed E2M1 levels doubled (int8), dw = 2^(e-128).
 struct WBlk {
     int v[8];
     float dw;
     int mult;
+    float dm;
+    int mmin;
+    int mult2;
 };
 
 template <int T>
 __device__ __forceinline__ int wdot(const WBlk& w, const XBlk& x) {
+    if constexpr (T == T_Q6_K) {
+        int lo = 0, hi = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            lo = dot4(w.v[i], x.q[i], lo);
+            hi = dot4(w.v[4 + i], x.q[4 + i], hi);
+        }
+        return __mul24(lo, w.mult) + __mul24(hi, w.mult2);   // |.| <= 2 * 16*32*127*128 < 2^24
+    }
     int s = 0;
 #pragma unroll
     for (int i = 0; i < 8; i++) s = dot4(w.v[i], x.q[i], s);
     if constexpr (T == T_Q4_0) return s - 8 * x.sumq;
-    else if constexpr (T == T_IQ3_S) return __mul24(s, w.mult);   // |s| < 2^23, mult <= 31
+    else if constexpr (T == T_IQ3_S || T == T_Q4_K || T == T_Q5_K) return __mul24(s, w.mult);   // < 2^23
     else return s;
 }
+
+// One block's update of a lane accumulator in the documented fp32 order:
+// acc = fmaf(f32(d_w)*f32(d_x), (float)sumi, acc); the K-quants with a min
+// (Q4_K, Q5_K) then add fmaf(-(f32(dmin)*f32(d_x)), (float)(m * sum q_x), acc).
+template <int T>
+__device__ __forceinline__ float wacc(const WBlk& w, const XBlk& x, float acc) {
+    acc = __builtin_fmaf(w.dw * x.d, (float)wdot<T>(w, x), acc);
+    if constexpr (T == T_Q4_K || T == T_Q5_K) acc = __builtin_fmaf(-(w.dm * x.d), (float)__mul24(w.mmin, x.sumq), acc);
+    return acc;
+}
+
+// Q8_1 blocks need the sum of their quants for these weight types
+template <int T>
+constexpr bool needs_sumq() { return T == T_Q4_0 || T == T_Q4_K || T == T_Q5_K; }
 
 __device__ __forceinline__ void wdec_q8_0_core(uint32_t dbits, const uint32_t (&q)[8], WBlk& w) {
     w.dw = h2f(dbits);
@@ -235,6 +285,110 @@ __device__ __forceinline__ void wdec_iq3_s_core(uint32_t dbits, uint32_t qs0, ui
     }
 }
 
+// 6-bit scale and min of sub-block j (0..7) from the 12 packed scale bytes
+// (as three little-endian words s0, s1, s2) of a Q4_K / Q5_K superblock
+// (gguf_loader.rs:1150-1163): j < 4: sc = b[j] & 63, m = b[j+4] & 63;
+// j >= 4: sc = (b[j+4] & 15) | (b[j-4] >> 6) << 4, m = (b[j+4] >> 4) | (b[j] >> 6) << 4.
+__device__ __forceinline__ void kq_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j, int& sc, int& m) {
+    if (j < 4) {
+        sc = (int)((s0 >> (8 * j)) & 63u);
+        m = (int)((s1 >> (8 * j)) & 63u);
+    } else {
+        const int k = 8 * (j - 4);
+        const uint32_t hi = (s2 >> k) & 0xFFu;
+        sc = (int)((hi & 15u) | (((s0 >> k) & 0xC0u) >> 2));
+        m = (int)((hi >> 4) | (((s1 >> k) & 0xC0u) >> 2));
+    }
+}
+
+// Q4_K superblock (144 B: f16 d, f16 dmin, scales[12], qs[128]) sub-block ib
+// (gguf_loader.rs:1265-1330): elements 32*ib + l = nibble (ib & 1) of
+// qs[32*(ib/2) + l].  `sb` is 4-byte aligned.
+__device__ __forceinline__ void wdec_q4_k(const uint8_t* sb, int ib, WBlk& w) {
+    const uint32_t* u = (const uint32_t*)sb;
+    w.dw = h2f(u[0] & 0xFFFFu);
+    w.dm = h2f(u[0] >> 16);
+    kq_scale_min(u[1], u[2], u[3], ib, w.mult, w.mmin);
+    const int sh = 4 * (ib & 1);
+    const uint32_t* qs = u + 4 + 8 * (ib >> 1);
+#pragma unroll
+    for (int i = 0; i < 8; i++) w.v[i] = (int)((qs[i] >> sh) & 0x0F0F0F0Fu);
+    w.mult2 = 0;
+}
+
+// Q5_K superblock (176 B: f16 d, f16 dmin, scales[12], qh[32], qs[128])
+// sub-block ib (gguf_loader.rs:1165-1263): the Q4_K nibble plus bit ib of
+// qh[l] as bit 4.  `sb` is 4-byte aligned.
+__device__ __forceinline__ void wdec_q5_k(const uint8_t* sb, int ib, WBlk& w) {
+    const uint32_t* u = (const uint32_t*)sb;
+    w.dw = h2f(u[0] & 0xFFFFu);
+    w.dm = h2f(u[0] >> 16);
+    kq_scale_min(u[1], u[2], u[3], ib, w.mult, w.mmin);
+    const int sh = 4 * (ib & 1);
+    const uint32_t* qh = u + 4;
+    const uint32_t* qs = u + 12 + 8 * (ib >> 1);
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+        w.v[i] = (int)(((qs[i] >> sh) & 0x0F0F0F0Fu) | (((qh[i] >> ib) & 0x01010101u) << 4));
+    w.mult2 = 0;
+}
+
+// Q6_K superblock (210 B: ql[128], qh[64], int8 scales[16], f16 d) sub-block
+// ib = 4*gi + jj (gguf_loader.rs:839-917): element l (0..31) =
+// (nibble (jj >> 1) of ql[64*gi + 32*(jj & 1) + l]) | ((qh[32*gi + l] >> 2*jj) & 3) << 4,
+// minus 32; scale scales[8*gi + 2*jj + l/16].  `row` is a 4-byte aligned
+// buffer, off the superblock's byte offset in it (even).
+__device__ __forceinline__ void wdec_q6_k(const uint8_t* row, int off, int ib, WBlk& w) {
+    const int gi = ib >> 2, jj = ib & 3;
+    const int lo_off = off + 64 * gi + 32 * (jj & 1), hi_off = off + 128 + 32 * gi;
+    const int nsh = 4 * (jj >> 1), hsh = 2 * jj;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const uint32_t u = ((lds_u32(row, lo_off + 4 * i) >> nsh) & 0x0F0F0F0Fu) |
+                           (((lds_u32(row, hi_off + 4 * i) >> hsh) & 0x03030303u) << 4);
+        // u - 32 per byte: t = u ^ 0x20 is the 6-bit two's complement, then sign-extend bit 5
+        const uint32_t t = u ^ 0x20202020u, sgn = t & 0x20202020u;
+        w.v[i] = (int)(t | (sgn << 1) | (sgn << 2));
+    }
+    const uint32_t scw = lds_u16(row, off + 192 + 8 * gi + 2 * jj);
+    w.mult = (int)(int8_t)(scw & 0xFFu);
+    w.mult2 = (int)(int8_t)(scw >> 8);
+    w.dw = h2f(lds_u16(row, off + 208));
+    w.dm = 0.0f;
+    w.mmin = 0;
+}
+
+// 2^(e-128) as a float from the E8M0 byte e (the "half" scale of MXFP4:
+// the element levels below are the E2M1 values doubled).
+__device__ __forceinline__ float e8m0_half(uint32_t e) {
+    const uint32_t bits = e >= 2 ? (e - 1) << 23 : 0x00200000u << e;
+    return __builtin_bit_cast(float, bits);
+}
+
+// MXFP4 block (17 B: E8M0 e, qs[16]; element j = low nibble of qs[j],
+// element j+16 = high nibble).  Nibble n -> level {0,1,2,3,4,6,8,12}[n & 7],
+// negated when n & 8.  `row` 4-byte aligned buffer, off the block's offset.
+__device__ __forceinline__ uint32_t mxfp4_levels(uint32_t nibs) {   // 4 nibbles in byte lanes
+    const uint32_t sel = nibs & 0x07070707u;
+    const uint32_t pos = __builtin_amdgcn_perm(0x0C080604u, 0x03020100u, sel);
+    const uint32_t neg = __builtin_amdgcn_perm(0xF4F8FAFCu, 0xFDFEFF00u, sel);
+    const uint32_t m = __builtin_amdgcn_perm(0u, 0u, ((nibs >> 3) & 0x01010101u) | 0x0C0C0C0Cu);
+    return (pos & ~m) | (neg & m);
+}
+__device__ __forceinline__ void wdec_mxfp4(const uint8_t* row, int off, WBlk& w) {
+    w.dw = e8m0_half(row[off]);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t q = lds_u32(row, off + 1 + 4 * i);
+        w.v[i] = (int)mxfp4_levels(q & 0x0F0F0F0Fu);
+        w.v[4 + i] = (int)mxfp4_levels((q >> 4) & 0x0F0F0F0Fu);
+    }
+    w.mult = 1;
+    w.mult2 = 0;
+    w.dm = 0.0f;
+    w.mmin = 0;
+}
+
 // Block b of a row chunk in LDS (layout as block_dot below), decoded.
 template <int T>
 __device__ __forceinline__ void block_decode(const uint8_t* row, int b, const uint32_t* grid, WBlk& w) {
@@ -250,6 +404,14 @@ __device__ __forceinline__ void block_decode(const uint8_t* row, int b, const ui
 #pragma unroll
         for (int i = 0; i < 4; i++) qs[i] = lds_u32(row, off + 2 + 4 * i);
         wdec_q4_0_core(lds_u16(row, off), qs, w);
+    } else if constexpr (T == T_Q4_K) {
+        wdec_q4_k(row + (b >> 3) * 144, b & 7, w);
+    } else if constexpr (T == T_Q5_K) {
+        wdec_q5_k(row + (b >> 3) * 176, b & 7, w);
+    } else if constexpr (T == T_Q6_K) {
+        wdec_q6_k(row, (b >> 3) * 210, b & 7, w);
+    } else if constexpr (T == T_MXFP4) {
+        wdec_mxfp4(row, b * 17, w);
     } else {
         const int off = (b >> 3) * 110, ib = b & 7;
         const uint32_t sc = row[off + 106 + (ib >> 1)];

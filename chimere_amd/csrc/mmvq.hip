@@ -1,5 +1,6 @@
-// mmvq.hip -- block-quantized GEMV (Q8_0 / Q4_0 / IQ3_S weights x Q8_1
-// activations) for 1..8 tokens, plain / batched-by-expert-id / debug dots.
+// mmvq.hip -- block-quantized GEMV (Q8_0 / Q4_0 / IQ3_S / Q4_K / Q5_K / Q6_K /
+// MXFP4 weights x Q8_1 activations) for 1..8 tokens, plain /
+// batched-by-expert-id / debug dots.
 //
 // Work-group = 256 threads = 16 row groups of 16 lanes; one tile = 16
 // consecutive rows, streamed through LDS by tile_gemv (which documents the
@@ -77,6 +78,10 @@ bool launch_mmvq(int type, const MmvqArgs& a, int nslots, hipStream_t s) {
     case T_Q8_0: launch_t<T_Q8_0>(a, nslots, s); break;
     case T_Q4_0: launch_t<T_Q4_0>(a, nslots, s); break;
     case T_IQ3_S: launch_t<T_IQ3_S>(a, nslots, s); break;
+    case T_Q4_K: launch_t<T_Q4_K>(a, nslots, s); break;
+    case T_Q5_K: launch_t<T_Q5_K>(a, nslots, s); break;
+    case T_Q6_K: launch_t<T_Q6_K>(a, nslots, s); break;
+    case T_MXFP4: launch_t<T_MXFP4>(a, nslots, s); break;
     default: return false;
     }
     return true;
@@ -86,10 +91,10 @@ bool launch_mmvq(int type, const MmvqArgs& a, int nslots, hipStream_t s) {
 static bool check_gemv(const char* who, int type, const void* W, const void* x, const float* y,
                        int ncols, int nrows, int nrows_y_padded, int ntok) {
     if (!W || !x || !y) { set_error(CHIMERE_ERR_ARG, "%s: null pointer", who); return false; }
-    if (type != T_Q8_0 && type != T_Q4_0 && type != T_IQ3_S) {
+    if (type_block_bytes(type) == 0) {
         set_error(CHIMERE_ERR_ARG, "%s: unsupported type %d", who, type); return false;
     }
-    const int elems = type == T_IQ3_S ? 256 : 32;
+    const int elems = type_block_elems(type);
     if (ncols <= 0 || nrows <= 0 || ncols % elems) {
         set_error(CHIMERE_ERR_ARG, "%s: ncols=%d must be a positive multiple of %d (nrows=%d)",
                   who, ncols, elems, nrows);
@@ -100,7 +105,8 @@ static bool check_gemv(const char* who, int type, const void* W, const void* x, 
         return false;
     }
     if (ntok < 1 || ntok > 8) { set_error(CHIMERE_ERR_ARG, "%s: ntok=%d not in 1..8", who, ntok); return false; }
-    if (((uintptr_t)x & 3) != 0 || ((uintptr_t)W & 1) != 0) {
+    // MXFP4's 17-byte blocks have no alignment; every other block starts with an f16
+    if (((uintptr_t)x & 3) != 0 || (type != T_MXFP4 && ((uintptr_t)W & 1) != 0)) {
         set_error(CHIMERE_ERR_ARG, "%s: Q8_1 input must be 4-byte and weights 2-byte aligned", who);
         return false;
     }
@@ -145,31 +151,40 @@ static void gemv_batched_entry(const char* who, int type, const void* W, const v
     check_launch(who);
 }
 
-// ---- debug: exact int32 per-block dots, one thread per (row, block)
-__global__ void k_block_dots(int type, const uint8_t* __restrict__ W, const uint8_t* __restrict__ x,
+// ---- debug: exact int32 per-block dots, one thread per (row, block).
+// Q4_K / Q5_K: the scaled quant dot sc * sum(q*q_x) (the block's min term is
+// m * sum(q_x), a function of the scale bytes and the activation alone).
+template <int T>
+__global__ void k_block_dots(const uint8_t* __restrict__ W, const uint8_t* __restrict__ x,
                              int32_t* __restrict__ out, int ncols, int nrows) {
-    __shared__ uint32_t grid[512];
-    for (int i = threadIdx.x; i < 512; i += blockDim.x) grid[i] = c_iq3s_grid_mmvq[i];
+    __shared__ uint32_t grid[T == T_IQ3_S ? 512 : 1];
+    if constexpr (T == T_IQ3_S)
+        for (int i = threadIdx.x; i < 512; i += blockDim.x) grid[i] = c_iq3s_grid_mmvq[i];
     __syncthreads();
     const int nb = ncols / 32;
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (int64_t)nb * nrows) return;
     const int r = (int)(i / nb), b = (int)(i % nb);
-    const uint8_t* row = W + (int64_t)r * row_bytes(type, ncols);
-    // copy the block (or its superblock) into a private 4-byte aligned buffer
-    uint8_t buf[116] __attribute__((aligned(4)));
-    int len, off;
-    if (type == T_IQ3_S) { len = 110; off = (b >> 3) * 110; }
-    else { len = type == T_Q8_0 ? 34 : 18; off = b * len; }
-    for (int k = 0; k < len; k++) buf[k] = row[off + k];
+    const uint8_t* row = W + (int64_t)r * row_bytes(T, ncols);
+    // the block (or its superblock) copied to a private 4-byte aligned buffer
+    constexpr int SUPER = QTraits<T>::ELEMS == 256;
+    constexpr int LEN = QTraits<T>::BYTES;
+    uint8_t buf[(LEN + 7) / 4 * 4] __attribute__((aligned(4)));
+    const int64_t off = SUPER ? (int64_t)(b >> 3) * LEN : (int64_t)b * LEN;
+    for (int k = 0; k < LEN; k++) buf[k] = row[off + k];
+    for (int k = LEN; k < (int)sizeof(buf); k++) buf[k] = 0;
     XBlk xb;
     load_xblk(x + (int64_t)b * Q8_1_BYTES, xb);
-    float dw;
-    int s;
-    if (type == T_Q8_0) s = dot_q8_0(buf, 0, xb, &dw);
-    else if (type == T_Q4_0) s = dot_q4_0(buf, 0, xb, &dw);
-    else s = dot_iq3_s(buf, 0, b & 7, xb, grid, &dw);
-    out[i] = s;
+    WBlk w;
+    block_decode<T>(buf, SUPER ? (b & 7) : 0, grid, w);
+    out[i] = wdot<T>(w, xb);
+}
+
+template <int T>
+static void launch_block_dots(const void* w, const void* x, int32_t* out, int ncols, int nrows, hipStream_t s) {
+    const int64_t n = (int64_t)(ncols / 32) * nrows;
+    hipLaunchKernelGGL((k_block_dots<T>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (const uint8_t*)w,
+                       (const uint8_t*)x, out, ncols, nrows);
 }
 
 }  // namespace chimere
@@ -214,6 +229,42 @@ void chimere_mmvq_q4_0_batched(const void* w, const void* x, float* y, const int
     gemv_batched_entry("mmvq_q4_0_batched", T_Q4_0, w, x, y, ids, ncols, nrows, nyp, es, is, top_k, s);
 }
 
+// ggml K-quant / MXFP4 entry points (ffi/ggml_cuda_gemv.cu:118-175, 292-460)
+void chimere_mmvq_q5k(const void* w, const void* x, float* y, int ncols, int nrows, int nyp, hipStream_t s) {
+    gemv_entry("mmvq_q5k", T_Q5_K, w, x, y, ncols, nrows, nyp, 1, s);
+}
+void chimere_mmvq_q4k(const void* w, const void* x, float* y, int ncols, int nrows, int nyp, hipStream_t s) {
+    gemv_entry("mmvq_q4k", T_Q4_K, w, x, y, ncols, nrows, nyp, 1, s);
+}
+void chimere_mmvq_q6k(const void* w, const void* x, float* y, int ncols, int nrows, int nyp, hipStream_t s) {
+    gemv_entry("mmvq_q6k", T_Q6_K, w, x, y, ncols, nrows, nyp, 1, s);
+}
+void chimere_mmvq_mxfp4(const void* w, const void* x, float* y, int ncols, int nrows, int nyp, hipStream_t s) {
+    gemv_entry("mmvq_mxfp4", T_MXFP4, w, x, y, ncols, nrows, nyp, 1, s);
+}
+void chimere_mmvq_q5k_f32(const void* w, const float* x, float* y, int ncols, int nrows, int ncp, void* scratch,
+                          hipStream_t s) {
+    gemv_f32_entry("mmvq_q5k_f32", T_Q5_K, w, x, y, ncols, nrows, ncp, scratch, s);
+}
+void chimere_mmvq_q4k_f32(const void* w, const float* x, float* y, int ncols, int nrows, int ncp, void* scratch,
+                          hipStream_t s) {
+    gemv_f32_entry("mmvq_q4k_f32", T_Q4_K, w, x, y, ncols, nrows, ncp, scratch, s);
+}
+void chimere_mmvq_q6k_f32(const void* w, const float* x, float* y, int ncols, int nrows, int ncp, void* scratch,
+                          hipStream_t s) {
+    gemv_f32_entry("mmvq_q6k_f32", T_Q6_K, w, x, y, ncols, nrows, ncp, scratch, s);
+}
+// argument order as the reference's: scratch before the output
+void chimere_mmvq_mxfp4_f32(const void* w, const float* x, void* scratch, float* y, int ncols, int nrows, int ncp,
+                            hipStream_t s) {
+    gemv_f32_entry("mmvq_mxfp4_f32", T_MXFP4, w, x, y, ncols, nrows, ncp, scratch, s);
+}
+// expert ids are read on the device (the reference dereferences them on the host)
+void chimere_mmvq_mxfp4_batched(const void* w, const void* x, float* y, const int* ids, int ncols, int nrows,
+                                int nyp, int64_t es, int64_t is, int top_k, hipStream_t s) {
+    gemv_batched_entry("mmvq_mxfp4_batched", T_MXFP4, w, x, y, ids, ncols, nrows, nyp, es, is, top_k, s);
+}
+
 void chimere_mmvq_multi(int type, const void* w, const void* x, float* y, int ncols, int nrows,
                         int nyp, int ntok, hipStream_t s) {
     gemv_entry("mmvq_multi", type, w, x, y, ncols, nrows, nyp, ntok, s);
@@ -236,9 +287,15 @@ void chimere_dbg_block_dots(int type, const void* w, const void* x, int32_t* out
                             int nrows, hipStream_t s) {
     if (!out || !check_gemv("dbg_block_dots", type, w, x, (const float*)out, ncols, nrows, ncols / 32, 1))
         return;
-    int64_t n = (int64_t)(ncols / 32) * nrows;
-    hipLaunchKernelGGL(k_block_dots, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, type,
-                       (const uint8_t*)w, (const uint8_t*)x, out, ncols, nrows);
+    switch (type) {
+    case T_Q8_0: launch_block_dots<T_Q8_0>(w, x, out, ncols, nrows, s); break;
+    case T_Q4_0: launch_block_dots<T_Q4_0>(w, x, out, ncols, nrows, s); break;
+    case T_IQ3_S: launch_block_dots<T_IQ3_S>(w, x, out, ncols, nrows, s); break;
+    case T_Q4_K: launch_block_dots<T_Q4_K>(w, x, out, ncols, nrows, s); break;
+    case T_Q5_K: launch_block_dots<T_Q5_K>(w, x, out, ncols, nrows, s); break;
+    case T_Q6_K: launch_block_dots<T_Q6_K>(w, x, out, ncols, nrows, s); break;
+    case T_MXFP4: launch_block_dots<T_MXFP4>(w, x, out, ncols, nrows, s); break;
+    }
     check_launch("dbg_block_dots");
 }
 

@@ -10,17 +10,28 @@
 // fp32 order (L=16, G=1): per lane acc = fmaf(f32(d_w)*f32(d_x), (float)sumi,
 // acc) over its blocks in ascending order, then the 16 lanes are summed with
 // the halving tree xor 8,4,2,1 (slot_reduce16).  sumi is the exact int32
-// block dot.
+// block dot.  Q4_K / Q5_K blocks add a second fmaf for their min term (wacc).
 #pragma once
 #include "common.h"
 
 namespace chimere {
 
+// Bytes of `blocks` 32-element blocks of a type-T row (256-element
+// superblock types: whole superblocks, blocks a multiple of 8).
+template <int T>
+__host__ __device__ constexpr int chunk_bytes(int blocks) {
+    return QTraits<T>::ELEMS == 256 ? blocks / 8 * QTraits<T>::BYTES : blocks * QTraits<T>::BYTES;
+}
+// Row chunks whose pieces may be only 4-byte aligned (superblocks of 110 or
+// 210 bytes, 17-byte blocks): staged with the dword asynchronous copy.
+template <int T>
+constexpr bool stage_dw() { return T == T_IQ3_S || T == T_Q6_K || T == T_MXFP4; }
+
 template <int T>
 struct ChunkGeom {
     // Q8_0 rows are 34 B per block: 32 blocks per chunk keeps 64-row tiles in LDS
     static constexpr int BLOCKS = T == T_Q8_0 ? 32 : 64;
-    static constexpr int BYTES = T == T_IQ3_S ? BLOCKS / 8 * 110 : BLOCKS * QTraits<T>::BYTES;
+    static constexpr int BYTES = chunk_bytes<T>(BLOCKS);
 };
 constexpr int MAX_CHUNK_BLOCKS = 64;
 
@@ -56,7 +67,7 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds* __re
                                           int64_t x_tok_stride, const int* toks, int ntok,
                                           float (&acc)[RPG][NT], uint64_t* ph = nullptr) {
     constexpr int NTH = RG * SLOTS;
-    static_assert(CBLK % SLOTS == 0 && (T != T_IQ3_S || CBLK % 8 == 0) && CBLK <= MAX_CHUNK_BLOCKS, "chunk");
+    static_assert(CBLK % SLOTS == 0 && (QTraits<T>::ELEMS != 256 || CBLK % 8 == 0) && CBLK <= MAX_CHUNK_BLOCKS, "chunk");
     const int tid = threadIdx.x;
     const int g = tid >> 4, j = tid & 15;
     const int nr = n1 + n2;
@@ -67,12 +78,12 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds* __re
         for (int t = 0; t < NT; t++) acc[r][t] = 0.0f;
     for (int b0 = 0; b0 < nb; b0 += CBLK) {
         const int cb = min(CBLK, nb - b0);
-        const int seg = T == T_IQ3_S ? cb / 8 * 110 : cb * QTraits<T>::BYTES;
-        const int64_t goff = T == T_IQ3_S ? (int64_t)b0 / 8 * 110 : (int64_t)b0 * QTraits<T>::BYTES;
+        const int seg = chunk_bytes<T>(cb);
+        const int64_t goff = (int64_t)b0 / (QTraits<T>::ELEMS / QK) * QTraits<T>::BYTES;
         __syncthreads();   // previous users of tile / xs are done
         // rows are packed with stride seg (== CB except in a ragged last chunk)
-        if (n1) stage_rows<T == T_IQ3_S, CPOL>(tile, base1 + goff, rb, n1, seg, tid, NTH);
-        if (n2) stage_rows<T == T_IQ3_S, CPOL>(tile + n1 * seg, base2 + goff, rb, n2, seg, tid, NTH);
+        if (n1) stage_rows<stage_dw<T>(), CPOL>(tile, base1 + goff, rb, n1, seg, tid, NTH);
+        if (n2) stage_rows<stage_dw<T>(), CPOL>(tile + n1 * seg, base2 + goff, rb, n2, seg, tid, NTH);
 #ifdef CHIMERE_PHASE_TIMING
         if (ph && tid == 0) ph[4] = __builtin_amdgcn_s_memrealtime();
 #endif
@@ -108,8 +119,7 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds* __re
                         if (t < ntok) {
                             XBlk xb;
                             xlds_to_blk(xs[t * CBLK + b], xb);
-                            const int s = wdot<T>(wb, xb);
-                            acc[r][t] = __builtin_fmaf(wb.dw * xb.d, (float)s, acc[r][t]);
+                            acc[r][t] = wacc<T>(wb, xb, acc[r][t]);
                         }
                     }
                 }
@@ -122,14 +132,8 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds* __re
 
 namespace chimere {
 
-// Bytes of `blocks` 32-element blocks of a type-T row (IQ3_S: whole superblocks).
-template <int T>
-__host__ __device__ constexpr int chunk_bytes(int blocks) {
-    return T == T_IQ3_S ? blocks / 8 * 110 : blocks * QTraits<T>::BYTES;
-}
-
 // Q8_1 block from raw bytes in LDS (36 bytes, 4-byte aligned); the sum of the
-// quants only where the weight type needs it (Q4_0).
+// quants only where the weight type needs it (Q4_0, Q4_K, Q5_K).
 template <int T>
 __device__ __forceinline__ void raw_xblk(const uint8_t* p, XBlk& x) {
     const uint32_t* w = (const uint32_t*)p;
@@ -138,7 +142,7 @@ __device__ __forceinline__ void raw_xblk(const uint8_t* p, XBlk& x) {
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         x.q[i] = (int)w[1 + i];
-        if constexpr (T == T_Q4_0) s = dot4(x.q[i], 0x01010101, s);
+        if constexpr (needs_sumq<T>()) s = dot4(x.q[i], 0x01010101, s);
     }
     x.sumq = s;
 }
@@ -156,7 +160,7 @@ __device__ __forceinline__ void tile_gemv_db(uint8_t* __restrict__ tile, int TB,
                                              const uint8_t* __restrict__ X, int64_t x_tok_stride, const int* toks,
                                              int ntok, float (&acc)[RPG][NT]) {
     constexpr int NTH = RG * SLOTS, XB = NT * CBLK * Q8_1_BYTES;
-    static_assert(CBLK % SLOTS == 0 && (T != T_IQ3_S || CBLK % 8 == 0) && CBLK <= MAX_CHUNK_BLOCKS, "chunk");
+    static_assert(CBLK % SLOTS == 0 && (QTraits<T>::ELEMS != 256 || CBLK % 8 == 0) && CBLK <= MAX_CHUNK_BLOCKS, "chunk");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = tid >> 4, j = tid & 15;
     const int nr = n1 + n2;
@@ -168,10 +172,10 @@ __device__ __forceinline__ void tile_gemv_db(uint8_t* __restrict__ tile, int TB,
     auto issue = [&](int c, int buf) {
         const int b0 = c * CBLK, cb = min(CBLK, nb - b0);
         const int seg = chunk_bytes<T>(cb);
-        const int64_t goff = T == T_IQ3_S ? (int64_t)b0 / 8 * 110 : (int64_t)b0 * QTraits<T>::BYTES;
+        const int64_t goff = (int64_t)b0 / (QTraits<T>::ELEMS / QK) * QTraits<T>::BYTES;
         uint8_t* tb = tile + buf * TB;
-        if (n1) stage_rows<T == T_IQ3_S, CPOL>(tb, base1 + goff, rb, n1, seg, tid, NTH);
-        if (n2) stage_rows<T == T_IQ3_S, CPOL>(tb + n1 * seg, base2 + goff, rb, n2, seg, tid, NTH);
+        if (n1) stage_rows<stage_dw<T>(), CPOL>(tb, base1 + goff, rb, n1, seg, tid, NTH);
+        if (n2) stage_rows<stage_dw<T>(), CPOL>(tb + n1 * seg, base2 + goff, rb, n2, seg, tid, NTH);
         // token t's cb blocks at xraw + buf*XB + t*cb*36 (16-byte pieces)
         const int per = cb * Q8_1_BYTES / 16, tot = ntok * per;
         uint8_t* xb = xraw + buf * XB;
@@ -207,8 +211,7 @@ __device__ __forceinline__ void tile_gemv_db(uint8_t* __restrict__ tile, int TB,
                         if (t < ntok) {
                             XBlk x;
                             raw_xblk<T>(xb + (t * cb + b) * Q8_1_BYTES, x);
-                            const int s = wdot<T>(wb, x);
-                            acc[r][t] = __builtin_fmaf(wb.dw * x.d, (float)s, acc[r][t]);
+                            acc[r][t] = wacc<T>(wb, x, acc[r][t]);
                         }
                     }
                 }

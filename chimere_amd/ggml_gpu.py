@@ -92,6 +92,45 @@ def ggml_gpu_gemv_q4_0_f32(weights, input, output, q8_scratch, nrows, ncols):
     _gemv_f32("chimere_mmvq_q4_0_f32", weights, input, output, q8_scratch, nrows, ncols)
 
 
+def ggml_gpu_gemv_q5k_q8(weights, q8_input, output, nrows, ncols):
+    """ggml_gpu.rs:747 -- Q5_K weights, pre-quantized Q8_1 input."""
+    _gemv_q8("chimere_mmvq_q5k", weights, q8_input, output, nrows, ncols)
+
+
+def ggml_gpu_gemv_q4k_q8(weights, q8_input, output, nrows, ncols):
+    _gemv_q8("chimere_mmvq_q4k", weights, q8_input, output, nrows, ncols)
+
+
+def ggml_gpu_gemv_q6k_q8(weights, q8_input, output, nrows, ncols):
+    _gemv_q8("chimere_mmvq_q6k", weights, q8_input, output, nrows, ncols)
+
+
+def ggml_gpu_gemv_mxfp4_q8(weights, q8_input, output, nrows, ncols):
+    _gemv_q8("chimere_mmvq_mxfp4", weights, q8_input, output, nrows, ncols)
+
+
+def ggml_gpu_gemv_q5k_f32(weights, input, output, q8_scratch, nrows, ncols):
+    """ggml_gpu.rs:834 -- fused F32 -> Q8_1 -> Q5_K GEMV."""
+    _gemv_f32("chimere_mmvq_q5k_f32", weights, input, output, q8_scratch, nrows, ncols)
+
+
+def ggml_gpu_gemv_q4k_f32(weights, input, output, q8_scratch, nrows, ncols):
+    """ggml_gpu.rs:995"""
+    _gemv_f32("chimere_mmvq_q4k_f32", weights, input, output, q8_scratch, nrows, ncols)
+
+
+def ggml_gpu_gemv_q6k_f32(weights, input, output, q8_scratch, nrows, ncols):
+    """ggml_gpu.rs:1034"""
+    _gemv_f32("chimere_mmvq_q6k_f32", weights, input, output, q8_scratch, nrows, ncols)
+
+
+def ggml_gpu_gemv_mxfp4_f32(weights, input, output, q8_scratch, nrows, ncols):
+    """ggml_cuda_gemv.cu:448 (its argument order: scratch before output)."""
+    lib().chimere_mmvq_mxfp4_f32(_ptr(weights), _ptr(input), _ptr(q8_scratch), _ptr(output), ncols, nrows,
+                                 pad(ncols, MATRIX_ROW_PADDING), _stream())
+    check()
+
+
 def _gemv_batched(name, all_weights, q8_input, output, expert_ids, nrows, ncols, expert_stride,
                   input_stride, top_k):
     nrows_y = pad(ncols, MATRIX_ROW_PADDING) // Q8_1_BLOCK_ELEMS
@@ -116,6 +155,13 @@ def ggml_gpu_gemv_q8_0_batched(all_weights, q8_input, output, expert_ids, nrows,
 def ggml_gpu_gemv_q4_0_batched(all_weights, q8_input, output, expert_ids, nrows, ncols, expert_stride,
                                input_stride, top_k):
     _gemv_batched("chimere_mmvq_q4_0_batched", all_weights, q8_input, output, expert_ids, nrows, ncols,
+                  expert_stride, input_stride, top_k)
+
+
+def ggml_gpu_gemv_mxfp4_batched(all_weights, q8_input, output, expert_ids, nrows, ncols, expert_stride,
+                                input_stride, top_k):
+    """ggml_cuda_gemv.cu:425 with device-resident ids."""
+    _gemv_batched("chimere_mmvq_mxfp4_batched", all_weights, q8_input, output, expert_ids, nrows, ncols,
                   expert_stride, input_stride, top_k)
 
 

@@ -79,6 +79,42 @@ void chimere_mmvq_q4_0_f32(const void *weights, const float *input_f32, float *o
                            int ncols, int nrows, int ncols_padded, void *q8_scratch,
                            hipStream_t stream);
 
+/* ggml K-quant and MXFP4 weights (ggml_cuda_gemv.cu:118-175, 292-387, 407-460).
+ * Block layouts: Q4_K 144 B / 256 (f16 d, f16 dmin, 12 packed 6-bit
+ * scale/min bytes, qs[128]; gguf_loader.rs:1265-1330), Q5_K 176 B / 256 (+
+ * qh[32] high bits; gguf_loader.rs:1165-1263), Q6_K 210 B / 256 (ql[128],
+ * qh[64], int8 scales[16], f16 d; gguf_loader.rs:839-917), MXFP4 17 B / 32
+ * (E8M0 scale byte, 16 bytes of E2M1 nibbles, low nibble = element j, high =
+ * j+16).  Per 32-element block: sumi exact in int32; Q4_K / Q5_K add the min
+ * term -f32(dmin)*f32(d_x) * (m * sum q_x) as a second fmaf in the same order. */
+void chimere_mmvq_q5k(const void *weights, const void *input_q8, float *output,
+                      int ncols, int nrows, int nrows_y_padded, hipStream_t stream);
+void chimere_mmvq_q4k(const void *weights, const void *input_q8, float *output,
+                      int ncols, int nrows, int nrows_y_padded, hipStream_t stream);
+void chimere_mmvq_q6k(const void *weights, const void *input_q8, float *output,
+                      int ncols, int nrows, int nrows_y_padded, hipStream_t stream);
+void chimere_mmvq_mxfp4(const void *weights, const void *input_q8, float *output,
+                        int ncols, int nrows, int nrows_y_padded, hipStream_t stream);
+void chimere_mmvq_q5k_f32(const void *weights, const float *input_f32, float *output,
+                          int ncols, int nrows, int ncols_padded, void *q8_scratch,
+                          hipStream_t stream);
+void chimere_mmvq_q4k_f32(const void *weights, const float *input_f32, float *output,
+                          int ncols, int nrows, int ncols_padded, void *q8_scratch,
+                          hipStream_t stream);
+void chimere_mmvq_q6k_f32(const void *weights, const float *input_f32, float *output,
+                          int ncols, int nrows, int ncols_padded, void *q8_scratch,
+                          hipStream_t stream);
+/* ggml_cuda_gemv.cu:448-461: note the argument order (scratch before output). */
+void chimere_mmvq_mxfp4_f32(const void *weights, const float *input_f32, void *q8_scratch,
+                            float *output, int ncols, int nrows, int ncols_padded,
+                            hipStream_t stream);
+/* ggml_cuda_gemv.cu:425-445, same contract as chimere_mmvq_iq3s_batched below:
+ * expert_ids is a DEVICE array (the reference reads it on the host). */
+void chimere_mmvq_mxfp4_batched(const void *all_weights, const void *input_q8, float *output,
+                                const int *expert_ids, int ncols, int nrows, int nrows_y_padded,
+                                int64_t expert_stride, int64_t input_stride, int top_k,
+                                hipStream_t stream);
+
 /* Batched expert GEMV with device-resident expert ids (ggml_cuda_gemv.cu:243-279):
  * for k < top_k: output[k*nrows + r] = W_{ids[k]}[r,:] . x_k with
  * W_e = all_weights + e*expert_stride bytes and x_k = input_q8 + k*input_stride
@@ -202,7 +238,9 @@ void chimere_quantize_weights(int type, const float *x, void *out, int64_t n,
 
 /* ------------------------------------------------------------ debug */
 /* Exact int32 per-block dots: out[r*(ncols/32) + b] (IQ3_S: per 32-element
- * sub-block, already multiplied by its (1 + 2*scale)). */
+ * sub-block, already multiplied by its (1 + 2*scale); Q4_K / Q5_K: sc*sum q*q_x
+ * without the min term; Q6_K: sc_lo*sum_lo + sc_hi*sum_hi of q-32).  type is a
+ * ggml id: Q4_0 2, Q8_0 8, Q4_K 12, Q5_K 13, Q6_K 14, IQ3_S 21, MXFP4 39. */
 void chimere_dbg_block_dots(int type, const void *weights, const void *input_q8,
                             int32_t *out, int ncols, int nrows, hipStream_t stream);
 

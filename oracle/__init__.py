@@ -10,7 +10,7 @@ import subprocess as _sp
 
 import numpy as np
 
-Q4_0, Q8_0, IQ3_S = 2, 8, 21
+Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, IQ3_S, MXFP4 = 2, 8, 12, 13, 14, 21, 39
 _HERE = _os.path.dirname(_os.path.abspath(__file__))
 _LIB = None
 
@@ -60,7 +60,8 @@ def pad512(n):
 
 
 def row_bytes(t, ncols):
-    return {Q8_0: ncols // 32 * 34, Q4_0: ncols // 32 * 18, IQ3_S: ncols // 256 * 110}[t]
+    return {Q8_0: ncols // 32 * 34, Q4_0: ncols // 32 * 18, IQ3_S: ncols // 256 * 110, Q4_K: ncols // 256 * 144,
+            Q5_K: ncols // 256 * 176, Q6_K: ncols // 256 * 210, MXFP4: ncols // 32 * 17}[t]
 
 
 def f32_to_f16(x):

@@ -21,6 +21,15 @@
  *   shared-expert gate  cs/src/scratch_pool.rs:243-277
  *   MoE op order        cs/src/qwen35_model/moe_ffn.rs:1081-1768
  *   f64 Q8_0 CPU path   cs/ffi/src/lib.rs:107-154
+ *   Q4_K / Q5_K layout  cs/src/gguf_loader.rs:1145-1330 (get_scale_min_k4 :1150-1163)
+ *   Q6_K layout         cs/src/gguf_loader.rs:839-917
+ *   K-quant dot ints    cs/kernels/chimere_kernels.cu:1344-1440 (sc * sum q*q_x and
+ *                       m * sum q_x, both exact integers)
+ *   MXFP4               entry points only (cs/ffi/ggml_cuda_gemv.cu:407-460); the
+ *                       block layout is ggml's published one (no code in the
+ *                       reference tree): [E8M0 e][16 B nibbles], level table
+ *                       {0,1,2,3,4,6,8,12} (E2M1 doubled), sign = bit 3,
+ *                       scale 2^(e-128).
  */
 #include "oracle.h"
 #include <math.h>
@@ -114,6 +123,10 @@ int64_t orc_row_bytes(int type, int64_t ncols) {
     case ORC_Q8_0: return ncols / 32 * 34;
     case ORC_Q4_0: return ncols / 32 * 18;
     case ORC_IQ3_S: return ncols / 256 * 110;
+    case ORC_Q4_K: return ncols / 256 * 144;
+    case ORC_Q5_K: return ncols / 256 * 176;
+    case ORC_Q6_K: return ncols / 256 * 210;
+    case ORC_MXFP4: return ncols / 32 * 17;
     default: return -1;
     }
 }
@@ -258,6 +271,44 @@ static inline int iq3s_mult(const uint8_t *blk, int ib) {
     return 1 + 2 * ((blk[106 + ib / 2] >> (4 * (ib & 1))) & 0xF);
 }
 
+/* Q4_K / Q5_K 6-bit scale and min of sub-block j (gguf_loader.rs:1150-1163) */
+static void kq_scale_min(const uint8_t *sc12, int j, int *sc, int *m) {
+    if (j < 4) {
+        *sc = sc12[j] & 63;
+        *m = sc12[j + 4] & 63;
+    } else {
+        *sc = (sc12[j + 4] & 0xF) | ((sc12[j - 4] >> 6) << 4);
+        *m = (sc12[j + 4] >> 4) | ((sc12[j] >> 6) << 4);
+    }
+}
+/* unsigned quant of element e (0..31) of sub-block ib: Q4_K 0..15, Q5_K 0..31 */
+static inline int q4k_quant(const uint8_t *blk, int ib, int e) {
+    return (blk[16 + 32 * (ib / 2) + e] >> (4 * (ib & 1))) & 0xF;
+}
+static inline int q5k_quant(const uint8_t *blk, int ib, int e) {
+    return ((blk[48 + 32 * (ib / 2) + e] >> (4 * (ib & 1))) & 0xF) | (((blk[16 + e] >> ib) & 1) << 4);
+}
+/* Q6_K signed quant (q - 32) of element e of sub-block ib, and its int8 scale */
+static inline int q6k_quant(const uint8_t *blk, int ib, int e) {
+    int gi = ib / 4, jj = ib % 4;
+    int lo = (blk[64 * gi + 32 * (jj & 1) + e] >> (4 * (jj >> 1))) & 0xF;
+    int hi = (blk[128 + 32 * gi + e] >> (2 * jj)) & 3;
+    return (lo | (hi << 4)) - 32;
+}
+static inline int q6k_scale(const uint8_t *blk, int ib, int e) {
+    return (int8_t)blk[192 + 8 * (ib / 4) + 2 * (ib % 4) + e / 16];
+}
+static const int8_t mxfp4_level[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
+static inline float e8m0_half(uint8_t e) {   /* 2^(e-128), exact */
+    uint32_t bits = e >= 2 ? (uint32_t)(e - 1) << 23 : 0x00200000u << e;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+static inline int mxfp4_quant(const uint8_t *blk, int e) {
+    return mxfp4_level[e < 16 ? blk[1 + e] & 0xF : blk[1 + e - 16] >> 4];
+}
+
 void orc_dequantize(int type, const uint8_t *w, int64_t n, float *out) {
     if (type == ORC_Q8_0) {
         for (int64_t b = 0; b < n / 32; b++) {
@@ -282,18 +333,53 @@ void orc_dequantize(int type, const uint8_t *w, int64_t n, float *out) {
                 for (int e = 0; e < 32; e++) out[sb * 256 + ib * 32 + e] = db * (float)iq3s_level(o, ib, e);
             }
         }
+    } else if (type == ORC_Q4_K || type == ORC_Q5_K) {
+        /* gguf_loader.rs:1228-1257 / :1310-1327: d*sc*q - dmin*m */
+        const int bytes = type == ORC_Q4_K ? 144 : 176;
+        for (int64_t sb = 0; sb < n / 256; sb++) {
+            const uint8_t *o = w + sb * bytes;
+            float d = orc_f16_to_f32(rd16(o)), dmin = orc_f16_to_f32(rd16(o + 2));
+            for (int ib = 0; ib < 8; ib++) {
+                int sc, m;
+                kq_scale_min(o + 4, ib, &sc, &m);
+                float d1 = d * (float)sc, m1 = dmin * (float)m;
+                for (int e = 0; e < 32; e++) {
+                    int q = type == ORC_Q4_K ? q4k_quant(o, ib, e) : q5k_quant(o, ib, e);
+                    out[sb * 256 + ib * 32 + e] = d1 * (float)q - m1;
+                }
+            }
+        }
+    } else if (type == ORC_Q6_K) {
+        for (int64_t sb = 0; sb < n / 256; sb++) {
+            const uint8_t *o = w + sb * 210;
+            float d = orc_f16_to_f32(rd16(o + 208));
+            for (int ib = 0; ib < 8; ib++)
+                for (int e = 0; e < 32; e++)
+                    out[sb * 256 + ib * 32 + e] = d * (float)q6k_scale(o, ib, e) * (float)q6k_quant(o, ib, e);
+        }
+    } else if (type == ORC_MXFP4) {
+        for (int64_t b = 0; b < n / 32; b++) {
+            const uint8_t *o = w + b * 17;
+            float d = e8m0_half(o[0]);
+            for (int e = 0; e < 32; e++) out[b * 32 + e] = (float)mxfp4_quant(o, e) * d;
+        }
     }
 }
 
 /* ---------------------------------------------------------- block dots */
 
 /* int32 dot of weight block b of a row with the Q8_1 block b; *scale gets
- * f32(d_w) * f32(d_x). */
-static inline int32_t block_dot(int type, const uint8_t *row, const uint8_t *xq, int b, float *scale) {
+ * f32(d_w) * f32(d_x).  Q4_K / Q5_K also give the min term's integer
+ * m * sum(q_x) in *s2 and its scale -(f32(dmin) * f32(d_x)) in *scale2
+ * (*s2 = 0 for the other types). */
+static inline int32_t block_dot2(int type, const uint8_t *row, const uint8_t *xq, int b, float *scale,
+                                 int32_t *s2, float *scale2) {
     const uint8_t *xb = xq + (int64_t)b * 36;
     const int8_t *qx = (const int8_t *)(xb + 4);
     float dx = orc_f16_to_f32(rd16(xb));
     int32_t s = 0;
+    *s2 = 0;
+    *scale2 = 0.0f;
     if (type == ORC_Q8_0) {
         const uint8_t *o = row + (int64_t)b * 34;
         for (int i = 0; i < 32; i++) s += (int32_t)(int8_t)o[2 + i] * qx[i];
@@ -305,14 +391,42 @@ static inline int32_t block_dot(int type, const uint8_t *row, const uint8_t *xq,
             s += ((o[2 + j] >> 4) - 8) * qx[j + 16];
         }
         *scale = orc_f16_to_f32(rd16(o)) * dx;
-    } else {
+    } else if (type == ORC_IQ3_S) {
         const uint8_t *o = row + (int64_t)(b >> 3) * 110;
         int ib = b & 7;
         for (int e = 0; e < 32; e++) s += iq3s_level(o, ib, e) * qx[e];
         s *= iq3s_mult(o, ib);
         *scale = orc_f16_to_f32(rd16(o)) * dx;
+    } else if (type == ORC_Q4_K || type == ORC_Q5_K) {
+        const uint8_t *o = row + (int64_t)(b >> 3) * (type == ORC_Q4_K ? 144 : 176);
+        int ib = b & 7, sc, m, sx = 0;
+        kq_scale_min(o + 4, ib, &sc, &m);
+        for (int e = 0; e < 32; e++) {
+            s += (type == ORC_Q4_K ? q4k_quant(o, ib, e) : q5k_quant(o, ib, e)) * qx[e];
+            sx += qx[e];
+        }
+        s *= sc;
+        *scale = orc_f16_to_f32(rd16(o)) * dx;
+        *s2 = m * sx;
+        *scale2 = -(orc_f16_to_f32(rd16(o + 2)) * dx);
+    } else if (type == ORC_Q6_K) {
+        const uint8_t *o = row + (int64_t)(b >> 3) * 210;
+        int ib = b & 7, lo = 0, hi = 0;
+        for (int e = 0; e < 16; e++) lo += q6k_quant(o, ib, e) * qx[e];
+        for (int e = 16; e < 32; e++) hi += q6k_quant(o, ib, e) * qx[e];
+        s = q6k_scale(o, ib, 0) * lo + q6k_scale(o, ib, 16) * hi;
+        *scale = orc_f16_to_f32(rd16(o + 208)) * dx;
+    } else if (type == ORC_MXFP4) {
+        const uint8_t *o = row + (int64_t)b * 17;
+        for (int e = 0; e < 32; e++) s += mxfp4_quant(o, e) * qx[e];
+        *scale = e8m0_half(o[0]) * dx;
     }
     return s;
+}
+static inline int32_t block_dot(int type, const uint8_t *row, const uint8_t *xq, int b, float *scale) {
+    int32_t s2;
+    float sc2;
+    return block_dot2(type, row, xq, b, scale, &s2, &sc2);
 }
 
 void orc_block_dots(int type, const uint8_t *W, const uint8_t *xq,
@@ -329,10 +443,12 @@ static float row_dot(int type, const uint8_t *row, const uint8_t *xq, int nb, in
     float acc[256];
     for (int j = 0; j < L; j++) acc[j] = 0.0f;
     for (int b = 0; b < nb; b++) {
-        float sc;
-        int32_t s = block_dot(type, row, xq, b, &sc);
+        float sc, sc2;
+        int32_t s2;
+        int32_t s = block_dot2(type, row, xq, b, &sc, &s2, &sc2);
         int j = (b / G) % L;
         acc[j] = fmaf(sc, (float)s, acc[j]);
+        if (type == ORC_Q4_K || type == ORC_Q5_K) acc[j] = fmaf(sc2, (float)s2, acc[j]);
     }
     for (int m = L / 2; m >= 1; m >>= 1)
         for (int i = 0; i < m; i++) acc[i] = acc[i] + acc[i + m];

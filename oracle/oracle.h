@@ -12,7 +12,12 @@
  *   Q8_1  36 B / 32 elem : [f16 d][f16 s][i8 q[32]]          chimere_kernels.cu:1495-1523
  *   IQ3_S 110 B / 256 elem: [f16 d][qs 64][qh 8][signs 32][scales 4]
  *                                                           gguf_loader.rs:1008-1142
- * Type ids follow ggml's enum: Q4_0 = 2, Q8_0 = 8, IQ3_S = 21.
+ *   Q4_K  144 B / 256    : [f16 d][f16 dmin][scales 12][qs 128]   gguf_loader.rs:1265-1330
+ *   Q5_K  176 B / 256    : [f16 d][f16 dmin][scales 12][qh 32][qs 128]  :1165-1263
+ *   Q6_K  210 B / 256    : [ql 128][qh 64][i8 scales 16][f16 d]   gguf_loader.rs:839-917
+ *   MXFP4  17 B / 32     : [E8M0 e][u8 nib[16]] lo=j, hi=j+16     (ggml layout, see oracle.c)
+ * Type ids follow ggml's enum: Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q5_K = 13,
+ * Q6_K = 14, IQ3_S = 21, MXFP4 = 39.
  *
  * Canonical fp32 order ("L,G order") of a quantized row dot product:
  *   per 32-element block b (IQ3_S: sub-block b = 8*superblock + ib):
@@ -20,6 +25,9 @@
  *     scale_b = f32(d_w) * f32(d_x)                  (one rounding)
  *   slot j in [0,L) accumulates the blocks with (b / G) % L == j, ascending b:
  *     acc_j = fmaf(scale_b, (float)sumi_b, acc_j)    starting from +0.0f
+ *     Q4_K / Q5_K then: acc_j = fmaf(-(f32(dmin)*f32(d_x)), (float)(m_b * sum q_x), acc_j)
+ *     (their sumi_b = sc_b * sum q*q_x; Q6_K's = sc_lo*sum_lo + sc_hi*sum_hi of q-32;
+ *      MXFP4's scale_b = 2^(e-128) * f32(d_x))
  *   then a halving tree: for m = L/2 .. 1: acc_i += acc_{i+m} (i < m); y = acc_0.
  * The GPU kernels document the (L, G) they use; the oracle reproduces that
  * order so that fp32 outputs (and hence every re-quantized intermediate)
@@ -32,7 +40,7 @@
 extern "C" {
 #endif
 
-enum { ORC_Q4_0 = 2, ORC_Q8_0 = 8, ORC_IQ3_S = 21 };
+enum { ORC_Q4_0 = 2, ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q5_K = 13, ORC_Q6_K = 14, ORC_IQ3_S = 21, ORC_MXFP4 = 39 };
 
 uint16_t orc_f32_to_f16(float x);
 float    orc_f16_to_f32(uint16_t h);

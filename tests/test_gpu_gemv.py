@@ -169,3 +169,78 @@ def test_q4_0_head_full_size(dev):
     G.ggml_gpu_quantize_q8_1(-x, xq, H)
     G.ggml_gpu_gemv_q4_0_q8(w, xq, y, V, H)
     assert (host(y) == -yg).all()
+
+
+# ---- ggml K-quants and MXFP4 (ffi/ggml_cuda_gemv.cu:118-175, 292-460)
+
+KQ_FN = {O.Q4_K: ("chimere_mmvq_q4k", "chimere_mmvq_q4k_f32"), O.Q5_K: ("chimere_mmvq_q5k", "chimere_mmvq_q5k_f32"),
+         O.Q6_K: ("chimere_mmvq_q6k", "chimere_mmvq_q6k_f32"), O.MXFP4: ("chimere_mmvq_mxfp4", None)}
+KQ_SHAPES = [(4096, 2048), (37, 2304), (300, 4096), (16, 256)]
+
+
+@pytest.mark.parametrize("t", [O.Q4_K, O.Q5_K, O.Q6_K, O.MXFP4])
+@pytest.mark.parametrize("nrows,ncols", KQ_SHAPES + [(64, 2080), (19, 96)])
+def test_kquant_gemv_bit_exact(dev, t, nrows, ncols):
+    """Bit-exact against the oracle's (L=16, G=1) order; within 1e-5 of the
+    float64 result; int32 block dots exact; the fused f32 entry gives the same
+    bits.  (64, 2080) and (19, 96) are MXFP4-only shapes (rows not 4-byte
+    aligned)."""
+    if O.row_bytes(t, ncols) <= 0 or (t != O.MXFP4 and ncols % 256):
+        pytest.skip("shape not valid for this type")
+    print(f"kquant gemv type={t} {nrows}x{ncols}", flush=True)
+    rng = np.random.default_rng(nrows * 3 + ncols + t)
+    w = npref.rand_kq(t, nrows, ncols, rng)
+    x = rng.standard_normal(ncols).astype(np.float32)
+    pad = G.pad(ncols, 512)
+    xq = O.quantize_q8_1(x, pad)
+    wd, xd, xqd = dev_t(w, dev), dev_t(x, dev), dev_t(xq, dev)
+    import ctypes as C
+    from chimere_amd._lib import check, lib
+    y = torch.zeros(nrows, dtype=torch.float32, device=dev)
+    q8, f32 = KQ_FN[t]
+    getattr(lib(), q8)(C.c_void_p(wd.data_ptr()), C.c_void_p(xqd.data_ptr()), C.c_void_p(y.data_ptr()), ncols,
+                       nrows, pad // 32, G._stream())
+    check()
+    yg = host(y)
+    yo = O.gemv(t, w, xq, ncols, nrows, L=16, G=1)
+    assert (yg.view(np.uint32) == yo.view(np.uint32)).all()
+    y64 = npref.kq_gemv_f64(t, w, xq, ncols)
+    assert np.linalg.norm(yg - y64) / np.linalg.norm(y64) < 1e-5
+    bd = torch.zeros(nrows, ncols // 32, dtype=torch.int32, device=dev)
+    G.block_dots(t, wd, xqd, bd, nrows, ncols)
+    assert (host(bd) == O.block_dots(t, w, xq, ncols, nrows)).all()
+    scratch = torch.zeros(pad // 32 * 36, dtype=torch.uint8, device=dev)
+    y2 = torch.zeros(nrows, dtype=torch.float32, device=dev)
+    {O.Q4_K: G.ggml_gpu_gemv_q4k_f32, O.Q5_K: G.ggml_gpu_gemv_q5k_f32, O.Q6_K: G.ggml_gpu_gemv_q6k_f32,
+     O.MXFP4: G.ggml_gpu_gemv_mxfp4_f32}[t](wd, xd, y2, scratch, nrows, ncols)
+    assert (host(y2).view(np.uint32) == yo.view(np.uint32)).all()
+
+
+@pytest.mark.parametrize("t", [O.Q4_K, O.Q5_K, O.Q6_K, O.MXFP4])
+def test_kquant_multi_token(dev, t):
+    rng = np.random.default_rng(400 + t)
+    nrows, ncols, ntok = 100, 2048, 3
+    w = npref.rand_kq(t, nrows, ncols, rng)
+    xq = O.quantize_q8_1(rng.standard_normal((ntok, ncols)).astype(np.float32))
+    y = torch.zeros(ntok, nrows, dtype=torch.float32, device=dev)
+    G.gemv_multi(t, dev_t(w, dev), dev_t(xq, dev), y, nrows, ncols, ntok)
+    yo = O.gemv(t, w, xq, ncols, nrows, ntok=ntok, xq_stride=xq.shape[1])
+    assert (host(y).view(np.uint32) == np.asarray(yo).view(np.uint32)).all()
+
+
+def test_mxfp4_batched_device_ids(dev):
+    """chimere_mmvq_mxfp4_batched reads the expert ids on the device (the
+    reference's host-side dereference, ggml_cuda_gemv.cu:438-444, is not kept)."""
+    rng = np.random.default_rng(39)
+    E, F, H, K = 6, 48, 1024, 4
+    w = npref.rand_kq(O.MXFP4, E * F, H, rng).reshape(E, -1)
+    xq = O.quantize_q8_1(rng.standard_normal((K, H)).astype(np.float32))
+    ids = np.array([5, 0, 5, 2], np.int32)
+    wd, xqd, idd = dev_t(w, dev), dev_t(xq, dev), dev_t(ids, dev)
+    for stride in (0, xq.shape[1]):
+        y = torch.zeros(K * F, dtype=torch.float32, device=dev)
+        G.ggml_gpu_gemv_mxfp4_batched(wd, xqd, y, idd, F, H, w.shape[1], stride, K)
+        yg = host(y).reshape(K, F)
+        for k in range(K):
+            yo = O.gemv(O.MXFP4, w[ids[k]], xq[k] if stride else xq[0], H, F)
+            assert (yg[k].view(np.uint32) == yo.view(np.uint32)).all()
