@@ -317,6 +317,30 @@ def main():
                                           "frac": round(bk / (tk / 32) / 1e9 / HBM_PEAK_GBS, 4)}
             del wk
 
+        # ---------------- attainable rates on this part (beside the datasheet peaks)
+        from chimere_amd._lib import lib as _clib
+        import ctypes as _C
+        big = torch.empty(2 << 30, dtype=torch.uint8, device=dev)
+        big.fill_(1)
+        fold = torch.empty(8192, dtype=torch.int32, device=dev)
+        best_rd = 0.0
+        for nb in (1024, 2048, 4096, 8192):
+            fns = [(lambda nb=nb: _clib().chimere_dbg_stream_read(_C.c_void_p(big.data_ptr()), big.numel(),
+                                                                  _C.c_void_p(fold.data_ptr()), nb, G._stream()))
+                   for _ in range(3)]
+            tr, _ = graph_time(fns)
+            best_rd = max(best_rd, big.numel() / (tr / 3) / 1e9)
+        del big
+        mo = torch.empty(1024 * 256, dtype=torch.int32, device=dev)
+        iters = 4000
+        fns = [lambda: _clib().chimere_dbg_mfma_i8(_C.c_void_p(mo.data_ptr()), iters, 1024, G._stream())]
+        tm, _ = graph_time(fns)
+        mops = 1024 * 4 * 4 * iters * 2 * 32 * 32 * 32 / tm / 1e12
+        extra["attainable"] = {"hbm_read_GBs": round(best_rd, 1), "hbm_read_frac_of_peak": round(best_rd / HBM_PEAK_GBS, 4),
+                               "mfma_i8_TOPs": round(mops, 1), "mfma_i8_frac_of_peak": round(mops / 5000.0, 4),
+                               "method": "2 GiB non-temporal dwordx4 read, best of 1024-8192 work-groups; "
+                                         "1024 WGs x 4 waves x 4 chains of v_mfma_i32_32x32x32_i8"}
+
     # ---------------- CPU baseline: the oracle (C restatement, OpenMP) on this host, M=1 Q4_0 layer
     cpu = None
     if not args.no_cpu:
@@ -333,9 +357,24 @@ def main():
             O.moe(xh[n % NSLOT:n % NSLOT + 1], *hw, O.Q4_0, K, sh=hsh, sh_type=O.Q4_0, nthreads=nthreads)
             n += 1
         dt = (time.perf_counter() - t0) / n
+        # single-thread figure on a shorter sample
+        n1, t1c = 0, time.perf_counter()
+        while time.perf_counter() - t1c < max(1.0, args.cpu_seconds / 4) and n1 < 500:
+            O.moe(xh[n1 % NSLOT:n1 % NSLOT + 1], *hw, O.Q4_0, K, sh=hsh, sh_type=O.Q4_0, nthreads=1)
+            n1 += 1
+        dt1 = (time.perf_counter() - t1c) / n1
+        model = ""
+        try:
+            for ln in open("/proc/cpuinfo"):
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+        except OSError:
+            pass
         cpu = {"value": round(sel_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
                "sample": f"{n} M=1 Q4_0 MoE layer calls of config 3 (oracle/oracle.c, OpenMP row-parallel), "
-                         f"{dt * 1e6:.0f} us/layer"}
+                         f"{dt * 1e6:.0f} us/layer",
+               "single_thread_GBs": round(sel_bytes / dt1 / 1e9, 3), "nproc": os.cpu_count(), "cpu_model": model}
 
     if args.calib_copy_mb:
         src = torch.empty(args.calib_copy_mb << 18, dtype=torch.float32, device=dev).fill_(1.0)
