@@ -8,7 +8,7 @@
 // fences or counters are needed):
 //   K1 k_moe_route    one work-group per router row (+1 for the shared-expert
 //                     gate vector) computing f32 logits for every token, plus
-//                     one work-group per token quantizing x to Q8_1.
+//                     work-groups quantizing x to Q8_1 (8 blocks each).
 //   K2 k_moe_expert   (distinct expert | shared) x (32-row block w of F).
 //                     Each routed work-group recomputes softmax/top-k (one wave
 //                     per token, registers only) and the distinct-expert plan
@@ -95,12 +95,14 @@ __global__ __launch_bounds__(256) void k_moe_route(MoeArgs a) {
     const int row = blockIdx.x;
     const int ng = a.sh_gate_w ? 1 : 0;
     if (row >= a.E + ng) {
-        const int t = row - a.E - ng;
-        const int nb = a.H / QK;
-        const float* xt = a.x + (int64_t)t * a.H;
-        uint8_t* dst = a.xq + t * a.xq_stride;
+        // Q8_1(x): 8 blocks per work-group (one per half-wave), so that this
+        // part of the grid finishes with the router rows
+        const int nb = a.H / QK, qwg = (nb + 7) / 8;
+        const int r = row - a.E - ng, t = r / qwg, b0 = (r - t * qwg) * 8;
+        const float* xt = a.x + (int64_t)t * a.H + (int64_t)b0 * QK;
+        uint8_t* dst = a.xq + t * a.xq_stride + b0 * Q8_1_BYTES;
         quantize_blocks(
-            nb, [&](int b, int i) { return xt[b * QK + i]; },
+            min(8, nb - b0), [&](int b, int i) { return xt[b * QK + i]; },
             [&](int b, int i, int q, float d, float sum) {
                 uint8_t* blk = dst + b * Q8_1_BYTES;
                 blk[4 + i] = (uint8_t)(int8_t)q;
@@ -179,7 +181,15 @@ __device__ __forceinline__ void route_plan(const MoeArgs& a, int* first, Plan& p
     const int MK = a.M * a.K;
 
     const int wave = tid >> 6;
+#ifdef CHIMERE_PHASE_TIMING
+    if (tid == 0) {   // latency of the first logits load alone
+        volatile float v = *(volatile const float*)(a.logits + 5);
+        (void)v;
+        PHASE(1, 10);
+    }
+#endif
     if (wave < a.M) topk_wave_any(a.logits + wave * a.E, a.E, a.K, s_ids + wave * a.K, s_w + wave * a.K);
+    PHASE(1, 1);
     if (a.M == 1) {
         // one token: its K experts are distinct; unit k = the k-th selected
         __syncthreads();
@@ -741,6 +751,12 @@ static WsPlan plan_ws(int H, int F, int E, int K, int M) {
     return p;
 }
 
+// K1 grid: router rows (+ the shared-expert gate row) and 8 Q8_1 blocks of x
+// per work-group
+static int route_grid(const MoeArgs& a) {
+    return a.E + (a.sh_gate_w ? 1 : 0) + a.M * ((a.H / QK + 7) / 8);
+}
+
 // K2 grid: all items, capped at one work-group per CU (a multiple of 8)
 static int expert_grid(int items) {
     static int cus[64] = {0};
@@ -758,7 +774,7 @@ static int expert_grid(int items) {
 template <int TE, int TS, int NT>
 static void launch_layer_nt(const MoeArgs& a, int stage, hipStream_t s) {
     if (stage < 0 || stage == 0)
-        hipLaunchKernelGGL((k_moe_route<NT>), dim3(a.E + (a.sh_gate_w ? 1 : 0) + a.M), dim3(256), 0, s, a);
+        hipLaunchKernelGGL((k_moe_route<NT>), dim3(route_grid(a)), dim3(256), 0, s, a);
     if (stage < 0 || stage == 1)
         hipLaunchKernelGGL((k_moe_expert<TE, TS, NT>), dim3(expert_grid(256)), dim3(EX_THREADS), 0, s, a);
     if (stage < 0 || stage == 2)
@@ -770,7 +786,7 @@ template <int TE, int TS>
 static void launch_layer_multi(const MoeArgs& a, int stage, hipStream_t s) {
     const int NB = a.F / QK, NU = a.M * a.K + 1;
     if (stage < 0 || stage == 0) {
-        hipLaunchKernelGGL((k_moe_route<MAX_TOK>), dim3(a.E + (a.sh_gate_w ? 1 : 0) + a.M), dim3(256), 0, s, a);
+        hipLaunchKernelGGL((k_moe_route<MAX_TOK>), dim3(route_grid(a)), dim3(256), 0, s, a);
         hipLaunchKernelGGL(k_moe_plan, dim3(1), dim3(EX_THREADS), 0, s, a);
     }
     if (stage < 0 || stage == 1)
