@@ -66,12 +66,13 @@ __device__ __forceinline__ uint32_t f2h(float x) {   // round to nearest even
 // reduction with ln2 split 0x1.62e4p-1 + 0x1.7f7d1cp-20, degree-7 Taylor
 // polynomial of e^r in Horner form, scaling by 2^n.  x < -86 -> 0,
 // x > 88.7228 -> +inf.  Relative error about 1 ulp.
+// Branch-free: the polynomial runs on x clamped to the finite range and the
+// special cases are selected afterwards (identical results, and several
+// exponentials in a row interleave).
 __device__ __forceinline__ float det_exp(float x) {
-    if (x != x) return x;
-    if (x > 88.72283905f) return __builtin_huge_valf();
-    if (x < -86.0f) return 0.0f;
-    float n = __builtin_rintf(x * 0x1.715476p+0f);
-    float r = __builtin_fmaf(-n, 0x1.62e4p-1f, x);
+    const float xc = __builtin_fminf(__builtin_fmaxf(x, -86.0f), 88.72283905f);
+    float n = __builtin_rintf(xc * 0x1.715476p+0f);
+    float r = __builtin_fmaf(-n, 0x1.62e4p-1f, xc);
     r = __builtin_fmaf(-n, 0x1.7f7d1cp-20f, r);
     float p = 0x1.a01a02p-13f;
     p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
@@ -81,7 +82,10 @@ __device__ __forceinline__ float det_exp(float x) {
     p = __builtin_fmaf(p, r, 0.5f);
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
-    return __builtin_ldexpf(p, (int)n);
+    float e = __builtin_ldexpf(p, (int)n);
+    e = x < -86.0f ? 0.0f : e;
+    e = x > 88.72283905f ? __builtin_huge_valf() : e;
+    return x != x ? x : e;
 }
 // silu(g) = g / (1 + exp(-g))   (fused_ops.rs:34-45)
 __device__ __forceinline__ float det_silu(float g) { return g / (1.0f + det_exp(-g)); }
