@@ -267,22 +267,37 @@ template <int T, int NTN>
 __device__ __forceinline__ void pf_mma_chunk(const uint8_t* xl, const float* xd, const int* xs8,
                                              const uint8_t* wrows, int cbytes, int nb, float (&acc)[NTN][4]) {
     const int lane = threadIdx.x & 63, q = lane >> 4, c = lane & 15;
-    for (int b = 0; b < nb; b++) {
-        const uint8_t* ab = xl + (c * PF_CHUNK + b) * 36 + 4 + 8 * q;
-        const long af = (long)(((uint64_t) * (const uint32_t*)(ab + 4) << 32) | *(const uint32_t*)ab);
-        const float4 dx = *(const float4*)(xd + b * PF_TILE + 4 * q);
-        v4i c0 = {0, 0, 0, 0};
-        if constexpr (T == T_Q4_0) c0 = *(const v4i*)(xs8 + b * PF_TILE + 4 * q);
+    // two blocks in flight: block b's matrix products are issued before block
+    // b-1's results are rescaled, so the MFMA latency overlaps VALU work
+    v4i r[NTN], rp[NTN];
+    float dw[NTN], dwp[NTN];
+    float4 dxp;
+    for (int b = 0; b <= nb; b++) {
+        float4 dx;
+        if (b < nb) {
+            const uint8_t* ab = xl + (c * PF_CHUNK + b) * 36 + 4 + 8 * q;
+            const long af = (long)(((uint64_t) * (const uint32_t*)(ab + 4) << 32) | *(const uint32_t*)ab);
+            dx = *(const float4*)(xd + b * PF_TILE + 4 * q);
+            v4i c0 = {0, 0, 0, 0};
+            if constexpr (T == T_Q4_0) c0 = *(const v4i*)(xs8 + b * PF_TILE + 4 * q);
 #pragma unroll
-        for (int n = 0; n < NTN; n++) {
-            float dw;
-            const long bf = pf_b_frag<T>(wrows + (16 * n + c) * cbytes, b, q, &dw);
-            const v4i r = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bf, c0, 0, 0, 0);
-            acc[n][0] = __builtin_fmaf(dw * dx.x, (float)r[0], acc[n][0]);
-            acc[n][1] = __builtin_fmaf(dw * dx.y, (float)r[1], acc[n][1]);
-            acc[n][2] = __builtin_fmaf(dw * dx.z, (float)r[2], acc[n][2]);
-            acc[n][3] = __builtin_fmaf(dw * dx.w, (float)r[3], acc[n][3]);
+            for (int n = 0; n < NTN; n++) {
+                const long bf = pf_b_frag<T>(wrows + (16 * n + c) * cbytes, b, q, &dw[n]);
+                r[n] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bf, c0, 0, 0, 0);
+            }
         }
+        if (b > 0) {
+#pragma unroll
+            for (int n = 0; n < NTN; n++) {
+                acc[n][0] = __builtin_fmaf(dwp[n] * dxp.x, (float)rp[n][0], acc[n][0]);
+                acc[n][1] = __builtin_fmaf(dwp[n] * dxp.y, (float)rp[n][1], acc[n][1]);
+                acc[n][2] = __builtin_fmaf(dwp[n] * dxp.z, (float)rp[n][2], acc[n][2]);
+                acc[n][3] = __builtin_fmaf(dwp[n] * dxp.w, (float)rp[n][3], acc[n][3]);
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < NTN; n++) { rp[n] = r[n]; dwp[n] = dw[n]; }
+        dxp = dx;
     }
 }
 
