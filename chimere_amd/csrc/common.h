@@ -432,13 +432,15 @@ template <int T> struct RegBlk;
 template <> struct RegBlk<T_Q4_0> {
     // 18-byte block at an even address: 16-byte + 2-byte loads, ordered by the
     // block's 4-byte phase (ph = 0: [0,16) + [16,18); ph = 2: [0,2) + [2,18))
+    static constexpr int LOADS = 2;   // vector-memory instructions issued by load()
     uint4 v;
     uint32_t t;
     bool ph2;
     __device__ __forceinline__ void load(const uint8_t* blk) {
+        // no branch: the two loads of either phase are issued unconditionally
         ph2 = ((uintptr_t)blk & 3) != 0;
-        if (!ph2) { v = *(const uint4*)blk; t = *(const uint16_t*)(blk + 16); }
-        else { t = *(const uint16_t*)blk; v = *(const uint4*)(blk + 2); }
+        v = *(const uint4*)(blk + (ph2 ? 2 : 0));
+        t = *(const uint16_t*)(blk + (ph2 ? 0 : 16));
     }
     __device__ __forceinline__ void fields(uint32_t& d, uint32_t (&qs)[4]) const {
         if (!ph2) {
@@ -465,13 +467,16 @@ template <> struct RegBlk<T_Q4_0> {
 };
 template <> struct RegBlk<T_Q8_0> {
     // 34-byte block at an even address: two 16-byte loads and one 2-byte load
+    static constexpr int LOADS = 3;
     uint4 v0, v1;
     uint32_t t;
     bool ph2;
     __device__ __forceinline__ void load(const uint8_t* blk) {
         ph2 = ((uintptr_t)blk & 3) != 0;
-        if (!ph2) { v0 = *(const uint4*)blk; v1 = *(const uint4*)(blk + 16); t = *(const uint16_t*)(blk + 32); }
-        else { t = *(const uint16_t*)blk; v0 = *(const uint4*)(blk + 2); v1 = *(const uint4*)(blk + 18); }
+        const uint8_t* q = blk + (ph2 ? 2 : 0);
+        v0 = *(const uint4*)q;
+        v1 = *(const uint4*)(q + 16);
+        t = *(const uint16_t*)(blk + (ph2 ? 0 : 32));
     }
     __device__ __forceinline__ int dot(const XBlk& x, const uint32_t*, float* dw) const {
         uint32_t d, q[8];
@@ -611,8 +616,8 @@ __device__ __forceinline__ void stage_rows(uint8_t* __restrict__ lds, const uint
 __device__ __forceinline__ void lds_copy_wait() { __builtin_amdgcn_s_waitcnt(0); }
 
 // Value of lane (lane ^ M) without going through LDS: DPP quad permutes for
-// M = 1, 2, row shifts by M (direction picked per lane) for M = 4, 8, and the
-// gfx950 v_permlane16/32_swap for M = 16, 32.  The partner lane must be
+// M = 1, 2, a half-row mirror plus a quad reversal for M = 4, a row rotation
+// by 8 for M = 8, and the gfx950 v_permlane16/32_swap for M = 16, 32.  The partner lane must be
 // active (all uses keep whole 2M-lane groups converged).
 template <int M>
 __device__ __forceinline__ int xlane(int v) {
@@ -620,10 +625,13 @@ __device__ __forceinline__ int xlane(int v) {
     const int lane = __lane_id();
     if constexpr (M == 1) return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);   // quad_perm 1,0,3,2
     else if constexpr (M == 2) return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false); // quad_perm 2,3,0,1
-    else if constexpr (M == 4 || M == 8) {
-        const int up = __builtin_amdgcn_update_dpp(0, v, 0x100 | M, 0xF, 0xF, false);   // row_shl: lane i+M
-        const int dn = __builtin_amdgcn_update_dpp(0, v, 0x110 | M, 0xF, 0xF, false);   // row_shr: lane i-M
-        return (lane & M) ? dn : up;
+    else if constexpr (M == 4) {
+        // row_half_mirror (i -> 7-i in each 8-lane half) then quad_perm 3,2,1,0:
+        // lane i ends with lane (i & ~7) | (7 - ((i & 4) | (3 - (i & 3)))) = i ^ 4
+        const int hm = __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
+        return __builtin_amdgcn_update_dpp(0, hm, 0x1B, 0xF, 0xF, false);
+    } else if constexpr (M == 8) {
+        return __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false);   // row_ror:8 = xor 8 in a 16-lane row
     } else if constexpr (M == 16) {
         const auto r = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
         return (int)((lane & 16) ? r[0] : r[1]);

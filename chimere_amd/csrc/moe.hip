@@ -27,18 +27,36 @@
 
 // Phase timestamps for latency analysis (debug builds with
 // -DCHIMERE_PHASE_TIMING only): thread 0 of a work-group records the 100 MHz
-// real-time counter at numbered points into workspace.
+// real-time counter at numbered points into LDS (a global store per point
+// would add its acknowledgement to the next wait on vector memory), and
+// PHASE_END copies them to the workspace.
 #ifdef CHIMERE_PHASE_TIMING
+namespace chimere {
+__device__ __forceinline__ uint64_t* phase_lds() {
+    __shared__ uint64_t s_phase[32];
+    return s_phase;
+}
+}
 #define PHASE(kern, i)                                                                      \
     do {                                                                                     \
-        if (threadIdx.x == 0)                                                                \
-            a.phase[((kern) * 4096 + blockIdx.x + blockIdx.y * gridDim.x) * 16 + (i)] =        \
-                __builtin_amdgcn_s_memrealtime();                                           \
+        if (threadIdx.x == 0) {                                                              \
+            if ((i) == 0)                                                                    \
+                for (int q_ = 1; q_ < 32; q_++) chimere::phase_lds()[q_] = 0;               \
+            chimere::phase_lds()[i] = __builtin_amdgcn_s_memrealtime();                     \
+        }                                                                                    \
     } while (0)
-#define PHASE_PTR(kern, i) (a.phase + ((kern) * 4096 + blockIdx.x + blockIdx.y * gridDim.x) * 16 + (i))
+#define PHASE_PTR(kern, i) (chimere::phase_lds() + (i))
+#define PHASE_END(kern)                                                                     \
+    do {                                                                                     \
+        if (threadIdx.x == 0)                                                                \
+            for (int q_ = 0; q_ < 32; q_++)                                                  \
+                a.phase[((kern) * 4096 + blockIdx.x + blockIdx.y * gridDim.x) * 32 + q_] =     \
+                    chimere::phase_lds()[q_];                                                \
+    } while (0)
 #else
 #define PHASE(kern, i) do {} while (0)
 #define PHASE_PTR(kern, i) nullptr
+#define PHASE_END(kern) do {} while (0)
 #endif
 
 namespace chimere {
@@ -108,6 +126,7 @@ __global__ __launch_bounds__(256) void k_moe_route(MoeArgs a) {
                 blk[4 + i] = (uint8_t)(int8_t)q;
                 if (i == 0) *(uint32_t*)blk = f2h(d) | (f2h(sum) << 16);
             });
+        PHASE_END(0);
         return;
     }
     float v[NT];
@@ -120,6 +139,7 @@ __global__ __launch_bounds__(256) void k_moe_route(MoeArgs a) {
         }
     }
     PHASE(0, 1);
+    PHASE_END(0);
 }
 
 constexpr int EX_RG = 64;                    // K2 row groups: 1024 threads
@@ -181,14 +201,9 @@ __device__ __forceinline__ void route_plan(const MoeArgs& a, int* first, Plan& p
     const int MK = a.M * a.K;
 
     const int wave = tid >> 6;
-#ifdef CHIMERE_PHASE_TIMING
-    if (tid == 0) {   // latency of the first logits load alone
-        volatile float v = *(volatile const float*)(a.logits + 5);
-        (void)v;
-        PHASE(1, 10);
-    }
-#endif
-    if (wave < a.M) topk_wave_any(a.logits + wave * a.E, a.E, a.K, s_ids + wave * a.K, s_w + wave * a.K);
+    PHASE(1, 10);
+    if (wave < a.M)
+        topk_wave_any(a.logits + wave * a.E, a.E, a.K, s_ids + wave * a.K, s_w + wave * a.K, PHASE_PTR(1, 11));
     PHASE(1, 1);
     if (a.M == 1) {
         // one token: its K experts are distinct; unit k = the k-th selected
@@ -289,7 +304,9 @@ __device__ __forceinline__ void expert_item(const MoeArgs& a, uint8_t* tile, XLd
             }
         }
     }
+    PHASE(1, 19);
     __syncthreads();
+    PHASE(1, 14);
     // one half-wave per token: Q8_1 of the 32-row block of h (ggml
     // semantics), kept decoded in LDS for the down terms
     if ((tid >> 5) < ntok) {
@@ -365,6 +382,7 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert(MoeArgs a) {
     const int nr = pl.nu > x ? (pl.nu - 1 - x) / 8 + 1 : 0;
     const int ns = a.has_shared ? (NB > x ? (NB - 1 - x) / 8 + 1 : 0) : 0;
     const int nx = nr * NB + ns;
+    PHASE(1, 16);
     if (lb >= nx) {
         // helper: first the up rows of this XCD's items (requested by the items
         // right behind their gate rows), then the down matrices; each helper
@@ -395,14 +413,18 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert(MoeArgs a) {
             sink += *(const uint16_t*)(base + (off & ~(int64_t)1));
         }
         if (a.H < 0) a.plan[0] = (int)sink;   // never taken: keeps the loads
+        PHASE_END(1);
         return;
     }
+    PHASE(1, 17);
     for (int i = lb; i < nx; i += G8) {
         const bool shared = i >= nr * NB;
         const int u = shared ? MK : x + 8 * (i / NB);
         const int w = shared ? x + 8 * (i - nr * NB) : i % NB;
         const int ntok = shared ? a.M : pl.untok[u];
+        PHASE(1, 18);
         __syncthreads();   // the previous item's readers of toks / pairs / hx are done
+        PHASE(1, 13);
         if (tid < ntok) {
             toks[tid] = shared ? tid : pl.utok[u][tid];
             pairs[tid] = shared ? MK + tid : pl.upair[u][tid];
@@ -414,6 +436,265 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert(MoeArgs a) {
                                     a.up + pl.uexp[u] * a.su, a.down + pl.uexp[u] * a.sd);
         PHASE(1, 4);
     }
+    PHASE_END(1);
+}
+
+// ------------------------------------------ one token, common shapes: K2'
+// k_moe_expert1 does K2's work for one token when every work-group holds at
+// most one item and the weight rows are 16-byte aligned (Q4_0 / Q8_0 experts
+// and shared expert, hidden <= 2048, ffn <= 512, top_k <= 8): the same items,
+// fp32 order and outputs, laid out for latency.
+//  * The shared expert's items do not wait for routing; the routed items'
+//    Q8_1(x) blocks are decoded by waves 1.. while wave 0 runs softmax/top-k.
+//  * Gate/up rows arrive in K chunks alternating between two LDS buffers, so
+//    the dots of one chunk overlap the copy of the next.  Wave w copies rows
+//    w, w+16, w+32, w+48 of a chunk (one asynchronous copy instruction per
+//    row), so every thread issues E1_ROWS copies per chunk and "chunk c has
+//    landed" is vmcnt <= E1_ROWS (copies of chunk c+1 outstanding).
+//  * The down column slice is requested behind the first two chunks, so its
+//    latency overlaps the gate/up dots.
+constexpr int E1_ROWS = 2 * QK / (EX_THREADS / 64);   // rows copied per wave and chunk: 4
+template <int T>
+constexpr int e1_cblk() { return T == T_Q8_0 ? 16 : 32; }   // blocks per chunk
+template <int T>
+constexpr int e1_cbytes() { return e1_cblk<T>() * QTraits<T>::BYTES; }
+constexpr int E1_MAX_H = 2048;
+
+// s_waitcnt with only the vector-memory count: at most n outstanding
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+
+// Work-group barrier that waits only for this wave's LDS accesses: the
+// release fence of __syncthreads() would also wait for every outstanding
+// asynchronous copy (they write LDS), including the next chunk's.  The empty
+// asm statements keep memory accesses on their side of the barrier.
+__device__ __forceinline__ void lds_barrier() {
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+}
+
+// Copies chunk c (blocks [c*CBLK, c*CBLK + cb)) of the 2*QK gate/up rows into
+// buf (row stride cbytes).  One copy instruction per (wave, row).
+template <int T>
+__device__ __forceinline__ void e1_issue(uint8_t* buf, const uint8_t* gate, const uint8_t* up, int64_t rb, int c,
+                                         int nbH) {
+    constexpr int CBLK = e1_cblk<T>();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int cb = min(CBLK, nbH - c * CBLK);
+    const int seg = cb * QTraits<T>::BYTES;   // a multiple of 16 (cb is a multiple of 8)
+    const int64_t goff = (int64_t)c * CBLK * QTraits<T>::BYTES;
+#pragma unroll
+    for (int k = 0; k < E1_ROWS; k++) {
+        const int r = wave + (EX_THREADS / 64) * k;
+        const uint8_t* src = (r < QK ? gate + (int64_t)r * rb : up + (int64_t)(r - QK) * rb) + goff;
+        if (lane * 16 < seg)
+            __builtin_amdgcn_global_load_lds((const glb_void_t*)(src + lane * 16),
+                                             (lds_void_t*)(buf + r * e1_cbytes<T>()), 16, 0, CPOL_STREAM);
+    }
+}
+
+// Dots of chunk c for this thread's row (row group g) and lane j: blocks
+// j, j+16, ... of the chunk, in ascending order (the L=16 order).
+template <int T>
+__device__ __forceinline__ float e1_dots(const uint8_t* buf, const XLds* xs, int c, int nbH, float acc) {
+    constexpr int CBLK = e1_cblk<T>();
+    const int g = threadIdx.x >> 4, j = threadIdx.x & 15;
+    const int cb = min(CBLK, nbH - c * CBLK);
+    const uint8_t* row = buf + g * e1_cbytes<T>();
+#pragma unroll
+    for (int b = j; b < CBLK; b += SLOTS) {
+        if (b < cb) {
+            WBlk wb;
+            block_decode<T>(row, b, nullptr, wb);
+            XBlk xb;
+            xlds_to_blk(xs[c * CBLK + b], xb);
+            acc = wacc<T>(wb, xb, acc);
+        }
+    }
+    return acc;
+}
+
+// The item: gate/up rows [32w, 32w+32) of one expert, h block w, and its down
+// terms (lane_acc[pair][w][r], F <= 512).
+template <int T>
+__device__ __forceinline__ void e1_item(const MoeArgs& a, uint8_t* bufA, uint8_t* bufB, const XLds* xs,
+                                        float (*hg)[QK], float (*hu)[QK], int pair, int w, const uint8_t* gate,
+                                        const uint8_t* up) {
+    constexpr int CBLK = e1_cblk<T>();
+    const int tid = threadIdx.x;
+    const int nbH = a.H / QK;
+    const int nc = (nbH + CBLK - 1) / CBLK;
+    const int64_t rb = row_bytes(T, a.H);
+    gate += (int64_t)w * QK * rb;
+    up += (int64_t)w * QK * rb;
+    e1_issue<T>(bufA, gate, up, rb, 0, nbH);
+    if (nc > 1) e1_issue<T>(bufB, gate, up, rb, 1, nbH);
+    // in issue order: chunk 0, chunk 1, then chunk c+2 while chunk c+1 is
+    // computed; chunk c has landed when at most the copies of the chunk after
+    // it are outstanding
+    float acc = 0.0f;
+    for (int c = 0; c < nc; c += 2) {
+        if (c + 1 < nc) wait_vm<E1_ROWS>();
+        else wait_vm<0>();
+        lds_barrier();
+        if (c == 0) PHASE(1, 10);
+        acc = e1_dots<T>(bufA, xs, c, nbH, acc);
+        if (c == 0) PHASE(1, 11);
+        if (c + 1 >= nc) break;
+        lds_barrier();   // every wave is done with buffer A
+        if (c + 2 < nc) {
+            e1_issue<T>(bufA, gate, up, rb, c + 2, nbH);
+            wait_vm<E1_ROWS>();
+        } else {
+            wait_vm<0>();
+        }
+        lds_barrier();
+        if (c == 0) PHASE(1, 12);
+        acc = e1_dots<T>(bufB, xs, c + 1, nbH, acc);
+        if (c == 0) PHASE(1, 13);
+        if (c + 2 >= nc) break;
+        lds_barrier();   // every wave is done with buffer B
+        if (c + 3 < nc) e1_issue<T>(bufB, gate, up, rb, c + 3, nbH);
+    }
+    PHASE(1, 4);
+    const int g = tid >> 4, j = tid & 15;
+    const float v = slot_reduce16(acc);
+    if (j == 0) {
+        if (g < QK) hg[0][g] = v;
+        else hu[0][g - QK] = v;
+    }
+    __syncthreads();
+    PHASE(1, 5);
+    // one half-wave: Q8_1 of the 32-row block w of h (ggml semantics), to
+    // the pair's row of hq for the down projection
+    if (tid < 32) {
+        const int i = tid;
+        const float xi = det_silu(hg[0][i]) * hu[0][i];
+        const float amax = bfly32_max(__builtin_fabsf(xi)), sum = bfly32_sum(xi);
+        const float d = amax / 127.0f;
+        const int q = amax == 0.0f ? 0 : (int)__builtin_roundf(xi / d);
+        uint8_t* o = a.hq + (int64_t)pair * a.hq_stride + w * Q8_1_BYTES;
+        o[4 + i] = (uint8_t)(int8_t)q;
+        if (i == 0) *(uint32_t*)o = f2h(d) | (f2h(sum) << 16);
+    }
+    PHASE(1, 6);
+}
+
+// helper work-groups of k_moe_expert1: L2 prefetch of the up rows of this
+// XCD's items, then of the down rows the down/combine launch reads here; LE / LS:
+// bytes of a 32-row block of an expert's / the shared up matrix, mb / sb:
+// bytes of an expert's / the shared down matrix
+struct E1Prefetch {
+    const uint8_t *up, *down, *sh_up, *sh_down;
+    int64_t su, sd, LE, LS, mb, sb;
+    int NB, K, has_shared;
+    int* sink_dst;
+};
+
+__device__ __forceinline__ void e1_prefetch(const E1Prefetch& p, const int* uexp, int x, int hb, int nh, int nr, int ns) {
+    uint32_t sink = 0;
+    const int NB = p.NB;
+    const int64_t ua = (int64_t)nr * NB * p.LE + ns * p.LS;
+    for (int64_t o = ua * hb / nh + 64 * (int64_t)threadIdx.x, e1 = ua * (hb + 1) / nh; o < e1;
+         o += 64 * EX_THREADS) {
+        const int64_t rl = (int64_t)nr * NB * p.LE;
+        const uint8_t* q;
+        if (o < rl) {
+            const int i = (int)(o / p.LE);
+            q = p.up + (int64_t)uexp[x + 8 * (i / NB)] * p.su + (int64_t)(i % NB) * p.LE + (o - (int64_t)i * p.LE);
+        } else {
+            const int j = (int)((o - rl) / p.LS);
+            q = p.sh_up + (int64_t)(x + 8 * j) * p.LS + (o - rl - (int64_t)j * p.LS);
+        }
+        sink += *(const uint16_t*)((uintptr_t)q & ~(uintptr_t)1);
+    }
+    // then the rows [x H/8, (x+1) H/8) of every pair's down matrix: the rows
+    // the down/combine launch reads on this XCD
+    const int64_t sE = p.mb / 8, sS = p.sb / 8;
+    const int64_t total = (int64_t)p.K * sE + (p.has_shared ? sS : 0);
+    for (int64_t o = total * hb / nh + 64 * (int64_t)threadIdx.x, e1 = total * (hb + 1) / nh; o < e1;
+         o += 64 * EX_THREADS) {
+        const int m = (int)(o / sE);
+        const uint8_t* base = m < p.K ? p.down + (int64_t)uexp[m] * p.sd + x * sE : p.sh_down + x * sS;
+        const int64_t off = m < p.K ? o - (int64_t)m * sE : o - (int64_t)p.K * sE;
+        sink += *(const uint16_t*)(base + (off & ~(int64_t)1));
+    }
+    if (p.NB < 0) *p.sink_dst = (int)sink;   // never taken: keeps the loads
+}
+
+template <int TE, int TS>
+__global__ __launch_bounds__(EX_THREADS) void k_moe_expert1(MoeArgs a) {
+    constexpr int CB = e1_cbytes<TE>() > e1_cbytes<TS>() ? e1_cbytes<TE>() : e1_cbytes<TS>();
+    __shared__ __attribute__((aligned(16))) uint8_t bufA[2 * QK * CB];
+    __shared__ __attribute__((aligned(16))) uint8_t bufB[2 * QK * CB];
+    __shared__ XLds xs[E1_MAX_H / QK];
+    __shared__ float hg[1][QK], hu[1][QK];
+    __shared__ int s_ids[MAX_K];
+    __shared__ float s_w[MAX_K];
+    PHASE(1, 0);
+    const int tid = threadIdx.x, wave = tid >> 6;
+    const int NB = a.F / QK, nbH = a.H / QK;
+    const int x = blockIdx.x & 7, lb = blockIdx.x >> 3, G8 = gridDim.x >> 3;
+    // items of XCD x (work-group ids are dealt round-robin to the 8 XCDs): the
+    // row blocks of the routed unit x (the x-th selected expert), then the
+    // shared expert's blocks x, x+8, ...; the rest are helpers
+    const int nr = a.K > x ? 1 : 0;
+    const int ns = a.has_shared ? (NB > x ? (NB - 1 - x) / 8 + 1 : 0) : 0;
+    const int nx = nr * NB + ns;
+    const bool routed = lb < nr * NB, shared = !routed && lb < nx;
+    if (!shared) {
+        // wave 0: softmax / top-k; the other waves decode Q8_1(x) meanwhile
+        if (wave == 0) {
+            topk_wave_any(a.logits, a.E, a.K, s_ids, s_w, PHASE_PTR(1, 8));
+            if (blockIdx.x == 0 && tid < a.K) {
+                a.wts[tid] = s_w[tid];
+                a.plan[PLAN_UEXP + tid] = s_ids[tid];
+                if (a.ids_out) { a.ids_out[tid] = s_ids[tid]; a.w_out[tid] = s_w[tid]; }
+            }
+        } else if (routed) {
+            for (int i = tid - 64; i < nbH; i += EX_THREADS - 64) {
+                XBlk xb;
+                load_xblk(a.xq + (int64_t)i * Q8_1_BYTES, xb);
+                xs[i].d = xb.d; xs[i].sumq = xb.sumq;
+#pragma unroll
+                for (int k = 0; k < 8; k++) xs[i].q[k] = xb.q[k];
+            }
+        }
+        __syncthreads();
+        PHASE(1, 1);
+        if (!routed) {
+            const int nh = G8 - nx, hb = lb - nx;
+            E1Prefetch p;
+            p.up = a.up; p.down = a.down; p.sh_up = a.sh_up; p.sh_down = a.sh_down;
+            p.su = a.su; p.sd = a.sd;
+            p.LE = QK * row_bytes(TE, a.H); p.LS = QK * row_bytes(TS, a.H);
+            p.mb = (int64_t)a.H * row_bytes(TE, a.F); p.sb = (int64_t)a.H * row_bytes(TS, a.F);
+            p.NB = NB; p.K = a.K; p.has_shared = a.has_shared;
+            p.sink_dst = a.plan;
+            e1_prefetch(p, s_ids, x, hb, nh, nr, ns);
+            PHASE_END(1);
+            return;
+        }
+        const int e = s_ids[x];
+        PHASE(1, 2);
+        e1_item<TE>(a, bufA, bufB, xs, hg, hu, x, lb, a.gate + e * a.sg, a.up + e * a.su);
+    } else {
+        for (int i = tid; i < nbH; i += EX_THREADS) {
+            XBlk xb;
+            load_xblk(a.xq + (int64_t)i * Q8_1_BYTES, xb);
+            xs[i].d = xb.d; xs[i].sumq = xb.sumq;
+#pragma unroll
+            for (int k = 0; k < 8; k++) xs[i].q[k] = xb.q[k];
+        }
+        PHASE(1, 2);
+        e1_item<TS>(a, bufA, bufB, xs, hg, hu, a.K, x + 8 * (lb - nr * NB), a.sh_gate, a.sh_up);
+    }
+    PHASE_END(1);
 }
 
 // K3: grid (ceil(H/16)), 256 threads: 16 down rows per work-group, 16 lanes
@@ -496,6 +777,82 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_combine(MoeArgs a) {
         }
     }
     PHASE(2, 2);
+    PHASE_END(2);
+}
+
+// K3' (with k_moe_expert1): down projection and combine for one token.
+// Grid H/4 work-groups of np*64 threads (np = K routed pairs in rank order,
+// then the shared expert): wave p takes pair p for the work-group's 4 down
+// rows, 16 lanes per row; lane j takes block j of the row (F <= 512: one
+// block per lane) against the pair's Q8_1(h) block j, so the row's value is
+// the L=16 halving tree of fmaf(f32(d_w) * f32(d_h), sumi, 0) -- the value K3
+// rebuilds from K2's lane terms.  Then the router-weighted sum in k order plus
+// the shared expert.  Work-group b runs on XCD b % 8 and takes the b/8-th
+// tile of XCD b % 8's contiguous row range.
+constexpr int DC1_ROWS = 4;
+
+template <int T>
+__device__ __forceinline__ float dc1_row(const uint8_t* drow, const uint8_t* hblk, bool act) {
+    RegBlk<T> rbk;
+    uint32_t hw[9];
+    if (act) {
+        rbk.load(drow);
+        const uint32_t* h = (const uint32_t*)hblk;
+#pragma unroll
+        for (int k = 0; k < 9; k++) hw[k] = h[k];
+    }
+    float v = 0.0f;
+    if (act) {
+        WBlk w;
+        rbk.decode(nullptr, w);
+        XBlk xb;
+        xb.d = h2f(hw[0] & 0xFFFFu);
+        int sq = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) { xb.q[k] = (int)hw[1 + k]; sq = dot4(xb.q[k], 0x01010101, sq); }
+        xb.sumq = sq;
+        v = __builtin_fmaf(w.dw * xb.d, (float)wdot<T>(w, xb), 0.0f);
+    }
+    return slot_reduce16(v);
+}
+
+template <int TE, int TS>
+__global__ __launch_bounds__((MAX_K + 1) * 64) void k_moe_dc1(MoeArgs a) {
+    __shared__ float dn[DC1_ROWS][MAX_K + 1];
+    PHASE(2, 0);
+    const int tid = threadIdx.x, j = tid & 15, rr = (tid >> 4) & (DC1_ROWS - 1), p = tid >> 6;
+    const int tile_i = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
+    const int r = tile_i * DC1_ROWS + rr;
+    const int NB = a.F / QK, K = a.K;
+    const bool act = j < NB && r < a.H;
+    const uint8_t* hb = a.hq + (int64_t)p * a.hq_stride + j * Q8_1_BYTES;
+    float v;
+    if (p < K) {
+        const int e = a.plan[PLAN_UEXP + p];
+        v = dc1_row<TE>(a.down + (int64_t)e * a.sd + (int64_t)r * row_bytes(TE, a.F) + j * QTraits<TE>::BYTES, hb,
+                        act);
+    } else {
+        v = dc1_row<TS>(a.sh_down + (int64_t)r * row_bytes(TS, a.F) + j * QTraits<TS>::BYTES, hb, act);
+    }
+    if (j == 0) dn[rr][p] = v;
+    __syncthreads();
+    PHASE(2, 1);
+    if (tid < DC1_ROWS) {
+        const int rg = tile_i * DC1_ROWS + tid;
+        if (rg < a.H) {
+            float acc = 0.0f;
+            for (int k = 0; k < K; k++) acc = __builtin_fmaf(a.wts[k], dn[tid][k], acc);
+            float o = acc;
+            if (a.has_shared) {
+                const float sh = dn[tid][K];
+                if (a.sh_gate_w) o = __builtin_fmaf(sh, 1.0f / (1.0f + det_exp(-a.glogit[0])), acc);
+                else o = sh + acc;
+            }
+            a.out[rg] = o;
+        }
+    }
+    PHASE(2, 2);
+    PHASE_END(2);
 }
 
 // ------------------------------------------------ several tokens (M > 1)
@@ -644,6 +1001,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_gateup(MoeArgs a) {
         if (i == 0) *(uint32_t*)o = f2h(d) | (f2h(sum) << 16);
     }
     PHASE(1, 3);
+    PHASE_END(1);
 }
 
 template <int T>
@@ -703,6 +1061,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_down(MoeArgs a) {
             }
         }
     PHASE(2, 3);
+    PHASE_END(2);
 }
 
 // KC: grid (ceil(H/256), M): out = sum_k fmaf(w_k, dn_k, acc) in k order (+ shared expert)
@@ -743,9 +1102,9 @@ static WsPlan plan_ws(int H, int F, int E, int K, int M) {
     p.xq = o; o += al256((size_t)M * p.xq_stride);
     p.terms = o; o += al256((size_t)P * H * (F / QK) * (F / QK <= SLOTS ? 4 : 8));
     p.hq_stride = pad_to(F, ROW_PAD) / QK * Q8_1_BYTES;
-    if (M > 1) { p.hq = o; o += al256((size_t)P * p.hq_stride); }
+    p.hq = o; o += al256((size_t)P * p.hq_stride);
 #ifdef CHIMERE_PHASE_TIMING
-    p.phase = o; o += al256((size_t)3 * 4096 * 16 * 8);
+    p.phase = o; o += al256((size_t)3 * 4096 * 32 * 8);
 #endif
     p.total = o;
     return p;
@@ -770,11 +1129,33 @@ static int expert_grid(int items) {
     return items < cus[dev] ? items : cus[dev];
 }
 
+// k_moe_expert1's conditions: one item per work-group, 16-byte aligned rows
+static bool expert1_fits(const MoeArgs& a, int te, int ts) {
+    const int NB = a.F / QK;
+    const int ns = a.has_shared ? (NB + 7) / 8 : 0;
+    const uintptr_t al = (uintptr_t)a.gate | (uintptr_t)a.up | (uintptr_t)a.down | (uintptr_t)a.sg |
+                         (uintptr_t)a.su | (uintptr_t)a.sd | (uintptr_t)a.sh_gate | (uintptr_t)a.sh_up |
+                         (uintptr_t)a.sh_down | (uintptr_t)a.xq;
+    (void)te; (void)ts;
+    return a.M == 1 && a.K <= 8 && a.H <= E1_MAX_H && NB <= SLOTS && (al & 15) == 0 &&
+           NB + ns <= expert_grid(256) / 8;
+}
+
 // stage < 0: all three kernels; 0, 1, 2: only K1, K2 or K3
 template <int TE, int TS, int NT>
 static void launch_layer_nt(const MoeArgs& a, int stage, hipStream_t s) {
     if (stage < 0 || stage == 0)
         hipLaunchKernelGGL((k_moe_route<NT>), dim3(route_grid(a)), dim3(256), 0, s, a);
+    if constexpr (NT == 1 && (TE == T_Q4_0 || TE == T_Q8_0) && (TS == T_Q4_0 || TS == T_Q8_0)) {
+        if (expert1_fits(a, TE, TS)) {
+            if (stage < 0 || stage == 1)
+                hipLaunchKernelGGL((k_moe_expert1<TE, TS>), dim3(expert_grid(256)), dim3(EX_THREADS), 0, s, a);
+            if (stage < 0 || stage == 2)
+                hipLaunchKernelGGL((k_moe_dc1<TE, TS>), dim3(a.H / DC1_ROWS), dim3((a.K + a.has_shared) * 64), 0, s,
+                                   a);
+            return;
+        }
+    }
     if (stage < 0 || stage == 1)
         hipLaunchKernelGGL((k_moe_expert<TE, TS, NT>), dim3(expert_grid(256)), dim3(EX_THREADS), 0, s, a);
     if (stage < 0 || stage == 2)

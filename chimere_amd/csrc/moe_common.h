@@ -95,12 +95,13 @@ __device__ __forceinline__ void f32_row_dot(const float* __restrict__ a, const f
 // to the lowest index; so does this, in registers: a round takes the wave
 // maximum of the keys f32bits(p) + 1 (0 marks a taken or padding entry; p >= 0
 // so the key order is the order of p; keys < 2^31) by a DPP scan, the lowest index
-// holding it (a second DPP scan), and clears that entry.  Weights are
+// holding it (ballots of key == max, slot by slot), and clears that entry.  Weights are
 // renormalised by the sequential sum of the selected probabilities (round
 // order).  Lane k < K writes entry k.  Requires E <= 1024, K <= min(E, 64).
 template <int NV>
 __device__ __forceinline__ void topk_wave(const float* __restrict__ logits, int E, int K,
-                                          int* __restrict__ idx_out, float* __restrict__ w_out) {
+                                          int* __restrict__ idx_out, float* __restrict__ w_out,
+                                          uint64_t* ph = nullptr) {
     const int lane = threadIdx.x & 63;
     float p[NV], ev[NV];
     float mx = -__builtin_huge_valf();
@@ -111,6 +112,9 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ logits, int 
         mx = __builtin_fmaxf(mx, p[i]);
     }
     mx = bfly32_max(__builtin_fmaxf(mx, xlane<32>(mx)));
+#ifdef CHIMERE_PHASE_TIMING
+    if (ph && lane == 0) ph[0] = __builtin_amdgcn_s_memrealtime();
+#endif
 #pragma unroll
     for (int i = 0; i < NV; i++) {
         ev[i] = (lane + 64 * i) < E ? det_exp(p[i] - mx) : 0.0f;
@@ -130,6 +134,9 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ logits, int 
         p[i] = s > 0.0f ? ev[i] / s : 1.0f / (float)E;
         key[i] = j < E ? __builtin_bit_cast(uint32_t, p[i]) + 1u : 0u;
     }
+#ifdef CHIMERE_PHASE_TIMING
+    if (ph && lane == 0) ph[1] = __builtin_amdgcn_s_memrealtime();
+#endif
     int my_idx = 0;
     float my_w = 0.0f;
     for (int k = 0; k < K; k++) {
@@ -137,12 +144,20 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ logits, int 
 #pragma unroll
         for (int i = 1; i < NV; i++) m = max(m, (int)key[i]);
         m = wave_max_nonneg(m);
-        // the lowest index holding m: a second DPP maximum, of (2^31-1 - index)
-        int c = 0;
+        // the lowest index holding m: indices of slot i (lane + 64 i) all
+        // precede those of slot i + 1, so it is the lowest lane of the first
+        // slot whose ballot of key == m is not empty
+        int win = 0;
+        bool found = false;
 #pragma unroll
-        for (int i = NV - 1; i >= 0; i--)
-            if (key[i] == (uint32_t)m) c = 0x7fffffff - (lane + 64 * i);
-        const int win = 0x7fffffff - wave_max_nonneg(c);
+        for (int i = 0; i < NV; i++) {
+            const uint64_t bm = __ballot(key[i] == (uint32_t)m);
+            if (!found && bm != 0) {
+                win = 64 * i + __builtin_ctzll(bm);
+                found = true;
+            }
+        }
+        win = __builtin_amdgcn_readfirstlane(win);
 #pragma unroll
         for (int i = 0; i < NV; i++)
             if (lane + 64 * i == win) key[i] = 0u;
@@ -157,12 +172,19 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ logits, int 
     }
 }
 
-__device__ __forceinline__ void topk_wave_any(const float* logits, int E, int K, int* idx, float* w) {
+// E outside (128, 256]: out of line, so that the common case's code stays
+// compact in the instruction cache
+static __device__ __noinline__ void topk_wave_other(const float* logits, int E, int K, int* idx, float* w) {
     if (E <= 64) topk_wave<1>(logits, E, K, idx, w);
     else if (E <= 128) topk_wave<2>(logits, E, K, idx, w);
-    else if (E <= 256) topk_wave<4>(logits, E, K, idx, w);
     else if (E <= 512) topk_wave<8>(logits, E, K, idx, w);
     else topk_wave<16>(logits, E, K, idx, w);
+}
+
+__device__ __forceinline__ void topk_wave_any(const float* logits, int E, int K, int* idx, float* w,
+                                              uint64_t* ph = nullptr) {
+    if (E > 128 && E <= 256) topk_wave<4>(logits, E, K, idx, w, ph);
+    else topk_wave_other(logits, E, K, idx, w);
 }
 
 // Q8_1 quantization of `nblk` 32-blocks (ggml semantics, see quant.hip) by a

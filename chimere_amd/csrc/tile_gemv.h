@@ -81,6 +81,9 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds* __re
         const int seg = chunk_bytes<T>(cb);
         const int64_t goff = (int64_t)b0 / (QTraits<T>::ELEMS / QK) * QTraits<T>::BYTES;
         __syncthreads();   // previous users of tile / xs are done
+#ifdef CHIMERE_PHASE_TIMING
+        if (ph && tid == 0) ph[10] = __builtin_amdgcn_s_memrealtime();
+#endif
         // rows are packed with stride seg (== CB except in a ragged last chunk)
         if (n1) stage_rows<stage_dw<T>(), CPOL>(tile, base1 + goff, rb, n1, seg, tid, NTH);
         if (n2) stage_rows<stage_dw<T>(), CPOL>(tile + n1 * seg, base2 + goff, rb, n2, seg, tid, NTH);

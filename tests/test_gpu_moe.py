@@ -168,3 +168,32 @@ def test_moe_wide_ffn(dev, et, M):
     layer = build(dev, 300 + et + M, H=1024, F=1024, E=32, K=4, et=et, st=O.Q8_0, gate_vec=True)
     g = torch.Generator(device=dev).manual_seed(9)
     run_and_check(layer, torch.randn(M, 1024, generator=g, device=dev))
+
+
+def misalign(t, off=2):
+    """Same bytes as t at an address 2 bytes past a 16-byte boundary."""
+    flat = torch.empty(t.numel() + 16, dtype=torch.uint8, device=t.device)
+    v = flat[off:off + t.numel()].view(t.shape)
+    v.copy_(t)
+    return v
+
+
+@pytest.mark.parametrize("et,st,gate_vec,K,E,H,F,mis", [
+    (O.Q8_0, O.Q8_0, True, 8, 64, 2048, 512, False),    # one-token kernel, 4 K chunks
+    (O.Q4_0, O.Q8_0, True, 6, 32, 1024, 256, False),    # mixed types, XCDs without a routed expert
+    (O.Q8_0, O.Q4_0, False, 3, 16, 256, 256, False),    # one K chunk shorter than a chunk
+    (O.Q4_0, None, False, 8, 64, 2048, 512, False),     # no shared expert
+    (O.IQ3_S, O.Q8_0, True, 8, 64, 2048, 512, False),   # IQ3_S: general one-token kernel
+    (O.Q4_0, O.Q4_0, False, 8, 64, 2048, 512, True),    # rows not 16-byte aligned: general kernel
+])
+def test_moe_m1_paths(dev, et, st, gate_vec, K, E, H, F, mis):
+    """One token through each one-token code path, bit-exact against the oracle."""
+    print(f"moe m1 et={et} st={st} gate={gate_vec} K={K} E={E} H={H} F={F} misaligned={mis}", flush=True)
+    layer = build(dev, 500 + K + E + H // 256, H=H, F=F, E=E, K=K, et=et, st=st, gate_vec=gate_vec)
+    if mis:
+        t = layer.tensors
+        sh = tuple(misalign(m) for m in t[6:9])
+        layer = MoeLayer(t[0], misalign(t[1]), misalign(t[2]), misalign(t[3]), et, K, shared=sh, shared_type=st)
+    g = torch.Generator(device=dev).manual_seed(12)
+    for _ in range(2):
+        run_and_check(layer, torch.randn(1, H, generator=g, device=dev))
