@@ -196,13 +196,12 @@ def main():
     kbytes = {
         # router weights + x + logits + Q8_1(x)
         "k_moe_route": E * H * 4 + H * 4 + E * 4 + (H // 32) * 36,
-        # 9 experts' gate/up/down weights + logits + Q8_1(x) + down terms written
-        "k_moe_expert": 9 * (2 * F * row_bytes(Q4_0, H) + H * row_bytes(Q4_0, F)) + E * 4 + (H // 32) * 36
-                        + 9 * H * NBF * 4,
-        # down terms read + routing weights + output
-        "k_moe_combine": 9 * H * NBF * 4 + K * 4 + H * 4,
+        # 9 experts' (8 routed + shared) gate/up rows + logits + Q8_1(x) + Q8_1(h) written
+        "k_moe_expert1": 9 * 2 * F * row_bytes(Q4_0, H) + E * 4 + (H // 32) * 36 + 9 * NBF * 36,
+        # 9 experts' down matrices + Q8_1(h) + routing weights + output
+        "k_moe_dc1": 9 * H * row_bytes(Q4_0, F) + 9 * NBF * 36 + K * 4 + H * 4,
     }
-    for stage, name in enumerate(["k_moe_route", "k_moe_expert", "k_moe_combine"]):
+    for stage, name in enumerate(["k_moe_route", "k_moe_expert1", "k_moe_dc1"]):
         n = 4 * NSLOT
         t, _ = graph_time([step_fn(i, stage) for i in range(n)])
         avg = t / n
@@ -214,7 +213,7 @@ def main():
     # FETCH_SIZE / WRITE_SIZE passes summarised in profiles/ (bench.py cannot
     # read hardware counters itself); null when no summary covers the kernel
     traffic, traffic_src = None, None
-    tpath = os.path.join(ROOT, "profiles", "k_moe_expert_m1_q4_0_traffic.json")
+    tpath = os.path.join(ROOT, "profiles", "k_moe_expert1_m1_q4_0_traffic.json")
     if os.path.exists(tpath):
         tj = json.load(open(tpath))
         for kname, kv in tj["kernels"].items():

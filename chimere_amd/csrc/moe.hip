@@ -585,36 +585,21 @@ __device__ __forceinline__ void e1_item(const MoeArgs& a, uint8_t* bufA, uint8_t
     PHASE(1, 6);
 }
 
-// helper work-groups of k_moe_expert1: L2 prefetch of the up rows of this
-// XCD's items, then of the down rows the down/combine launch reads here; LE / LS:
-// bytes of a 32-row block of an expert's / the shared up matrix, mb / sb:
-// bytes of an expert's / the shared down matrix
+// Helper work-groups of k_moe_expert1 (those without an item) prefetch the
+// down rows that the down/combine launch reads on their XCD: rows
+// [x H/8, (x+1) H/8) of every pair's down matrix (mb / sb: bytes of an
+// expert's / the shared down matrix), one 2-byte load per 64 bytes, each
+// helper an equal contiguous share.  (Prefetching the items' own up rows as
+// well was measured slower: it only adds traffic next to the items' requests.)
 struct E1Prefetch {
-    const uint8_t *up, *down, *sh_up, *sh_down;
-    int64_t su, sd, LE, LS, mb, sb;
-    int NB, K, has_shared;
+    const uint8_t *down, *sh_down;
+    int64_t sd, mb, sb;
+    int K, has_shared;
     int* sink_dst;
 };
 
-__device__ __forceinline__ void e1_prefetch(const E1Prefetch& p, const int* uexp, int x, int hb, int nh, int nr, int ns) {
+__device__ __forceinline__ void e1_prefetch(const E1Prefetch& p, const int* uexp, int x, int hb, int nh) {
     uint32_t sink = 0;
-    const int NB = p.NB;
-    const int64_t ua = (int64_t)nr * NB * p.LE + ns * p.LS;
-    for (int64_t o = ua * hb / nh + 64 * (int64_t)threadIdx.x, e1 = ua * (hb + 1) / nh; o < e1;
-         o += 64 * EX_THREADS) {
-        const int64_t rl = (int64_t)nr * NB * p.LE;
-        const uint8_t* q;
-        if (o < rl) {
-            const int i = (int)(o / p.LE);
-            q = p.up + (int64_t)uexp[x + 8 * (i / NB)] * p.su + (int64_t)(i % NB) * p.LE + (o - (int64_t)i * p.LE);
-        } else {
-            const int j = (int)((o - rl) / p.LS);
-            q = p.sh_up + (int64_t)(x + 8 * j) * p.LS + (o - rl - (int64_t)j * p.LS);
-        }
-        sink += *(const uint16_t*)((uintptr_t)q & ~(uintptr_t)1);
-    }
-    // then the rows [x H/8, (x+1) H/8) of every pair's down matrix: the rows
-    // the down/combine launch reads on this XCD
     const int64_t sE = p.mb / 8, sS = p.sb / 8;
     const int64_t total = (int64_t)p.K * sE + (p.has_shared ? sS : 0);
     for (int64_t o = total * hb / nh + 64 * (int64_t)threadIdx.x, e1 = total * (hb + 1) / nh; o < e1;
@@ -624,7 +609,7 @@ __device__ __forceinline__ void e1_prefetch(const E1Prefetch& p, const int* uexp
         const int64_t off = m < p.K ? o - (int64_t)m * sE : o - (int64_t)p.K * sE;
         sink += *(const uint16_t*)(base + (off & ~(int64_t)1));
     }
-    if (p.NB < 0) *p.sink_dst = (int)sink;   // never taken: keeps the loads
+    if (p.K < 0) *p.sink_dst = (int)sink;   // never taken: keeps the loads
 }
 
 template <int TE, int TS>
@@ -670,13 +655,11 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert1(MoeArgs a) {
         if (!routed) {
             const int nh = G8 - nx, hb = lb - nx;
             E1Prefetch p;
-            p.up = a.up; p.down = a.down; p.sh_up = a.sh_up; p.sh_down = a.sh_down;
-            p.su = a.su; p.sd = a.sd;
-            p.LE = QK * row_bytes(TE, a.H); p.LS = QK * row_bytes(TS, a.H);
+            p.down = a.down; p.sh_down = a.sh_down; p.sd = a.sd;
             p.mb = (int64_t)a.H * row_bytes(TE, a.F); p.sb = (int64_t)a.H * row_bytes(TS, a.F);
-            p.NB = NB; p.K = a.K; p.has_shared = a.has_shared;
+            p.K = a.K; p.has_shared = a.has_shared;
             p.sink_dst = a.plan;
-            e1_prefetch(p, s_ids, x, hb, nh, nr, ns);
+            e1_prefetch(p, s_ids, x, hb, nh);
             PHASE_END(1);
             return;
         }
