@@ -158,27 +158,44 @@ __device__ __forceinline__ int dot_q4_0_core(uint32_t dbits, const uint32_t (&qs
 
 // IQ3_S sub-block: qs0/qs1 its 8 index bytes, qh its high-bit byte, sg its 4
 // sign bytes, nib its 4-bit scale; grid = codebook (LDS)
+// Signed grid levels of an IQ3_S sub-block: word k (elements 4k..4k+3) is
+// grid[qs[k] | (bit k of qh) << 8] with the bytes whose sign bit (bit 4k+i of
+// sg) is set negated.  Indices are formed two at a time: v_perm interleaves
+// two qs bytes with their high bits (bit k of qh spread to byte k) into two
+// 16-bit indices, and one shift turns both into byte offsets of the table.
+// Negation per byte: (g ^ m) + (m & 1) with m = 0xFF bytes, no carry across
+// bytes since every level is >= 1.
+__device__ __forceinline__ void iq3s_levels(uint32_t qs0, uint32_t qs1, uint32_t qh, uint32_t sg,
+                                            const uint32_t* grid, uint32_t (&v)[8]) {
+    const uint32_t h0 = nib_bits(qh & 0xFu), h1 = nib_bits((qh >> 4) & 0xFu);
+    uint32_t g[8];
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        // bytes: qs[2p], hi bit 2p, qs[2p+1], hi bit 2p+1 (selector 0..3: src1 bytes, 4..7: src0 bytes)
+        const uint32_t pr = __builtin_amdgcn_perm(p < 2 ? h0 : h1, p < 2 ? qs0 : qs1,
+                                                  (p & 1) ? 0x07030602u : 0x05010400u);
+        const uint32_t ab = pr << 2;                      // both indices times 4
+        g[2 * p] = *(const uint32_t*)((const uint8_t*)grid + (ab & 0x7FCu));
+        g[2 * p + 1] = *(const uint32_t*)((const uint8_t*)grid + (ab >> 16));
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const uint32_t b = nib_bits((sg >> (4 * k)) & 0xFu);
+        const uint32_t m = __builtin_amdgcn_perm(0u, 0u, b | 0x0C0C0C0Cu);
+        v[k] = (g[k] ^ m) + b;
+    }
+}
+
 __device__ __forceinline__ int dot_iq3_s_core(uint32_t dbits, uint32_t qs0, uint32_t qs1, uint32_t qh, uint32_t sg,
                                               uint32_t nib, const XBlk& x, const uint32_t* grid, float* dw) {
     *dw = h2f(dbits);
-    const int mult = 1 + 2 * (int)nib;
+    uint32_t v[8];
+    iq3s_levels(qs0, qs1, qh, sg, grid, v);
     int s = 0;
 #pragma unroll
-    for (int l = 0; l < 4; l++) {
-        const uint32_t qsw = l < 2 ? qs0 : qs1;
-        const uint32_t i0 = ((qsw >> (16 * (l & 1))) & 0xFFu) | (((qh >> (2 * l)) & 1u) << 8);
-        const uint32_t i1 = ((qsw >> (16 * (l & 1) + 8)) & 0xFFu) | (((qh >> (2 * l + 1)) & 1u) << 8);
-        const uint32_t sb = (sg >> (8 * l)) & 0xFFu;
-        const uint32_t m0 = nib_mask(sb & 0xFu), m1 = nib_mask(sb >> 4);
-        // signed levels: (g ^ m) + (m & 1): per-byte negation, no carry since g >= 1
-        const uint32_t v0 = (grid[i0] ^ m0) + (m0 & 0x01010101u);
-        const uint32_t v1 = (grid[i1] ^ m1) + (m1 & 0x01010101u);
-        s = dot4((int)v0, x.q[2 * l], s);
-        s = dot4((int)v1, x.q[2 * l + 1], s);
-    }
-    return __mul24(s, mult);
+    for (int k = 0; k < 8; k++) s = dot4((int)v[k], x.q[k], s);
+    return __mul24(s, 1 + 2 * (int)nib);
 }
-
 __device__ __forceinline__ int dot_q8_0(const uint8_t* row, int off, const XBlk& x, float* dw) {
     uint32_t q[8];
 #pragma unroll
@@ -274,19 +291,10 @@ __device__ __forceinline__ void wdec_iq3_s_core(uint32_t dbits, uint32_t qs0, ui
                                                 uint32_t nib, const uint32_t* grid, WBlk& w) {
     w.dw = h2f(dbits);
     w.mult = 1 + 2 * (int)nib;
+    uint32_t v[8];
+    iq3s_levels(qs0, qs1, qh, sg, grid, v);
 #pragma unroll
-    for (int l = 0; l < 4; l++) {
-        const uint32_t qsw = l < 2 ? qs0 : qs1;
-        const uint32_t i0 = ((qsw >> (16 * (l & 1))) & 0xFFu) | (((qh >> (2 * l)) & 1u) << 8);
-        const uint32_t i1 = ((qsw >> (16 * (l & 1) + 8)) & 0xFFu) | (((qh >> (2 * l + 1)) & 1u) << 8);
-        const uint32_t sb = (sg >> (8 * l)) & 0xFFu;
-        const uint32_t b0 = nib_bits(sb & 0xFu), b1 = nib_bits(sb >> 4);
-        const uint32_t m0 = __builtin_amdgcn_perm(0u, 0u, b0 | 0x0C0C0C0Cu);
-        const uint32_t m1 = __builtin_amdgcn_perm(0u, 0u, b1 | 0x0C0C0C0Cu);
-        // signed levels: (g ^ m) + (m & 1): per-byte negation, no carry since g >= 1
-        w.v[2 * l] = (int)((grid[i0] ^ m0) + b0);
-        w.v[2 * l + 1] = (int)((grid[i1] ^ m1) + b1);
-    }
+    for (int k = 0; k < 8; k++) w.v[k] = (int)v[k];
 }
 
 // 6-bit scale and min of sub-block j (0..7) from the 12 packed scale bytes
@@ -609,6 +617,48 @@ __device__ __forceinline__ void stage_rows(uint8_t* __restrict__ lds, const uint
             }
         }
     }
+}
+
+// Asynchronous global->LDS copy, in one loop, of (1) n1 row segments of seg
+// bytes at g1 + r*gstride and n2 at g2 + r*gstride, each as the 16-byte
+// aligned span holding it (one piece per 16 bytes), to LDS rows of stride
+// rs = 16 * pieces-per-row from `lds`, and (2) nx 16-byte pieces xsrc(i) to
+// xlds + 16*i, starting at a multiple of 64 pieces so that each wave's 64
+// lanes write one contiguous LDS run (the LDS address of these copies is
+// wave-uniform).  One loop, because the compiler separates copy loops it
+// cannot prove disjoint by a full wait.  Needs gstride % 16 == 0 and g1, g2
+// at the same offset modulo 16 (every row then starts `pre` bytes into its
+// LDS row: the return value; rs is returned in *rs_out).  Reads at most 15
+// bytes beyond each end of a segment, inside the 16-byte granules holding
+// its ends (so never outside a mapped page).
+template <int CPOL, class XSrc>
+__device__ __forceinline__ int stage_spans(uint8_t* __restrict__ lds, const uint8_t* g1, int n1, const uint8_t* g2,
+                                           int n2, int64_t gstride, int seg, int* rs_out,
+                                           uint8_t* __restrict__ xlds, int nx, XSrc xsrc, int tid, int nthreads) {
+    const int pre = (int)((uintptr_t)g1 & 15);
+    const int per = (pre + seg + 15) >> 4;
+    *rs_out = per * 16;
+    const uint8_t* b1 = g1 - pre;
+    const uint8_t* b2 = g2 - pre;
+    const int t1 = per * n1, tw = t1 + per * n2;
+    const int twp = (tw + 63) & ~63, tot = twp + nx;
+    const int lane = tid & 63, wave = tid >> 6, nw = nthreads >> 6;
+    for (int c0 = wave * 64; c0 < tot; c0 += nw * 64) {
+        const int c = c0 + lane;
+        if (c0 < twp) {
+            if (c < tw) {
+                const bool second = c >= t1;
+                const int cc = second ? c - t1 : c;
+                const int r = cc / per, col = cc - r * per;
+                const uint8_t* src = (second ? b2 : b1) + r * gstride + col * 16;
+                __builtin_amdgcn_global_load_lds((const glb_void_t*)src, (lds_void_t*)(lds + c0 * 16), 16, 0, CPOL);
+            }
+        } else if (c < tot) {
+            __builtin_amdgcn_global_load_lds((const glb_void_t*)xsrc(c - twp), (lds_void_t*)(xlds + (c0 - twp) * 16),
+                                             16, 0, 0);
+        }
+    }
+    return pre;
 }
 
 // Waits for this thread's outstanding memory operations, including the

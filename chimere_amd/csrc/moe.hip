@@ -895,7 +895,7 @@ __device__ __forceinline__ void kg_tile(uint8_t* tile, XLds* xs, uint8_t* xraw, 
         float a1[4][1];
         if constexpr (kg_db<T>())
             tile_gemv_db<T, 1, KG_RG, 4, KG_BLK, CPOL_STREAM>(tile, KG_BUF, xraw, grid, g, QK, u, QK, rb, a.H, a.xq, a.xq_stride,
-                                                 toks, 1, a1);
+                                                 toks, 1, a1, PHASE_PTR(1, 10));
         else
             tile_gemv<T, 1, KG_RG, 4, KG_BLK, CPOL_STREAM>(tile, xs, grid, g, QK, u, QK, rb, a.H, a.xq, a.xq_stride, toks, 1, a1);
 #pragma unroll

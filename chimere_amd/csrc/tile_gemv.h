@@ -109,20 +109,38 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds* __re
 #ifdef CHIMERE_PHASE_TIMING
         if (ph && tid == 0) ph[1] = __builtin_amdgcn_s_memrealtime();
 #endif
+        const uint8_t* tl = tile;
+        if constexpr (NT == 1) {
+            // one token: the activation block is read once for all RPG rows
+            for (int b = j; b < cb; b += SLOTS) {
+                XBlk xb;
+                xlds_to_blk(xs[b], xb);
 #pragma unroll
-        for (int r = 0; r < RPG; r++) {
-            const int row_i = g + RG * r;
-            if (row_i < nr) {
-                const uint8_t* row = tile + row_i * seg;
-                for (int b = j; b < cb; b += SLOTS) {
-                    WBlk wb;   // decoded once, used for every token
-                    block_decode<T>(row, b, grid, wb);
+                for (int r = 0; r < RPG; r++) {
+                    const int row_i = g + RG * r;
+                    if (row_i < nr) {
+                        WBlk wb;
+                        block_decode<T>(tl + row_i * seg, b, grid, wb);
+                        acc[r][0] = wacc<T>(wb, xb, acc[r][0]);
+                    }
+                }
+            }
+        } else {
 #pragma unroll
-                    for (int t = 0; t < NT; t++) {
-                        if (t < ntok) {
-                            XBlk xb;
-                            xlds_to_blk(xs[t * CBLK + b], xb);
-                            acc[r][t] = wacc<T>(wb, xb, acc[r][t]);
+            for (int r = 0; r < RPG; r++) {
+                const int row_i = g + RG * r;
+                if (row_i < nr) {
+                    const uint8_t* row = tl + row_i * seg;
+                    for (int b = j; b < cb; b += SLOTS) {
+                        WBlk wb;   // decoded once, used for every token
+                        block_decode<T>(row, b, grid, wb);
+#pragma unroll
+                        for (int t = 0; t < NT; t++) {
+                            if (t < ntok) {
+                                XBlk xb;
+                                xlds_to_blk(xs[t * CBLK + b], xb);
+                                acc[r][t] = wacc<T>(wb, xb, acc[r][t]);
+                            }
                         }
                     }
                 }
@@ -161,7 +179,7 @@ __device__ __forceinline__ void tile_gemv_db(uint8_t* __restrict__ tile, int TB,
                                              const uint32_t* __restrict__ grid, const uint8_t* base1, int n1,
                                              const uint8_t* base2, int n2, int64_t rb, int ncols,
                                              const uint8_t* __restrict__ X, int64_t x_tok_stride, const int* toks,
-                                             int ntok, float (&acc)[RPG][NT]) {
+                                             int ntok, float (&acc)[RPG][NT], uint64_t* ph = nullptr) {
     constexpr int NTH = RG * SLOTS, XB = NT * CBLK * Q8_1_BYTES;
     static_assert(CBLK % SLOTS == 0 && (QTraits<T>::ELEMS != 256 || CBLK % 8 == 0) && CBLK <= MAX_CHUNK_BLOCKS, "chunk");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -172,16 +190,34 @@ __device__ __forceinline__ void tile_gemv_db(uint8_t* __restrict__ tile, int TB,
     for (int r = 0; r < RPG; r++)
 #pragma unroll
         for (int t = 0; t < NT; t++) acc[r][t] = 0.0f;
+    // 16-byte aligned spans of 4-byte aligned rows (IQ3_S, Q6_K, MXFP4 chunks)
+    // where they fit the buffer: 16-byte copies instead of dword ones
+    const bool spans = stage_dw<T>() && (rb & 15) == 0 && (n2 == 0 || (((uintptr_t)base1 ^ (uintptr_t)base2) & 15) == 0) &&
+                       nr * ((chunk_bytes<T>(CBLK) + 30) / 16 * 16) <= TB;
+    int pre0 = 0, pre1 = 0, rs0 = 0, rs1 = 0;   // per buffer: data offset and LDS row stride
     auto issue = [&](int c, int buf) {
         const int b0 = c * CBLK, cb = min(CBLK, nb - b0);
         const int seg = chunk_bytes<T>(cb);
         const int64_t goff = (int64_t)b0 / (QTraits<T>::ELEMS / QK) * QTraits<T>::BYTES;
         uint8_t* tb = tile + buf * TB;
-        if (n1) stage_rows<stage_dw<T>(), CPOL>(tb, base1 + goff, rb, n1, seg, tid, NTH);
-        if (n2) stage_rows<stage_dw<T>(), CPOL>(tb + n1 * seg, base2 + goff, rb, n2, seg, tid, NTH);
         // token t's cb blocks at xraw + buf*XB + t*cb*36 (16-byte pieces)
         const int per = cb * Q8_1_BYTES / 16, tot = ntok * per;
         uint8_t* xb = xraw + buf * XB;
+        auto xsrc = [&](int cc) {
+            const int t = cc / per, col = cc - t * per;
+            const int tk = toks ? toks[t] : t;
+            return X + tk * x_tok_stride + (int64_t)b0 * Q8_1_BYTES + col * 16;
+        };
+        if (spans) {
+            int rs;
+            const int pre = stage_spans<CPOL>(tb, base1 + goff, n1, base2 + goff, n2, rb, seg, &rs, xb, tot, xsrc,
+                                              tid, NTH);
+            if (buf) { pre1 = pre; rs1 = rs; } else { pre0 = pre; rs0 = rs; }
+            return;
+        }
+        if (buf) { pre1 = 0; rs1 = seg; } else { pre0 = 0; rs0 = seg; }
+        if (n1) stage_rows<stage_dw<T>(), CPOL>(tb, base1 + goff, rb, n1, seg, tid, NTH);
+        if (n2) stage_rows<stage_dw<T>(), CPOL>(tb + n1 * seg, base2 + goff, rb, n2, seg, tid, NTH);
         for (int c0 = wave * 64; c0 < tot; c0 += NTH) {
             const int cc = c0 + lane;
             if (cc < tot) {
@@ -195,31 +231,56 @@ __device__ __forceinline__ void tile_gemv_db(uint8_t* __restrict__ tile, int TB,
     };
     issue(0, 0);
     for (int c = 0; c < nc; c++) {
-        const int buf = c & 1, cb = min(CBLK, nb - c * CBLK), seg = chunk_bytes<T>(cb);
+        const int buf = c & 1, cb = min(CBLK, nb - c * CBLK);
         lds_copy_wait();
         __syncthreads();   // chunk c landed; every wave is done with chunk c-1
+#ifdef CHIMERE_PHASE_TIMING
+        if (ph && tid == 0 && c < 4) ph[2 * c] = __builtin_amdgcn_s_memrealtime();
+#endif
         if (c + 1 < nc) issue(c + 1, buf ^ 1);
-        const uint8_t* tb = tile + buf * TB;
+        const uint8_t* tb = tile + buf * TB + (buf ? pre1 : pre0);
+        const int seg = buf ? rs1 : rs0;   // LDS row stride of this chunk
         const uint8_t* xb = xraw + buf * XB;
+        if constexpr (NT == 1) {
+            // one token: the activation block is read once for all RPG rows
+            // (each row still accumulates its blocks in ascending order)
+            for (int b = j; b < cb; b += SLOTS) {
+                XBlk x;
+                raw_xblk<T>(xb + b * Q8_1_BYTES, x);
 #pragma unroll
-        for (int r = 0; r < RPG; r++) {
-            const int row_i = g + RG * r;
-            if (row_i < nr) {
-                const uint8_t* row = tb + row_i * seg;
-                for (int b = j; b < cb; b += SLOTS) {
-                    WBlk wb;
-                    block_decode<T>(row, b, grid, wb);
+                for (int r = 0; r < RPG; r++) {
+                    const int row_i = g + RG * r;
+                    if (row_i < nr) {
+                        WBlk wb;
+                        block_decode<T>(tb + row_i * seg, b, grid, wb);
+                        acc[r][0] = wacc<T>(wb, x, acc[r][0]);
+                    }
+                }
+            }
+        } else {
 #pragma unroll
-                    for (int t = 0; t < NT; t++) {
-                        if (t < ntok) {
-                            XBlk x;
-                            raw_xblk<T>(xb + (t * cb + b) * Q8_1_BYTES, x);
-                            acc[r][t] = wacc<T>(wb, x, acc[r][t]);
+            for (int r = 0; r < RPG; r++) {
+                const int row_i = g + RG * r;
+                if (row_i < nr) {
+                    const uint8_t* row = tb + row_i * seg;
+                    for (int b = j; b < cb; b += SLOTS) {
+                        WBlk wb;
+                        block_decode<T>(row, b, grid, wb);
+#pragma unroll
+                        for (int t = 0; t < NT; t++) {
+                            if (t < ntok) {
+                                XBlk x;
+                                raw_xblk<T>(xb + (t * cb + b) * Q8_1_BYTES, x);
+                                acc[r][t] = wacc<T>(wb, x, acc[r][t]);
+                            }
                         }
                     }
                 }
             }
         }
+#ifdef CHIMERE_PHASE_TIMING
+        if (ph && tid == 0 && c < 4) ph[2 * c + 1] = __builtin_amdgcn_s_memrealtime();
+#endif
     }
 }
 
