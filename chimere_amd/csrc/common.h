@@ -560,24 +560,26 @@ template <bool DW = false, int CPOL = 0>
 __device__ __forceinline__ void stage_rows(uint8_t* __restrict__ lds, const uint8_t* __restrict__ g,
                                            int64_t gstride, int nrows, int seg, int tid, int nthreads) {
     const uintptr_t al = (uintptr_t)g | (uintptr_t)gstride | (uintptr_t)seg | (uintptr_t)lds;
-    if ((al & 15) == 0) {
+    if (gstride == seg && (((uintptr_t)g | (uintptr_t)lds | (uintptr_t)(seg * nrows)) & 15) == 0) {
+        // rows contiguous in memory and the whole run 16-byte aligned (even
+        // when a row is not, e.g. 220-byte IQ3_S rows): one linear copy
+        const int tot = seg * nrows / 16;
+        const int lane = tid & 63, wave = tid >> 6, nw = nthreads >> 6;
+        for (int c0 = wave * 64; c0 < tot; c0 += nw * 64) {
+            const int c = c0 + lane;
+            if (c < tot)
+                __builtin_amdgcn_global_load_lds((const glb_void_t*)(g + c * 16), (lds_void_t*)(lds + c0 * 16), 16,
+                                                 0, CPOL);
+        }
+    } else if ((al & 15) == 0) {
         const int per = seg >> 4, tot = per * nrows;
         const int lane = tid & 63, wave = tid >> 6, nw = nthreads >> 6;
-        if (gstride == seg) {   // rows contiguous in memory: one linear copy
-            for (int c0 = wave * 64; c0 < tot; c0 += nw * 64) {
-                const int c = c0 + lane;
-                if (c < tot)
-                    __builtin_amdgcn_global_load_lds((const glb_void_t*)(g + c * 16), (lds_void_t*)(lds + c0 * 16),
-                                                     16, 0, CPOL);
-            }
-        } else {
-            for (int c0 = wave * 64; c0 < tot; c0 += nw * 64) {
-                const int c = c0 + lane;
-                if (c < tot) {
-                    const int r = c / per, col = c - r * per;
-                    __builtin_amdgcn_global_load_lds((const glb_void_t*)(g + r * gstride + col * 16),
-                                                     (lds_void_t*)(lds + c0 * 16), 16, 0, CPOL);
-                }
+        for (int c0 = wave * 64; c0 < tot; c0 += nw * 64) {
+            const int c = c0 + lane;
+            if (c < tot) {
+                const int r = c / per, col = c - r * per;
+                __builtin_amdgcn_global_load_lds((const glb_void_t*)(g + r * gstride + col * 16),
+                                                 (lds_void_t*)(lds + c0 * 16), 16, 0, CPOL);
             }
         }
     } else if (DW && (al & 3) == 0) {
