@@ -441,9 +441,9 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert(MoeArgs a) {
 
 // ------------------------------------------ one token, common shapes: K2'
 // k_moe_expert1 does K2's work for one token when every work-group holds at
-// most one item and the weight rows are 16-byte aligned (Q4_0 / Q8_0 experts
-// and shared expert, hidden <= 2048, ffn <= 512, top_k <= 8): the same items,
-// fp32 order and outputs, laid out for latency.
+// most one item and the weight rows are 16-byte aligned (Q4_0 / Q8_0 experts,
+// Q4_0 / Q8_0 / Q4_K / Q5_K shared expert, hidden <= 2048, ffn <= 512,
+// top_k <= 8): the same items, fp32 order and outputs, laid out for latency.
 //  * The shared expert's items do not wait for routing; the routed items'
 //    Q8_1(x) blocks are decoded by waves 1.. while wave 0 runs softmax/top-k.
 //  * Gate/up rows arrive in K chunks alternating between two LDS buffers, so
@@ -457,7 +457,7 @@ constexpr int E1_ROWS = 2 * QK / (EX_THREADS / 64);   // rows copied per wave an
 template <int T>
 constexpr int e1_cblk() { return T == T_Q8_0 ? 16 : 32; }   // blocks per chunk
 template <int T>
-constexpr int e1_cbytes() { return e1_cblk<T>() * QTraits<T>::BYTES; }
+constexpr int e1_cbytes() { return chunk_bytes<T>(e1_cblk<T>()); }
 constexpr int E1_MAX_H = 2048;
 
 // s_waitcnt with only the vector-memory count: at most n outstanding
@@ -486,8 +486,8 @@ __device__ __forceinline__ void e1_issue(uint8_t* buf, const uint8_t* gate, cons
     constexpr int CBLK = e1_cblk<T>();
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int cb = min(CBLK, nbH - c * CBLK);
-    const int seg = cb * QTraits<T>::BYTES;   // a multiple of 16 (cb is a multiple of 8)
-    const int64_t goff = (int64_t)c * CBLK * QTraits<T>::BYTES;
+    const int seg = chunk_bytes<T>(cb);   // a multiple of 16 for the types this kernel takes
+    const int64_t goff = chunk_bytes<T>(c * CBLK);
 #pragma unroll
     for (int k = 0; k < E1_ROWS; k++) {
         const int r = wave + (EX_THREADS / 64) * k;
@@ -794,7 +794,33 @@ __device__ __forceinline__ float dc1_row(const uint8_t* drow, const uint8_t* hbl
 #pragma unroll
         for (int k = 0; k < 8; k++) { xb.q[k] = (int)hw[1 + k]; sq = dot4(xb.q[k], 0x01010101, sq); }
         xb.sumq = sq;
-        v = __builtin_fmaf(w.dw * xb.d, (float)wdot<T>(w, xb), 0.0f);
+        v = wacc<T>(w, xb, 0.0f);
+    }
+    return slot_reduce16(v);
+}
+
+template <int T>
+constexpr bool is_kquant() { return T == T_Q4_K || T == T_Q5_K || T == T_Q6_K; }
+
+// K-quant shared expert (256-element superblocks whose blocks are spread over
+// the superblock): the wave stages its 4 rows in LDS with 2-byte loads, then
+// each lane decodes its block from there.
+template <int T>
+__device__ __forceinline__ float dc1_row_lds(uint8_t* rows, const uint8_t* d0, int64_t rbF, int rr, int j,
+                                             const uint8_t* hblk, bool act) {
+    const int lane = threadIdx.x & 63;
+    const int n16 = (int)(DC1_ROWS * rbF / 2);
+    for (int i = lane; i < n16; i += 64) {
+        const int r = i / (int)(rbF / 2), c = i - r * (int)(rbF / 2);
+        ((uint16_t*)rows)[i] = *(const uint16_t*)(d0 + r * rbF + 2 * c);
+    }
+    float v = 0.0f;
+    if (act) {
+        WBlk w;
+        block_decode<T>(rows + rr * rbF, j, nullptr, w);
+        XBlk xb;
+        load_xblk(hblk, xb);
+        v = wacc<T>(w, xb, 0.0f);
     }
     return slot_reduce16(v);
 }
@@ -802,6 +828,7 @@ __device__ __forceinline__ float dc1_row(const uint8_t* drow, const uint8_t* hbl
 template <int TE, int TS>
 __global__ __launch_bounds__((MAX_K + 1) * 64) void k_moe_dc1(MoeArgs a) {
     __shared__ float dn[DC1_ROWS][MAX_K + 1];
+    __shared__ __attribute__((aligned(16))) uint8_t srows[is_kquant<TS>() ? DC1_ROWS * 2 * 256 : 1];   // F <= 512
     PHASE(2, 0);
     const int tid = threadIdx.x, j = tid & 15, rr = (tid >> 4) & (DC1_ROWS - 1), p = tid >> 6;
     const int tile_i = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
@@ -814,6 +841,9 @@ __global__ __launch_bounds__((MAX_K + 1) * 64) void k_moe_dc1(MoeArgs a) {
         const int e = a.plan[PLAN_UEXP + p];
         v = dc1_row<TE>(a.down + (int64_t)e * a.sd + (int64_t)r * row_bytes(TE, a.F) + j * QTraits<TE>::BYTES, hb,
                         act);
+    } else if constexpr (is_kquant<TS>()) {
+        const int64_t rbF = row_bytes(TS, a.F);
+        v = dc1_row_lds<TS>(srows, a.sh_down + (int64_t)tile_i * DC1_ROWS * rbF, rbF, rr, j, hb, act);
     } else {
         v = dc1_row<TS>(a.sh_down + (int64_t)r * row_bytes(TS, a.F) + j * QTraits<TS>::BYTES, hb, act);
     }
@@ -1129,7 +1159,8 @@ template <int TE, int TS, int NT>
 static void launch_layer_nt(const MoeArgs& a, int stage, hipStream_t s) {
     if (stage < 0 || stage == 0)
         hipLaunchKernelGGL((k_moe_route<NT>), dim3(route_grid(a)), dim3(256), 0, s, a);
-    if constexpr (NT == 1 && (TE == T_Q4_0 || TE == T_Q8_0) && (TS == T_Q4_0 || TS == T_Q8_0)) {
+    if constexpr (NT == 1 && (TE == T_Q4_0 || TE == T_Q8_0) &&
+                  (TS == T_Q4_0 || TS == T_Q8_0 || TS == T_Q4_K || TS == T_Q5_K)) {
         if (expert1_fits(a, TE, TS)) {
             if (stage < 0 || stage == 1)
                 hipLaunchKernelGGL((k_moe_expert1<TE, TS>), dim3(expert_grid(256)), dim3(EX_THREADS), 0, s, a);
@@ -1139,10 +1170,12 @@ static void launch_layer_nt(const MoeArgs& a, int stage, hipStream_t s) {
             return;
         }
     }
-    if (stage < 0 || stage == 1)
-        hipLaunchKernelGGL((k_moe_expert<TE, TS, NT>), dim3(expert_grid(256)), dim3(EX_THREADS), 0, s, a);
-    if (stage < 0 || stage == 2)
-        hipLaunchKernelGGL(k_moe_combine, dim3((a.H + TILE_ROWS - 1) / TILE_ROWS), dim3(GEMV_THREADS), 0, s, a);
+    if constexpr (!is_kquant<TS>()) {
+        if (stage < 0 || stage == 1)
+            hipLaunchKernelGGL((k_moe_expert<TE, TS, NT>), dim3(expert_grid(256)), dim3(EX_THREADS), 0, s, a);
+        if (stage < 0 || stage == 2)
+            hipLaunchKernelGGL(k_moe_combine, dim3((a.H + TILE_ROWS - 1) / TILE_ROWS), dim3(GEMV_THREADS), 0, s, a);
+    }
 }
 
 // M > 1: five launches (stage 0: router + plan, 1: gate/up, 2: down + combine)
@@ -1165,8 +1198,17 @@ static void launch_layer_multi(const MoeArgs& a, int stage, hipStream_t s) {
 // one token: the fused three-launch layer
 template <int TE, int TS>
 static void launch_layer(const MoeArgs& a, int stage, hipStream_t s) {
-    if (a.M == 1) launch_layer_nt<TE, TS, 1>(a, stage, s);
-    else launch_layer_multi<TE, TS>(a, stage, s);
+    if constexpr (is_kquant<TS>()) {
+        // K-quant shared expert: the one-token kernel where it fits, else the
+        // several-token launches (K2 / K3 have no K-quant down path)
+        if (a.M == 1 && (TE == T_Q4_0 || TE == T_Q8_0) && TS != T_Q6_K && expert1_fits(a, TE, TS))
+            launch_layer_nt<TE, TS, 1>(a, stage, s);
+        else
+            launch_layer_multi<TE, TS>(a, stage, s);
+    } else {
+        if (a.M == 1) launch_layer_nt<TE, TS, 1>(a, stage, s);
+        else launch_layer_multi<TE, TS>(a, stage, s);
+    }
 }
 
 template <int TE>
@@ -1175,6 +1217,9 @@ static bool dispatch_ts(int ts, const MoeArgs& a, int stage, hipStream_t s) {
     case T_Q8_0: launch_layer<TE, T_Q8_0>(a, stage, s); return true;
     case T_Q4_0: launch_layer<TE, T_Q4_0>(a, stage, s); return true;
     case T_IQ3_S: launch_layer<TE, T_IQ3_S>(a, stage, s); return true;
+    case T_Q4_K: launch_layer<TE, T_Q4_K>(a, stage, s); return true;
+    case T_Q5_K: launch_layer<TE, T_Q5_K>(a, stage, s); return true;
+    case T_Q6_K: launch_layer<TE, T_Q6_K>(a, stage, s); return true;
     }
     return false;
 }
@@ -1190,6 +1235,8 @@ static bool dispatch_layer(int te, int ts, const MoeArgs& a, int stage, hipStrea
 }
 
 static bool valid_type(int t) { return t == T_Q8_0 || t == T_Q4_0 || t == T_IQ3_S; }
+// the shared expert may also be a K-quant (Q5_K in the reference model)
+static bool valid_shared_type(int t) { return valid_type(t) || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
 
 // ---------------------------------------------- standalone glue kernels
 
@@ -1257,7 +1304,7 @@ static void moe_decode(const chimere_moe_layer* L, const float* x, float* out, i
                     "moe_ffn_decode: n_experts=%d top_k=%d out of range", E, K);
     CHIMERE_REQUIRE(valid_type(L->expert_type), CHIMERE_ERR_ARG, "moe_ffn_decode: expert_type %d", L->expert_type);
     const bool has_sh = L->shared_type >= 0;
-    CHIMERE_REQUIRE(!has_sh || (valid_type(L->shared_type) && L->sh_gate && L->sh_up && L->sh_down),
+    CHIMERE_REQUIRE(!has_sh || (valid_shared_type(L->shared_type) && L->sh_gate && L->sh_up && L->sh_down),
                     CHIMERE_ERR_ARG, "moe_ffn_decode: shared expert incomplete");
     CHIMERE_REQUIRE(L->router_w && L->gate_exps && L->up_exps && L->down_exps, CHIMERE_ERR_ARG,
                     "moe_ffn_decode: null weight pointer");

@@ -197,3 +197,28 @@ def test_moe_m1_paths(dev, et, st, gate_vec, K, E, H, F, mis):
     g = torch.Generator(device=dev).manual_seed(12)
     for _ in range(2):
         run_and_check(layer, torch.randn(1, H, generator=g, device=dev))
+
+
+@pytest.mark.parametrize("et,st,M,H,F", [
+    (O.Q4_0, O.Q5_K, 1, 2048, 512),     # one-token kernel with the reference model's shared type
+    (O.Q8_0, O.Q4_K, 1, 2048, 512),
+    (O.Q4_0, O.Q6_K, 1, 1024, 256),     # Q6_K shared: several-token launches for one token
+    (O.IQ3_S, O.Q5_K, 1, 2048, 512),    # the reference model's types (IQ3_S experts, Q5_K shared)
+    (O.IQ3_S, O.Q5_K, 4, 2048, 512),
+    (O.Q4_0, O.Q6_K, 3, 1024, 256),
+])
+def test_moe_kquant_shared(dev, et, st, M, H, F):
+    """K-quant shared expert (valid random blocks from the independent packer), bit-exact."""
+    import npref
+    print(f"moe kquant shared et={et} st={st} M={M} H={H} F={F}", flush=True)
+    E, K = 64, 8
+    g = torch.Generator(device=dev).manual_seed(600 + st + M)
+    router = torch.randn(E, H, generator=g, device=dev) * 0.02
+    gate, up, down = qmat(et, F, H, E, g, dev), qmat(et, F, H, E, g, dev), qmat(et, H, F, E, g, dev)
+    rng = np.random.default_rng(700 + st)
+    sh = tuple(torch.from_numpy(np.ascontiguousarray(npref.rand_kq(st, r, c, rng).reshape(-1))).to(dev)
+               for r, c in ((F, H), (F, H), (H, F)))
+    gw = torch.randn(H, generator=g, device=dev) * 0.02
+    layer = MoeLayer(router, gate, up, down, et, K, shared=sh, shared_type=st, sh_gate_w=gw)
+    x = torch.randn(M, H, generator=g, device=dev)
+    run_and_check(layer, x)
