@@ -12,6 +12,8 @@ come from HBM and not from the 256 MB Infinity Cache.  Timed as one HIP graph
 of exactly K steps between events, after W warm-up steps.
 
 Also reported (extra): M=8 IQ3_S layer (config 4, uniform and Zipf routing),
+one token through the IQ3_S layers with a Q8_0 and with a Q5_K shared expert
+(the reference model's types),
 the 512-token Q4_0 prefill chunk (config 5, int8 MFMA), the Q4_0 151936x2048
 head GEMV (config 2), the Q8_0 4096x2048 GEMV (config 1),
 per-kernel times and the roofline of the dominant kernel, and the CPU
@@ -254,6 +256,31 @@ def main():
             ub = np.mean(uniq) * (2 * F * row_bytes(IQ3_S, H) + H * row_bytes(IQ3_S, F))
             extra[f"m8_iq3s_{label}"] = {"us_per_layer": round(us8, 2), "mean_unique_experts": round(float(np.mean(uniq)), 2),
                                          "GBs_unique_expert_bytes": round(ub / (us8 * 1e-6) / 1e9, 1)}
+            if bias is None:
+                # one token through the same IQ3_S layers, and with the reference
+                # model's Q5_K shared expert (valid random Q5_K blocks: random
+                # quant and scale bytes, f16 d = 1e-3, dmin = 2e-4)
+                gq = torch.Generator(device=dev).manual_seed(9)
+
+                def rand_q5k(rows, cols):
+                    blk = torch.randint(0, 256, (rows, cols // 256, 176), dtype=torch.uint8, device=dev, generator=gq)
+                    blk[:, :, 0:2] = torch.full((rows, cols // 256, 1), 1e-3, dtype=torch.float16,
+                                                device=dev).view(torch.uint8)
+                    blk[:, :, 2:4] = torch.full((rows, cols // 256, 1), 2e-4, dtype=torch.float16,
+                                                device=dev).view(torch.uint8)
+                    return blk.reshape(-1)
+                sh5 = (rand_q5k(F, H), rand_q5k(F, H), rand_q5k(H, F))
+                l5 = [MoeLayer(L.tensors[0], L.tensors[1], L.tensors[2], L.tensors[3], IQ3_S, K, shared=sh5,
+                               shared_type=13) for L in l8]
+                x1 = torch.randn(64, 1, H, generator=gx, device=dev)
+                o1 = torch.empty(1, H, device=dev)
+                sel3 = K * (2 * F * row_bytes(IQ3_S, H) + H * row_bytes(IQ3_S, F))
+                for tag, ls in (("m1_iq3s_q8_0", l8), ("m1_iq3s_q5k", l5)):
+                    fns = [(lambda i=i, ls=ls: ls[i % R8].forward(x1[i % 64], out=o1)) for i in range(192)]
+                    t1m, _ = graph_time(fns)
+                    u1 = t1m / 192 * 1e6
+                    extra[tag] = {"us_per_layer": round(u1, 2), "GBs_selected": round(sel3 / (u1 * 1e-6) / 1e9, 1)}
+                del l5, sh5
             del l8
             torch.cuda.empty_cache()
 

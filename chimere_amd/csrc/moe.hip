@@ -458,6 +458,10 @@ template <int T>
 constexpr int e1_cblk() { return T == T_Q8_0 ? 16 : 32; }   // blocks per chunk
 template <int T>
 constexpr int e1_cbytes() { return chunk_bytes<T>(e1_cblk<T>()); }
+// LDS row stride of a chunk: IQ3_S chunks (4 superblocks, 440 B) are copied as
+// the 16-byte aligned span holding them, up to 15 bytes more on each side
+template <int T>
+constexpr int e1_stride() { return T == T_IQ3_S ? (e1_cbytes<T>() + 15 + 15) / 16 * 16 : e1_cbytes<T>(); }
 constexpr int E1_MAX_H = 2048;
 
 // s_waitcnt with only the vector-memory count: at most n outstanding
@@ -479,38 +483,44 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // Copies chunk c (blocks [c*CBLK, c*CBLK + cb)) of the 2*QK gate/up rows into
-// buf (row stride cbytes).  One copy instruction per (wave, row).
+// buf (row stride e1_stride).  One copy instruction per (wave, row).  Rows
+// start 16-byte aligned; a chunk that does not (IQ3_S) is copied as the
+// 16-byte aligned span holding it and starts `pre` bytes into its LDS row
+// (the same for every row): the return value.
 template <int T>
-__device__ __forceinline__ void e1_issue(uint8_t* buf, const uint8_t* gate, const uint8_t* up, int64_t rb, int c,
-                                         int nbH) {
+__device__ __forceinline__ int e1_issue(uint8_t* buf, const uint8_t* gate, const uint8_t* up, int64_t rb, int c,
+                                        int nbH) {
     constexpr int CBLK = e1_cblk<T>();
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int cb = min(CBLK, nbH - c * CBLK);
-    const int seg = chunk_bytes<T>(cb);   // a multiple of 16 for the types this kernel takes
     const int64_t goff = chunk_bytes<T>(c * CBLK);
+    const int pre = (int)(goff & 15);
+    const int span = pre + chunk_bytes<T>(cb);   // bytes from the aligned start
 #pragma unroll
     for (int k = 0; k < E1_ROWS; k++) {
         const int r = wave + (EX_THREADS / 64) * k;
-        const uint8_t* src = (r < QK ? gate + (int64_t)r * rb : up + (int64_t)(r - QK) * rb) + goff;
-        if (lane * 16 < seg)
+        const uint8_t* src = (r < QK ? gate + (int64_t)r * rb : up + (int64_t)(r - QK) * rb) + goff - pre;
+        if (lane * 16 < span)
             __builtin_amdgcn_global_load_lds((const glb_void_t*)(src + lane * 16),
-                                             (lds_void_t*)(buf + r * e1_cbytes<T>()), 16, 0, CPOL_STREAM);
+                                             (lds_void_t*)(buf + r * e1_stride<T>()), 16, 0, CPOL_STREAM);
     }
+    return pre;
 }
 
 // Dots of chunk c for this thread's row (row group g) and lane j: blocks
 // j, j+16, ... of the chunk, in ascending order (the L=16 order).
 template <int T>
-__device__ __forceinline__ float e1_dots(const uint8_t* buf, const XLds* xs, int c, int nbH, float acc) {
+__device__ __forceinline__ float e1_dots(const uint8_t* buf, int pre, const XLds* xs, const uint32_t* grid, int c,
+                                         int nbH, float acc) {
     constexpr int CBLK = e1_cblk<T>();
     const int g = threadIdx.x >> 4, j = threadIdx.x & 15;
     const int cb = min(CBLK, nbH - c * CBLK);
-    const uint8_t* row = buf + g * e1_cbytes<T>();
+    const uint8_t* row = buf + g * e1_stride<T>() + pre;
 #pragma unroll
     for (int b = j; b < CBLK; b += SLOTS) {
         if (b < cb) {
             WBlk wb;
-            block_decode<T>(row, b, nullptr, wb);
+            block_decode<T>(row, b, grid, wb);
             XBlk xb;
             xlds_to_blk(xs[c * CBLK + b], xb);
             acc = wacc<T>(wb, xb, acc);
@@ -523,8 +533,8 @@ __device__ __forceinline__ float e1_dots(const uint8_t* buf, const XLds* xs, int
 // terms (lane_acc[pair][w][r], F <= 512).
 template <int T>
 __device__ __forceinline__ void e1_item(const MoeArgs& a, uint8_t* bufA, uint8_t* bufB, const XLds* xs,
-                                        float (*hg)[QK], float (*hu)[QK], int pair, int w, const uint8_t* gate,
-                                        const uint8_t* up) {
+                                        const uint32_t* grid, float (*hg)[QK], float (*hu)[QK], int pair, int w,
+                                        const uint8_t* gate, const uint8_t* up) {
     constexpr int CBLK = e1_cblk<T>();
     const int tid = threadIdx.x;
     const int nbH = a.H / QK;
@@ -532,8 +542,8 @@ __device__ __forceinline__ void e1_item(const MoeArgs& a, uint8_t* bufA, uint8_t
     const int64_t rb = row_bytes(T, a.H);
     gate += (int64_t)w * QK * rb;
     up += (int64_t)w * QK * rb;
-    e1_issue<T>(bufA, gate, up, rb, 0, nbH);
-    if (nc > 1) e1_issue<T>(bufB, gate, up, rb, 1, nbH);
+    int preA = e1_issue<T>(bufA, gate, up, rb, 0, nbH), preB = 0;
+    if (nc > 1) preB = e1_issue<T>(bufB, gate, up, rb, 1, nbH);
     // in issue order: chunk 0, chunk 1, then chunk c+2 while chunk c+1 is
     // computed; chunk c has landed when at most the copies of the chunk after
     // it are outstanding
@@ -543,23 +553,23 @@ __device__ __forceinline__ void e1_item(const MoeArgs& a, uint8_t* bufA, uint8_t
         else wait_vm<0>();
         lds_barrier();
         if (c == 0) PHASE(1, 10);
-        acc = e1_dots<T>(bufA, xs, c, nbH, acc);
+        acc = e1_dots<T>(bufA, preA, xs, grid, c, nbH, acc);
         if (c == 0) PHASE(1, 11);
         if (c + 1 >= nc) break;
         lds_barrier();   // every wave is done with buffer A
         if (c + 2 < nc) {
-            e1_issue<T>(bufA, gate, up, rb, c + 2, nbH);
+            preA = e1_issue<T>(bufA, gate, up, rb, c + 2, nbH);
             wait_vm<E1_ROWS>();
         } else {
             wait_vm<0>();
         }
         lds_barrier();
         if (c == 0) PHASE(1, 12);
-        acc = e1_dots<T>(bufB, xs, c + 1, nbH, acc);
+        acc = e1_dots<T>(bufB, preB, xs, grid, c + 1, nbH, acc);
         if (c == 0) PHASE(1, 13);
         if (c + 2 >= nc) break;
         lds_barrier();   // every wave is done with buffer B
-        if (c + 3 < nc) e1_issue<T>(bufB, gate, up, rb, c + 3, nbH);
+        if (c + 3 < nc) preB = e1_issue<T>(bufB, gate, up, rb, c + 3, nbH);
     }
     PHASE(1, 4);
     const int g = tid >> 4, j = tid & 15;
@@ -614,9 +624,10 @@ __device__ __forceinline__ void e1_prefetch(const E1Prefetch& p, const int* uexp
 
 template <int TE, int TS>
 __global__ __launch_bounds__(EX_THREADS) void k_moe_expert1(MoeArgs a) {
-    constexpr int CB = e1_cbytes<TE>() > e1_cbytes<TS>() ? e1_cbytes<TE>() : e1_cbytes<TS>();
+    constexpr int CB = e1_stride<TE>() > e1_stride<TS>() ? e1_stride<TE>() : e1_stride<TS>();
     __shared__ __attribute__((aligned(16))) uint8_t bufA[2 * QK * CB];
     __shared__ __attribute__((aligned(16))) uint8_t bufB[2 * QK * CB];
+    __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
     __shared__ XLds xs[E1_MAX_H / QK];
     __shared__ float hg[1][QK], hu[1][QK];
     __shared__ int s_ids[MAX_K];
@@ -632,6 +643,8 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert1(MoeArgs a) {
     const int ns = a.has_shared ? (NB > x ? (NB - 1 - x) / 8 + 1 : 0) : 0;
     const int nx = nr * NB + ns;
     const bool routed = lb < nr * NB, shared = !routed && lb < nx;
+    if constexpr (TE == T_IQ3_S || TS == T_IQ3_S)   // visible after the first barrier below
+        for (int i = tid; i < 512; i += EX_THREADS) grid[i] = c_iq3s_grid_moe[i];
     if (!shared) {
         // wave 0: softmax / top-k; the other waves decode Q8_1(x) meanwhile
         if (wave == 0) {
@@ -665,7 +678,7 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert1(MoeArgs a) {
         }
         const int e = s_ids[x];
         PHASE(1, 2);
-        e1_item<TE>(a, bufA, bufB, xs, hg, hu, x, lb, a.gate + e * a.sg, a.up + e * a.su);
+        e1_item<TE>(a, bufA, bufB, xs, grid, hg, hu, x, lb, a.gate + e * a.sg, a.up + e * a.su);
     } else {
         for (int i = tid; i < nbH; i += EX_THREADS) {
             XBlk xb;
@@ -675,7 +688,7 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert1(MoeArgs a) {
             for (int k = 0; k < 8; k++) xs[i].q[k] = xb.q[k];
         }
         PHASE(1, 2);
-        e1_item<TS>(a, bufA, bufB, xs, hg, hu, a.K, x + 8 * (lb - nr * NB), a.sh_gate, a.sh_up);
+        e1_item<TS>(a, bufA, bufB, xs, grid, hg, hu, a.K, x + 8 * (lb - nr * NB), a.sh_gate, a.sh_up);
     }
     PHASE_END(1);
 }
@@ -775,11 +788,13 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_combine(MoeArgs a) {
 constexpr int DC1_ROWS = 4;
 
 template <int T>
-__device__ __forceinline__ float dc1_row(const uint8_t* drow, const uint8_t* hblk, bool act) {
+__device__ __forceinline__ float dc1_row(const uint8_t* row, int j, const uint8_t* hblk, const uint32_t* grid,
+                                         bool act) {
     RegBlk<T> rbk;
     uint32_t hw[9];
     if (act) {
-        rbk.load(drow);
+        if constexpr (T == T_IQ3_S) rbk.load(row + (j >> 3) * 110, j & 7);
+        else rbk.load(row + j * QTraits<T>::BYTES);
         const uint32_t* h = (const uint32_t*)hblk;
 #pragma unroll
         for (int k = 0; k < 9; k++) hw[k] = h[k];
@@ -787,7 +802,7 @@ __device__ __forceinline__ float dc1_row(const uint8_t* drow, const uint8_t* hbl
     float v = 0.0f;
     if (act) {
         WBlk w;
-        rbk.decode(nullptr, w);
+        rbk.decode(grid, w);
         XBlk xb;
         xb.d = h2f(hw[0] & 0xFFFFu);
         int sq = 0;
@@ -829,6 +844,7 @@ template <int TE, int TS>
 __global__ __launch_bounds__((MAX_K + 1) * 64) void k_moe_dc1(MoeArgs a) {
     __shared__ float dn[DC1_ROWS][MAX_K + 1];
     __shared__ __attribute__((aligned(16))) uint8_t srows[is_kquant<TS>() ? DC1_ROWS * 2 * 256 : 1];   // F <= 512
+    __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
     PHASE(2, 0);
     const int tid = threadIdx.x, j = tid & 15, rr = (tid >> 4) & (DC1_ROWS - 1), p = tid >> 6;
     const int tile_i = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
@@ -837,15 +853,18 @@ __global__ __launch_bounds__((MAX_K + 1) * 64) void k_moe_dc1(MoeArgs a) {
     const bool act = j < NB && r < a.H;
     const uint8_t* hb = a.hq + (int64_t)p * a.hq_stride + j * Q8_1_BYTES;
     float v;
+    if constexpr (TE == T_IQ3_S || TS == T_IQ3_S) {
+        for (int i = tid; i < 512; i += blockDim.x) grid[i] = c_iq3s_grid_moe[i];
+        __syncthreads();
+    }
     if (p < K) {
         const int e = a.plan[PLAN_UEXP + p];
-        v = dc1_row<TE>(a.down + (int64_t)e * a.sd + (int64_t)r * row_bytes(TE, a.F) + j * QTraits<TE>::BYTES, hb,
-                        act);
+        v = dc1_row<TE>(a.down + (int64_t)e * a.sd + (int64_t)r * row_bytes(TE, a.F), j, hb, grid, act);
     } else if constexpr (is_kquant<TS>()) {
         const int64_t rbF = row_bytes(TS, a.F);
         v = dc1_row_lds<TS>(srows, a.sh_down + (int64_t)tile_i * DC1_ROWS * rbF, rbF, rr, j, hb, act);
     } else {
-        v = dc1_row<TS>(a.sh_down + (int64_t)r * row_bytes(TS, a.F) + j * QTraits<TS>::BYTES, hb, act);
+        v = dc1_row<TS>(a.sh_down + (int64_t)r * row_bytes(TS, a.F), j, hb, grid, act);
     }
     if (j == 0) dn[rr][p] = v;
     __syncthreads();
@@ -1148,8 +1167,8 @@ static bool expert1_fits(const MoeArgs& a, int te, int ts) {
     const int ns = a.has_shared ? (NB + 7) / 8 : 0;
     const uintptr_t al = (uintptr_t)a.gate | (uintptr_t)a.up | (uintptr_t)a.down | (uintptr_t)a.sg |
                          (uintptr_t)a.su | (uintptr_t)a.sd | (uintptr_t)a.sh_gate | (uintptr_t)a.sh_up |
-                         (uintptr_t)a.sh_down | (uintptr_t)a.xq;
-    (void)te; (void)ts;
+                         (uintptr_t)a.sh_down | (uintptr_t)a.xq | (uintptr_t)row_bytes(te, a.H) |
+                         (uintptr_t)(a.has_shared ? row_bytes(ts, a.H) : 0);
     return a.M == 1 && a.K <= 8 && a.H <= E1_MAX_H && NB <= SLOTS && (al & 15) == 0 &&
            NB + ns <= expert_grid(256) / 8;
 }
@@ -1159,8 +1178,8 @@ template <int TE, int TS, int NT>
 static void launch_layer_nt(const MoeArgs& a, int stage, hipStream_t s) {
     if (stage < 0 || stage == 0)
         hipLaunchKernelGGL((k_moe_route<NT>), dim3(route_grid(a)), dim3(256), 0, s, a);
-    if constexpr (NT == 1 && (TE == T_Q4_0 || TE == T_Q8_0) &&
-                  (TS == T_Q4_0 || TS == T_Q8_0 || TS == T_Q4_K || TS == T_Q5_K)) {
+    if constexpr (NT == 1 && (TE == T_Q4_0 || TE == T_Q8_0 || TE == T_IQ3_S) &&
+                  (TS == T_Q4_0 || TS == T_Q8_0 || TS == T_IQ3_S || TS == T_Q4_K || TS == T_Q5_K)) {
         if (expert1_fits(a, TE, TS)) {
             if (stage < 0 || stage == 1)
                 hipLaunchKernelGGL((k_moe_expert1<TE, TS>), dim3(expert_grid(256)), dim3(EX_THREADS), 0, s, a);
@@ -1201,7 +1220,7 @@ static void launch_layer(const MoeArgs& a, int stage, hipStream_t s) {
     if constexpr (is_kquant<TS>()) {
         // K-quant shared expert: the one-token kernel where it fits, else the
         // several-token launches (K2 / K3 have no K-quant down path)
-        if (a.M == 1 && (TE == T_Q4_0 || TE == T_Q8_0) && TS != T_Q6_K && expert1_fits(a, TE, TS))
+        if (a.M == 1 && TS != T_Q6_K && expert1_fits(a, TE, TS))
             launch_layer_nt<TE, TS, 1>(a, stage, s);
         else
             launch_layer_multi<TE, TS>(a, stage, s);

@@ -183,7 +183,9 @@ def misalign(t, off=2):
     (O.Q4_0, O.Q8_0, True, 6, 32, 1024, 256, False),    # mixed types, XCDs without a routed expert
     (O.Q8_0, O.Q4_0, False, 3, 16, 256, 256, False),    # one K chunk shorter than a chunk
     (O.Q4_0, None, False, 8, 64, 2048, 512, False),     # no shared expert
-    (O.IQ3_S, O.Q8_0, True, 8, 64, 2048, 512, False),   # IQ3_S: general one-token kernel
+    (O.IQ3_S, O.Q8_0, True, 8, 64, 2048, 512, False),   # IQ3_S chunks as 16-byte aligned spans
+    (O.IQ3_S, O.IQ3_S, False, 8, 64, 2048, 512, False),
+    (O.IQ3_S, O.Q8_0, True, 8, 64, 1024, 256, False),   # 440-byte IQ3_S rows: general one-token kernel
     (O.Q4_0, O.Q4_0, False, 8, 64, 2048, 512, True),    # rows not 16-byte aligned: general kernel
 ])
 def test_moe_m1_paths(dev, et, st, gate_vec, K, E, H, F, mis):
