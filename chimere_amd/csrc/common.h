@@ -667,6 +667,42 @@ __device__ __forceinline__ int stage_spans(uint8_t* __restrict__ lds, const uint
 // asynchronous global->LDS copies; follow with __syncthreads().
 __device__ __forceinline__ void lds_copy_wait() { __builtin_amdgcn_s_waitcnt(0); }
 
+// s_waitcnt with only the vector-memory count: at most n outstanding
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+
+// One 16-byte asynchronous global->LDS copy per lane (lane i writes
+// lds_wave + 16 i; lds_wave must be the same for the whole wave).  Issued as
+// inline assembly so that the compiler does not track it: it then inserts no
+// vmcnt waits of its own before LDS reads it cannot prove disjoint from the
+// copy, and the caller owns the wait (wait_vm, counted per wave in issue
+// order) before reading the destination.  Compiler-tracked loads stay
+// correct: an untracked copy issued after one of them only makes a vmcnt
+// wait for it stricter.
+__device__ __forceinline__ void copy16_lds_untracked(const void* g, void* lds_wave) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_wave);
+    uint32_t saved;   // m0 is restored: compiler-generated code may keep a value there
+    __asm__ volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\t"
+                     "s_mov_b32 m0, %0"
+                     : "=&s"(saved)
+                     : "v"(g), "s"(m)
+                     : "memory");
+}
+
+// Work-group barrier that waits only for this wave's LDS accesses: the
+// release fence of __syncthreads() would also wait for every outstanding
+// asynchronous copy (they write LDS), including the next chunk's.  The empty
+// asm statements keep memory accesses on their side of the barrier.
+__device__ __forceinline__ void lds_barrier() {
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+}
+
 // Value of lane (lane ^ M) without going through LDS: DPP quad permutes for
 // M = 1, 2, a half-row mirror plus a quad reversal for M = 4, a row rotation
 // by 8 for M = 8, and the gfx950 v_permlane16/32_swap for M = 16, 32.  The partner lane must be

@@ -464,24 +464,6 @@ template <int T>
 constexpr int e1_stride() { return T == T_IQ3_S ? (e1_cbytes<T>() + 15 + 15) / 16 * 16 : e1_cbytes<T>(); }
 constexpr int E1_MAX_H = 2048;
 
-// s_waitcnt with only the vector-memory count: at most n outstanding
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
-}
-
-// Work-group barrier that waits only for this wave's LDS accesses: the
-// release fence of __syncthreads() would also wait for every outstanding
-// asynchronous copy (they write LDS), including the next chunk's.  The empty
-// asm statements keep memory accesses on their side of the barrier.
-__device__ __forceinline__ void lds_barrier() {
-    __asm__ volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    __asm__ volatile("" ::: "memory");
-}
-
 // Copies chunk c (blocks [c*CBLK, c*CBLK + cb)) of the 2*QK gate/up rows into
 // buf (row stride e1_stride).  One copy instruction per (wave, row).  Rows
 // start 16-byte aligned; a chunk that does not (IQ3_S) is copied as the

@@ -208,17 +208,23 @@ constexpr int pf_row_chunk_bytes() { return PF_CHUNK * QTraits<T>::BYTES; }
 
 // 8 weight values of block b of an LDS row as int8, and f32(d)
 template <int T>
-__device__ __forceinline__ long pf_b_frag(const uint8_t* row, int b, int q, float* dw) {
+__device__ __forceinline__ long pf_b_frag(const uint8_t* row, int b, int q, uint32_t* dw) {
     uint32_t lo, hi;
     if constexpr (T == T_Q4_0) {
+        // bytes o .. o+7 of the row hold the 16 nibbles (low nibbles for
+        // q < 2, high for q >= 2); o is 2 mod 4 for even b, 0 mod 4 for odd
+        // b, so three aligned dwords and one funnel shift per result dword
+        // (byte alignment and nibble select in one) do it
         const int off = b * 18;
-        *dw = h2f(lds_u16(row, off));
-        const int o = off + 2 + 8 * (q & 1), sh = 4 * (q >> 1);
-        lo = (lds_u32(row, o) >> sh) & 0x0F0F0F0Fu;
-        hi = (lds_u32(row, o + 4) >> sh) & 0x0F0F0F0Fu;
+        *dw = lds_u16(row, off);
+        const int o = off + 2 + 8 * (q & 1), a = o & ~3, sh = 8 * (o & 3) + 4 * (q >> 1);
+        const uint32_t* w = (const uint32_t*)(row + a);
+        const uint32_t d0 = w[0], d1 = w[1], d2 = w[2];
+        lo = __builtin_amdgcn_alignbit(d1, d0, sh) & 0x0F0F0F0Fu;
+        hi = __builtin_amdgcn_alignbit(d2, d1, sh) & 0x0F0F0F0Fu;
     } else {
         const int off = b * 34;
-        *dw = h2f(lds_u16(row, off));
+        *dw = lds_u16(row, off);
         lo = lds_u32(row, off + 2 + 8 * q);
         hi = lds_u32(row, off + 6 + 8 * q);
     }
@@ -282,7 +288,9 @@ __device__ __forceinline__ void pf_mma_chunk(const uint8_t* xl, const float* xd,
             if constexpr (T == T_Q4_0) c0 = *(const v4i*)(xs8 + b * PF_TILE + 4 * q);
 #pragma unroll
             for (int n = 0; n < NTN; n++) {
-                const long bf = pf_b_frag<T>(wrows + (16 * n + c) * cbytes, b, q, &dw[n]);
+                uint32_t dwb;
+                const long bf = pf_b_frag<T>(wrows + (16 * n + c) * cbytes, b, q, &dwb);
+                dw[n] = h2f(dwb);
                 r[n] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bf, c0, 0, 0, 0);
             }
         }
@@ -301,57 +309,131 @@ __device__ __forceinline__ void pf_mma_chunk(const uint8_t* xl, const float* xd,
     }
 }
 
-// Double-buffered K loop of one work-group: nwrows weight rows starting at
-// w0 (and w1 for the second half when split, see callers), activation rows
-// xrows of xsrc; wave `wave` computes NTN 16-row tiles at LDS row wrow0.
-template <int T, int NTN>
-__device__ __forceinline__ void pf_gemm(uint8_t* wl, uint8_t* xl, float* xd, int* xs8, const uint8_t* w0, int n0,
-                                        const uint8_t* w1, int n1, int64_t rb, int nbk, const uint8_t* xsrc,
-                                        const int* xrows, int64_t xstride, int wrow0, float (&acc)[NTN][4]) {
+// LDS buffers of one pipeline stage: the weight chunk rows, the tile's
+// activation chunk and its per-block metadata
+struct PfStage {
+    uint8_t* w;
+    uint8_t* x;
+    float* xd;
+    int* xs;
+};
+
+// K loop of one work-group: NR weight rows (n0 at w0, the rest at w1; global
+// row stride rb), activation rows xrows of xsrc; wave `wave` computes NTN
+// 16-row tiles at LDS row wrow0.
+//
+// With 16-byte aligned rows: two stages, chunk c + 1 copied into one while
+// chunk c is computed from the other.  Every copy of a chunk (weight rows and
+// activation rows) is one untracked 16-byte copy per lane from a single loop,
+// so the compiler adds no waits of its own (its alias analysis does not
+// separate the stages), and the barriers wait for LDS accesses only: the
+// release fence of __syncthreads() would also wait for the copies in flight.
+// Otherwise one stage, copied and waited for per chunk.
+template <int T, int NTN, int NR, bool AL>
+__device__ __forceinline__ void pf_gemm_k(const PfStage& s0, const PfStage& s1, const uint8_t* w0, int n0,
+                                          const uint8_t* w1, int64_t rb, int nbk, const uint8_t* xsrc,
+                                          const int* xrows, int64_t xstride, int wrow0, float (&acc)[NTN][4]) {
     constexpr int CB = pf_row_chunk_bytes<T>();
-    const int nrows = n0 + n1;
-    const int WST = nrows * CB + 16, XST = PF_TILE * PF_CHUNK * 36;
+    static_assert(CB % 16 == 0, "chunk rows in 16-byte pieces");
+    constexpr int PCB = CB / 16, PER = 36 * PF_CHUNK / 16;
+    constexpr int TW = NR * PCB, TWP = (TW + 63) & ~63, TOT = TWP + PF_TILE * PER;
 #pragma unroll
     for (int n = 0; n < NTN; n++)
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[n][i] = 0.0f;
     const int nc = nbk / PF_CHUNK;
-    auto issue = [&](int c, int buf) {
-        const int64_t goff = (int64_t)c * CB;
-        uint8_t* wb = wl + buf * WST;
-        stage_rows(wb, w0 + goff, rb, n0, CB, threadIdx.x, PF_THREADS);
-        pf_issue(wb + n0 * CB, w1 + goff, rb, n1, CB, xl + buf * XST, xsrc, xrows, xstride,
-                 (int64_t)c * PF_CHUNK * 36);
-    };
-    issue(0, 0);
-    for (int c = 0; c < nc; c++) {
-        const int buf = c & 1;
-        lds_copy_wait();
-        __syncthreads();   // chunk c landed; every wave is done with chunk c-1
-        pf_xmeta(xl + buf * XST, xd + buf * PF_TILE * PF_CHUNK, xs8 + buf * PF_TILE * PF_CHUNK);
-        if (c + 1 < nc) issue(c + 1, buf ^ 1);
-        __syncthreads();
-        pf_mma_chunk<T, NTN>(xl + buf * XST, xd + buf * PF_TILE * PF_CHUNK, xs8 + buf * PF_TILE * PF_CHUNK,
-                             wl + buf * WST + wrow0 * CB, CB, PF_CHUNK, acc);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if constexpr (!AL) {
+        for (int c = 0; c < nc; c++) {
+            const int64_t goff = (int64_t)c * CB, xoff = (int64_t)c * PF_CHUNK * 36;
+            stage_rows(s0.w, w0 + goff, rb, n0, CB, threadIdx.x, PF_THREADS);
+            pf_issue(s0.w + n0 * CB, w1 + goff, rb, NR - n0, CB, s0.x, xsrc, xrows, xstride, xoff);
+            lds_copy_wait();
+            __syncthreads();
+            pf_xmeta(s0.x, s0.xd, s0.xs);
+            __syncthreads();
+            pf_mma_chunk<T, NTN>(s0.x, s0.xd, s0.xs, s0.w + wrow0 * CB, CB, PF_CHUNK, acc);
+            __syncthreads();
+        }
+    } else {
+        auto issue = [&](int c, const PfStage& s) {
+            const int64_t goff = (int64_t)c * CB, xoff = (int64_t)c * PF_CHUNK * 36;
+            for (int c0 = wave * 64; c0 < TOT; c0 += PF_THREADS) {
+                const int cc = c0 + lane;
+                if (c0 < TWP) {
+                    if (cc < TW) {
+                        const int row = cc / PCB, col = cc - row * PCB;
+                        const uint8_t* src = (row < n0 ? w0 + row * rb : w1 + (row - n0) * rb) + goff + col * 16;
+                        copy16_lds_untracked(src, s.w + c0 * 16);
+                    }
+                } else {
+                    const int xc = cc - TWP;
+                    if (xc < PF_TILE * PER) {
+                        const int r = xc / PER, col = xc - r * PER;
+                        copy16_lds_untracked(xsrc + xrows[r] * xstride + xoff + col * 16, s.x + (c0 - TWP) * 16);
+                    }
+                }
+            }
+        };
+        // chunk c from stage cur, chunk c + 1 issued into nxt (the stage chunk
+        // c - 1 was computed from: every wave has passed the barrier since)
+        auto step = [&](int c, const PfStage& cur, const PfStage& nxt) {
+            wait_vm<0>();
+            lds_barrier();   // chunk c landed (every wave's share)
+            pf_xmeta(cur.x, cur.xd, cur.xs);
+            if (c + 1 < nc) issue(c + 1, nxt);
+            lds_barrier();   // metadata written
+            pf_mma_chunk<T, NTN>(cur.x, cur.xd, cur.xs, cur.w + wrow0 * CB, CB, PF_CHUNK, acc);
+        };
+        issue(0, s0);
+        for (int c = 0; c < nc; c += 2) {
+            step(c, s0, s1);
+            if (c + 1 >= nc) break;
+            step(c + 1, s1, s0);
+        }
     }
+    lds_barrier();   // every wave is done with the stages (callers reuse them)
+}
+
+template <int T, int NTN, int NR>
+__device__ __forceinline__ void pf_gemm(const PfStage& s0, const PfStage& s1, const uint8_t* w0, int n0,
+                                        const uint8_t* w1, int64_t rb, int nbk, const uint8_t* xsrc,
+                                        const int* xrows, int64_t xstride, int wrow0, float (&acc)[NTN][4]) {
+    const bool al16 = (((uintptr_t)w0 | (uintptr_t)w1 | (uintptr_t)rb | (uintptr_t)xsrc | (uintptr_t)xstride) & 15) == 0;
+    if (al16) pf_gemm_k<T, NTN, NR, true>(s0, s1, w0, n0, w1, rb, nbk, xsrc, xrows, xstride, wrow0, acc);
+    else pf_gemm_k<T, NTN, NR, false>(s0, s1, w0, n0, w1, rb, nbk, xsrc, xrows, xstride, wrow0, acc);
 }
 
 template <int T>
 constexpr int pf_wst(int nrows) { return nrows * pf_row_chunk_bytes<T>() + 16; }
 constexpr int PF_XST = PF_TILE * PF_CHUNK * 36;
 
-// P4: grid (F/64, max_tiles).  Waves 0, 1: gate rows f0 + [0,32), up rows
-// f0 + [0,32); waves 2, 3: the same for f0 + [32, 64) (two 16-row tiles per
-// wave); then h = silu(gate) * up and Q8_1 of its two 32-row blocks per pair.
+// LDS arrays of the two pipeline stages (separate arrays) and their PfStage
+#define PF_STAGE_ARRAYS(WS)                                                                           \
+    __shared__ __attribute__((aligned(16))) uint8_t wl0[WS], wl1[WS];                                 \
+    __shared__ __attribute__((aligned(16))) uint8_t xl0[PF_XST], xl1[PF_XST];                         \
+    __shared__ __attribute__((aligned(16))) float xd0[PF_TILE * PF_CHUNK], xd1[PF_TILE * PF_CHUNK];   \
+    __shared__ __attribute__((aligned(16))) int xs0[PF_TILE * PF_CHUNK], xs1[PF_TILE * PF_CHUNK];     \
+    const PfStage s0{wl0, xl0, xd0, xs0}, s1{wl1, xl1, xd1, xs1}
+
+// Rows per gate_up work-group: PF_GU_NTN 16-row tiles per wave, half the
+// waves on gate rows and half on the same up rows
+constexpr int PF_GU_NTN = 2;   // 64-row work-groups (one tile per wave) measured slower
+constexpr int PF_GU_ROWS = 32 * PF_GU_NTN;   // gate (and up) rows per work-group
+
+// P4: grid (F/PF_GU_ROWS, max_tiles).  Waves 0, 1: gate and up rows f0 +
+// [0, 16*NTN); waves 2, 3: the same for the next 16*NTN rows (NTN 16-row
+// tiles per wave); then h = silu(gate) * up and Q8_1 of its 32-row blocks per
+// pair.
 template <int TE, int TS>
 __global__ __launch_bounds__(PF_THREADS) void k_pf_gate_up(PfArgs a) {
-    constexpr int WS = pf_wst<TE>(128) > pf_wst<TS>(128) ? pf_wst<TE>(128) : pf_wst<TS>(128);
-    __shared__ __attribute__((aligned(16))) uint8_t wl[2 * WS];
-    __shared__ __attribute__((aligned(16))) uint8_t xl[2 * PF_XST];
-    __shared__ __attribute__((aligned(16))) float xd[2 * PF_TILE * PF_CHUNK];
-    __shared__ __attribute__((aligned(16))) int xs8[2 * PF_TILE * PF_CHUNK];
+    constexpr int NTN = PF_GU_NTN, R = PF_GU_ROWS;
+    constexpr int WS = pf_wst<TE>(2 * R) > pf_wst<TS>(2 * R) ? pf_wst<TE>(2 * R) : pf_wst<TS>(2 * R);
+    PF_STAGE_ARRAYS(WS);
     __shared__ int prs[PF_TILE], xrows[PF_TILE];
-    __shared__ float gu[2][PF_TILE][65];
+    // gate / up results per (pair, row), in stage 0's weight buffer once the K loop is done
+    static_assert(2 * PF_TILE * (R + 1) * sizeof(float) <= WS, "gate/up results fit a stage");
+    float(*gu)[PF_TILE][R + 1] = reinterpret_cast<float(*)[PF_TILE][R + 1]>(wl0);
     const int ti = blockIdx.y;
     if (ti >= *a.ntiles) return;
     const int e = a.tiles[ti * 3], start = a.tiles[ti * 3 + 1], n = a.tiles[ti * 3 + 2];
@@ -363,35 +445,36 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_gate_up(PfArgs a) {
     }
     __syncthreads();
     const bool sh = e == a.E;
-    const int f0 = blockIdx.x * 64;
+    const int f0 = blockIdx.x * R;
     const int wave = tid >> 6, mat = wave & 1, rh = wave >> 1;
-    float acc[2][4];
+    float acc[NTN][4];
     auto run = [&](auto tag) {
         constexpr int T = decltype(tag)::value;
         const int64_t rb = row_bytes(T, a.H);
         const uint8_t* g = sh ? a.sh_gate : a.gate + (int64_t)e * a.sg;
         const uint8_t* u = sh ? a.sh_up : a.up + (int64_t)e * a.su;
-        pf_gemm<T, 2>(wl, xl, xd, xs8, g + f0 * rb, 64, u + f0 * rb, 64, rb, a.H / QK, a.xq, xrows, a.xq_stride,
-                      mat * 64 + rh * 32, acc);
+        pf_gemm<T, NTN, 2 * R>(s0, s1, g + f0 * rb, R, u + f0 * rb, rb, a.H / QK, a.xq, xrows, a.xq_stride,
+                               mat * R + rh * 16 * NTN, acc);
     };
-    if (sh) {
-        if constexpr (TS == T_Q4_0) run(std::integral_constant<int, T_Q4_0>{});
+    if (TE == TS || !sh) {   // one instance of the K loop when both types agree
+        if constexpr (TE == T_Q4_0) run(std::integral_constant<int, T_Q4_0>{});
         else run(std::integral_constant<int, T_Q8_0>{});
     } else {
-        if constexpr (TE == T_Q4_0) run(std::integral_constant<int, T_Q4_0>{});
+        if constexpr (TS == T_Q4_0) run(std::integral_constant<int, T_Q4_0>{});
         else run(std::integral_constant<int, T_Q8_0>{});
     }
     {
         const int lane = tid & 63, q = lane >> 4, c = lane & 15;
 #pragma unroll
-        for (int nn = 0; nn < 2; nn++)
+        for (int nn = 0; nn < NTN; nn++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) gu[mat][4 * q + i][rh * 32 + 16 * nn + c] = acc[nn][i];
+            for (int i = 0; i < 4; i++) gu[mat][4 * q + i][rh * 16 * NTN + 16 * nn + c] = acc[nn][i];
     }
     __syncthreads();
-    // Q8_1(h) of the two 32-row blocks for each pair: one half-wave per (pair, block)
-    for (int qq = tid >> 5; qq < 2 * n; qq += PF_THREADS / 32) {
-        const int m = qq >> 1, blk = qq & 1, i = tid & 31;
+    // Q8_1(h) of the R/32 32-row blocks for each pair: one half-wave per (pair, block)
+    constexpr int NBH = R / QK;
+    for (int qq = tid >> 5; qq < NBH * n; qq += PF_THREADS / 32) {
+        const int m = qq / NBH, blk = qq % NBH, i = tid & 31;
         const float xi = det_silu(gu[0][m][blk * 32 + i]) * gu[1][m][blk * 32 + i];
         const float amax = bfly32_max(__builtin_fabsf(xi)), sum = bfly32_sum(xi);
         const float d = amax / 127.0f;
@@ -407,10 +490,7 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_gate_up(PfArgs a) {
 template <int TE, int TS>
 __global__ __launch_bounds__(PF_THREADS) void k_pf_down(PfArgs a) {
     constexpr int WS = pf_wst<TE>(128) > pf_wst<TS>(128) ? pf_wst<TE>(128) : pf_wst<TS>(128);
-    __shared__ __attribute__((aligned(16))) uint8_t wl[2 * WS];
-    __shared__ __attribute__((aligned(16))) uint8_t xl[2 * PF_XST];
-    __shared__ __attribute__((aligned(16))) float xd[2 * PF_TILE * PF_CHUNK];
-    __shared__ __attribute__((aligned(16))) int xs8[2 * PF_TILE * PF_CHUNK];
+    PF_STAGE_ARRAYS(WS);
     __shared__ int prs[PF_TILE];
     const int ti = blockIdx.y;
     if (ti >= *a.ntiles) return;
@@ -425,14 +505,13 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_down(PfArgs a) {
         constexpr int T = decltype(tag)::value;
         const int64_t rb = row_bytes(T, a.F);
         const uint8_t* d = sh ? a.sh_down : a.down + (int64_t)e * a.sd;
-        pf_gemm<T, 2>(wl, xl, xd, xs8, d + r0 * rb, 128, d, 0, rb, a.F / QK, a.hq, prs, a.hq_stride, wave * 32,
-                      acc);
+        pf_gemm<T, 2, 128>(s0, s1, d + r0 * rb, 128, d, rb, a.F / QK, a.hq, prs, a.hq_stride, wave * 32, acc);
     };
-    if (sh) {
-        if constexpr (TS == T_Q4_0) run(std::integral_constant<int, T_Q4_0>{});
+    if (TE == TS || !sh) {   // one instance of the K loop when both types agree
+        if constexpr (TE == T_Q4_0) run(std::integral_constant<int, T_Q4_0>{});
         else run(std::integral_constant<int, T_Q8_0>{});
     } else {
-        if constexpr (TE == T_Q4_0) run(std::integral_constant<int, T_Q4_0>{});
+        if constexpr (TS == T_Q4_0) run(std::integral_constant<int, T_Q4_0>{});
         else run(std::integral_constant<int, T_Q8_0>{});
     }
     const int lane = tid & 63, q = lane >> 4, c = lane & 15;
@@ -500,7 +579,7 @@ static void launch_pf(const PfArgs& a, const PfPlan& p, hipStream_t s) {
     launch_quantize_q8_1(a.x, a.xq, a.H, p.xq_stride / Q8_1_BYTES * QK, a.T, s);
     hipLaunchKernelGGL(k_pf_topk, dim3(a.T), dim3(64), 0, s, a);
     hipLaunchKernelGGL(k_pf_plan, dim3(1), dim3(1024), 0, s, a);
-    hipLaunchKernelGGL((k_pf_gate_up<TE, TS>), dim3(a.F / 64, p.max_tiles), dim3(PF_THREADS), 0, s, a);
+    hipLaunchKernelGGL((k_pf_gate_up<TE, TS>), dim3(a.F / PF_GU_ROWS, p.max_tiles), dim3(PF_THREADS), 0, s, a);
     hipLaunchKernelGGL((k_pf_down<TE, TS>), dim3(a.H / 128, p.max_tiles), dim3(PF_THREADS), 0, s, a);
     hipLaunchKernelGGL(k_pf_combine, dim3((a.H + 255) / 256, a.T), dim3(256), 0, s, a);
 }
