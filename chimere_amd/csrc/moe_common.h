@@ -139,6 +139,46 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ logits, int 
 #endif
     int my_idx = 0;
     float my_w = 0.0f;
+    if constexpr (NV == 4) {
+        // Each lane's keys sorted once, descending, equal keys by index (the
+        // order (key, -index) is total, so any sorting network gives it).
+        // A round is then a maximum over the lanes' heads: the winner is the
+        // lane whose head holds it (the lowest index among several such
+        // lanes: a slow path for exact ties), which then pops its head.
+        uint32_t kk[4] = {key[0], key[1], key[2], key[3]};
+        int sl[4] = {0, 1, 2, 3};
+        auto cx = [&](int a, int b) {
+            const bool sw = kk[b] > kk[a] || (kk[b] == kk[a] && sl[b] < sl[a]);
+            const uint32_t ka = kk[a], kb = kk[b];
+            const int sa = sl[a], sb = sl[b];
+            kk[a] = sw ? kb : ka;
+            kk[b] = sw ? ka : kb;
+            sl[a] = sw ? sb : sa;
+            sl[b] = sw ? sa : sb;
+        };
+        cx(0, 1);
+        cx(2, 3);
+        cx(0, 2);
+        cx(1, 3);
+        cx(1, 2);
+        for (int k = 0; k < K; k++) {
+            const int m = wave_max_nonneg((int)kk[0]);
+            const uint64_t bm = __ballot(kk[0] == (uint32_t)m);
+            int wl;
+            if (__builtin_popcountll(bm) == 1) {
+                wl = __builtin_ctzll(bm);
+            } else {
+                const int cand = kk[0] == (uint32_t)m ? 0x7FFFFFFF - (lane + 64 * sl[0]) : 0;
+                wl = (0x7FFFFFFF - wave_max_nonneg(cand)) & 63;
+            }
+            const int win = __builtin_amdgcn_readlane(lane + 64 * sl[0], wl);
+            if (lane == wl) {
+                kk[0] = kk[1]; kk[1] = kk[2]; kk[2] = kk[3]; kk[3] = 0u;
+                sl[0] = sl[1]; sl[1] = sl[2]; sl[2] = sl[3];
+            }
+            if (lane == k) { my_idx = win; my_w = __builtin_bit_cast(float, (uint32_t)m - 1u); }
+        }
+    } else
     for (int k = 0; k < K; k++) {
         int m = (int)key[0];
 #pragma unroll
