@@ -203,14 +203,37 @@ __global__ __launch_bounds__(1024) void k_pf_plan(PfArgs a) {
 // at -8 * sum(q_x) of the pair's block, which makes the result
 // sum((nib - 8) * q_x).
 
+// bytes of a PF_CHUNK-block chunk of a row (IQ3_S: one 110-byte superblock)
 template <int T>
-constexpr int pf_row_chunk_bytes() { return PF_CHUNK * QTraits<T>::BYTES; }
+constexpr int pf_row_chunk_bytes() {
+    return QTraits<T>::ELEMS == 256 ? PF_CHUNK / 8 * QTraits<T>::BYTES : PF_CHUNK * QTraits<T>::BYTES;
+}
 
-// 8 weight values of block b of an LDS row as int8, and f32(d)
+__constant__ uint32_t c_iq3s_grid_pf[512] = CHIMERE_IQ3S_GRID_INIT;
+
+// 8 weight values of block b of an LDS row as int8, and f32(d); IQ3_S also
+// sets *mult = 1 + 2 * (4-bit scale of sub-block b), the factor of its exact
+// block dot (cs/src/kernels/iq3s_gemv.rs:292-352)
 template <int T>
-__device__ __forceinline__ long pf_b_frag(const uint8_t* row, int b, int q, uint32_t* dw) {
+__device__ __forceinline__ long pf_b_frag(const uint8_t* row, int b, int q, uint32_t* dw, int* mult,
+                                          const uint32_t* grid) {
     uint32_t lo, hi;
-    if constexpr (T == T_Q4_0) {
+    if constexpr (T == T_IQ3_S) {
+        // sub-block b of the superblock [f16 d][qs 64][qh 8][signs 32][scales 4];
+        // lane group q holds elements 8q .. 8q+7: grid entries qs[8b+2q] and
+        // qs[8b+2q+1] with high bits 2q and 2q+1 of qh[b], negated per byte by
+        // bits 0..3 / 4..7 of signs[4b+q]
+        *dw = lds_u16(row, 0);
+        const uint32_t qs = lds_u16(row, 2 + 8 * b + 2 * q);
+        const uint32_t qh = row[66 + b] >> (2 * q);
+        const uint32_t i0 = (qs & 0xFFu) | ((qh & 1u) << 8), i1 = (qs >> 8) | ((qh & 2u) << 7);
+        const uint32_t sg = row[74 + 4 * b + q];
+        const uint32_t b0 = nib_bits(sg & 0xFu), b1 = nib_bits(sg >> 4);
+        const uint32_t m0 = __builtin_amdgcn_perm(0u, 0u, b0 | 0x0C0C0C0Cu), m1 = __builtin_amdgcn_perm(0u, 0u, b1 | 0x0C0C0C0Cu);
+        lo = (grid[i0] ^ m0) + b0;
+        hi = (grid[i1] ^ m1) + b1;
+        *mult = 1 + 2 * (int)((row[106 + (b >> 1)] >> (4 * (b & 1))) & 0xFu);
+    } else if constexpr (T == T_Q4_0) {
         // bytes o .. o+7 of the row hold the 16 nibbles (low nibbles for
         // q < 2, high for q >= 2); o is 2 mod 4 for even b, 0 mod 4 for odd
         // b, so three aligned dwords and one funnel shift per result dword
@@ -228,6 +251,8 @@ __device__ __forceinline__ long pf_b_frag(const uint8_t* row, int b, int q, uint
         lo = lds_u32(row, off + 2 + 8 * q);
         hi = lds_u32(row, off + 6 + 8 * q);
     }
+    (void)mult;
+    (void)grid;
     return (long)(((uint64_t)hi << 32) | lo);
 }
 
@@ -271,12 +296,14 @@ __device__ __forceinline__ void pf_issue(uint8_t* wl, const uint8_t* w, int64_t 
 // row 16n + l%16), updated per block as fmaf(f32(d_w)*f32(d_x), sumi, acc).
 template <int T, int NTN>
 __device__ __forceinline__ void pf_mma_chunk(const uint8_t* xl, const float* xd, const int* xs8,
-                                             const uint8_t* wrows, int cbytes, int nb, float (&acc)[NTN][4]) {
+                                             const uint8_t* wrows, int cbytes, int nb, const uint32_t* grid,
+                                             float (&acc)[NTN][4]) {
     const int lane = threadIdx.x & 63, q = lane >> 4, c = lane & 15;
     // two blocks in flight: block b's matrix products are issued before block
     // b-1's results are rescaled, so the MFMA latency overlaps VALU work
     v4i r[NTN], rp[NTN];
     float dw[NTN], dwp[NTN];
+    int mu[NTN], mup[NTN];   // IQ3_S sub-block factors
     float4 dxp;
     for (int b = 0; b <= nb; b++) {
         float4 dx;
@@ -289,12 +316,18 @@ __device__ __forceinline__ void pf_mma_chunk(const uint8_t* xl, const float* xd,
 #pragma unroll
             for (int n = 0; n < NTN; n++) {
                 uint32_t dwb;
-                const long bf = pf_b_frag<T>(wrows + (16 * n + c) * cbytes, b, q, &dwb);
+                const long bf = pf_b_frag<T>(wrows + (16 * n + c) * cbytes, b, q, &dwb, &mu[n], grid);
                 dw[n] = h2f(dwb);
                 r[n] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bf, c0, 0, 0, 0);
             }
         }
         if (b > 0) {
+            if constexpr (T == T_IQ3_S) {
+#pragma unroll
+                for (int n = 0; n < NTN; n++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) rp[n][i] = __mul24(rp[n][i], mup[n]);   // |.| < 2^21
+            }
 #pragma unroll
             for (int n = 0; n < NTN; n++) {
                 acc[n][0] = __builtin_fmaf(dwp[n] * dxp.x, (float)rp[n][0], acc[n][0]);
@@ -304,7 +337,7 @@ __device__ __forceinline__ void pf_mma_chunk(const uint8_t* xl, const float* xd,
             }
         }
 #pragma unroll
-        for (int n = 0; n < NTN; n++) { rp[n] = r[n]; dwp[n] = dw[n]; }
+        for (int n = 0; n < NTN; n++) { rp[n] = r[n]; dwp[n] = dw[n]; mup[n] = mu[n]; }
         dxp = dx;
     }
 }
@@ -332,9 +365,10 @@ struct PfStage {
 template <int T, int NTN, int NR, bool AL>
 __device__ __forceinline__ void pf_gemm_k(const PfStage& s0, const PfStage& s1, const uint8_t* w0, int n0,
                                           const uint8_t* w1, int64_t rb, int nbk, const uint8_t* xsrc,
-                                          const int* xrows, int64_t xstride, int wrow0, float (&acc)[NTN][4]) {
+                                          const int* xrows, int64_t xstride, int wrow0, const uint32_t* grid,
+                                          float (&acc)[NTN][4]) {
     constexpr int CB = pf_row_chunk_bytes<T>();
-    static_assert(CB % 16 == 0, "chunk rows in 16-byte pieces");
+    static_assert(!AL || CB % 16 == 0, "chunk rows in 16-byte pieces");
     constexpr int PCB = CB / 16, PER = 36 * PF_CHUNK / 16;
     constexpr int TW = NR * PCB, TWP = (TW + 63) & ~63, TOT = TWP + PF_TILE * PER;
 #pragma unroll
@@ -352,7 +386,7 @@ __device__ __forceinline__ void pf_gemm_k(const PfStage& s0, const PfStage& s1, 
             __syncthreads();
             pf_xmeta(s0.x, s0.xd, s0.xs);
             __syncthreads();
-            pf_mma_chunk<T, NTN>(s0.x, s0.xd, s0.xs, s0.w + wrow0 * CB, CB, PF_CHUNK, acc);
+            pf_mma_chunk<T, NTN>(s0.x, s0.xd, s0.xs, s0.w + wrow0 * CB, CB, PF_CHUNK, grid, acc);
             __syncthreads();
         }
     } else {
@@ -383,7 +417,7 @@ __device__ __forceinline__ void pf_gemm_k(const PfStage& s0, const PfStage& s1, 
             pf_xmeta(cur.x, cur.xd, cur.xs);
             if (c + 1 < nc) issue(c + 1, nxt);
             lds_barrier();   // metadata written
-            pf_mma_chunk<T, NTN>(cur.x, cur.xd, cur.xs, cur.w + wrow0 * CB, CB, PF_CHUNK, acc);
+            pf_mma_chunk<T, NTN>(cur.x, cur.xd, cur.xs, cur.w + wrow0 * CB, CB, PF_CHUNK, grid, acc);
         };
         issue(0, s0);
         for (int c = 0; c < nc; c += 2) {
@@ -398,10 +432,18 @@ __device__ __forceinline__ void pf_gemm_k(const PfStage& s0, const PfStage& s1, 
 template <int T, int NTN, int NR>
 __device__ __forceinline__ void pf_gemm(const PfStage& s0, const PfStage& s1, const uint8_t* w0, int n0,
                                         const uint8_t* w1, int64_t rb, int nbk, const uint8_t* xsrc,
-                                        const int* xrows, int64_t xstride, int wrow0, float (&acc)[NTN][4]) {
-    const bool al16 = (((uintptr_t)w0 | (uintptr_t)w1 | (uintptr_t)rb | (uintptr_t)xsrc | (uintptr_t)xstride) & 15) == 0;
-    if (al16) pf_gemm_k<T, NTN, NR, true>(s0, s1, w0, n0, w1, rb, nbk, xsrc, xrows, xstride, wrow0, acc);
-    else pf_gemm_k<T, NTN, NR, false>(s0, s1, w0, n0, w1, rb, nbk, xsrc, xrows, xstride, wrow0, acc);
+                                        const int* xrows, int64_t xstride, int wrow0, const uint32_t* grid,
+                                        float (&acc)[NTN][4]) {
+    // the two-stage path copies 16-byte pieces of the chunk rows: not for
+    // IQ3_S (110-byte superblock chunks)
+    const bool al16 = pf_row_chunk_bytes<T>() % 16 == 0 &&
+                      (((uintptr_t)w0 | (uintptr_t)w1 | (uintptr_t)rb | (uintptr_t)xsrc | (uintptr_t)xstride) & 15) == 0;
+    if constexpr (pf_row_chunk_bytes<T>() % 16 == 0)
+        if (al16) {
+            pf_gemm_k<T, NTN, NR, true>(s0, s1, w0, n0, w1, rb, nbk, xsrc, xrows, xstride, wrow0, grid, acc);
+            return;
+        }
+    pf_gemm_k<T, NTN, NR, false>(s0, s1, w0, n0, w1, rb, nbk, xsrc, xrows, xstride, wrow0, grid, acc);
 }
 
 template <int T>
@@ -431,6 +473,7 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_gate_up(PfArgs a) {
     constexpr int WS = pf_wst<TE>(2 * R) > pf_wst<TS>(2 * R) ? pf_wst<TE>(2 * R) : pf_wst<TS>(2 * R);
     PF_STAGE_ARRAYS(WS);
     __shared__ int prs[PF_TILE], xrows[PF_TILE];
+    __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
     // gate / up results per (pair, row), in stage 0's weight buffer once the K loop is done
     static_assert(2 * PF_TILE * (R + 1) * sizeof(float) <= WS, "gate/up results fit a stage");
     float(*gu)[PF_TILE][R + 1] = reinterpret_cast<float(*)[PF_TILE][R + 1]>(wl0);
@@ -443,6 +486,8 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_gate_up(PfArgs a) {
         prs[tid] = p;
         xrows[tid] = p < TK ? p / a.K : p - TK;
     }
+    if constexpr (TE == T_IQ3_S || TS == T_IQ3_S)
+        for (int i = tid; i < 512; i += PF_THREADS) grid[i] = c_iq3s_grid_pf[i];
     __syncthreads();
     const bool sh = e == a.E;
     const int f0 = blockIdx.x * R;
@@ -454,15 +499,11 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_gate_up(PfArgs a) {
         const uint8_t* g = sh ? a.sh_gate : a.gate + (int64_t)e * a.sg;
         const uint8_t* u = sh ? a.sh_up : a.up + (int64_t)e * a.su;
         pf_gemm<T, NTN, 2 * R>(s0, s1, g + f0 * rb, R, u + f0 * rb, rb, a.H / QK, a.xq, xrows, a.xq_stride,
-                               mat * R + rh * 16 * NTN, acc);
+                               mat * R + rh * 16 * NTN, grid, acc);
     };
-    if (TE == TS || !sh) {   // one instance of the K loop when both types agree
-        if constexpr (TE == T_Q4_0) run(std::integral_constant<int, T_Q4_0>{});
-        else run(std::integral_constant<int, T_Q8_0>{});
-    } else {
-        if constexpr (TS == T_Q4_0) run(std::integral_constant<int, T_Q4_0>{});
-        else run(std::integral_constant<int, T_Q8_0>{});
-    }
+    if constexpr (TE == TS) run(std::integral_constant<int, TE>{});   // one instance of the K loop
+    else if (!sh) run(std::integral_constant<int, TE>{});
+    else run(std::integral_constant<int, TS>{});
     {
         const int lane = tid & 63, q = lane >> 4, c = lane & 15;
 #pragma unroll
@@ -492,11 +533,14 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_down(PfArgs a) {
     constexpr int WS = pf_wst<TE>(128) > pf_wst<TS>(128) ? pf_wst<TE>(128) : pf_wst<TS>(128);
     PF_STAGE_ARRAYS(WS);
     __shared__ int prs[PF_TILE];
+    __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
     const int ti = blockIdx.y;
     if (ti >= *a.ntiles) return;
     const int e = a.tiles[ti * 3], start = a.tiles[ti * 3 + 1], n = a.tiles[ti * 3 + 2];
     const int tid = threadIdx.x;
     if (tid < PF_TILE) prs[tid] = a.spairs[start + min(tid, n - 1)];
+    if constexpr (TE == T_IQ3_S || TS == T_IQ3_S)
+        for (int i = tid; i < 512; i += PF_THREADS) grid[i] = c_iq3s_grid_pf[i];
     __syncthreads();
     const bool sh = e == a.E;
     const int r0 = blockIdx.x * 128, wave = tid >> 6;
@@ -505,15 +549,11 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_down(PfArgs a) {
         constexpr int T = decltype(tag)::value;
         const int64_t rb = row_bytes(T, a.F);
         const uint8_t* d = sh ? a.sh_down : a.down + (int64_t)e * a.sd;
-        pf_gemm<T, 2, 128>(s0, s1, d + r0 * rb, 128, d, rb, a.F / QK, a.hq, prs, a.hq_stride, wave * 32, acc);
+        pf_gemm<T, 2, 128>(s0, s1, d + r0 * rb, 128, d, rb, a.F / QK, a.hq, prs, a.hq_stride, wave * 32, grid, acc);
     };
-    if (TE == TS || !sh) {   // one instance of the K loop when both types agree
-        if constexpr (TE == T_Q4_0) run(std::integral_constant<int, T_Q4_0>{});
-        else run(std::integral_constant<int, T_Q8_0>{});
-    } else {
-        if constexpr (TS == T_Q4_0) run(std::integral_constant<int, T_Q4_0>{});
-        else run(std::integral_constant<int, T_Q8_0>{});
-    }
+    if constexpr (TE == TS) run(std::integral_constant<int, TE>{});   // one instance of the K loop
+    else if (!sh) run(std::integral_constant<int, TE>{});
+    else run(std::integral_constant<int, TS>{});
     const int lane = tid & 63, q = lane >> 4, c = lane & 15;
 #pragma unroll
     for (int nn = 0; nn < 2; nn++)
@@ -605,9 +645,9 @@ void chimere_moe_prefill(const chimere_moe_layer* L, const float* x, float* out,
     CHIMERE_REQUIRE(E >= 1 && E <= MAX_E && K >= 1 && K <= MAX_K && K <= E, CHIMERE_ERR_ARG,
                     "moe_prefill: n_experts=%d top_k=%d out of range", E, K);
     const bool has_sh = L->shared_type >= 0;
-    CHIMERE_REQUIRE((L->expert_type == T_Q4_0 || L->expert_type == T_Q8_0) &&
-                        (!has_sh || L->shared_type == T_Q4_0 || L->shared_type == T_Q8_0),
-                    CHIMERE_ERR_ARG, "moe_prefill: Q4_0 / Q8_0 weights only (expert %d, shared %d)", L->expert_type,
+    auto pf_type = [](int t) { return t == T_Q4_0 || t == T_Q8_0 || t == T_IQ3_S; };
+    CHIMERE_REQUIRE(pf_type(L->expert_type) && (!has_sh || pf_type(L->shared_type)), CHIMERE_ERR_ARG,
+                    "moe_prefill: Q4_0 / Q8_0 / IQ3_S weights only (expert %d, shared %d)", L->expert_type,
                     L->shared_type);
     CHIMERE_REQUIRE(!has_sh || (L->sh_gate && L->sh_up && L->sh_down), CHIMERE_ERR_ARG,
                     "moe_prefill: shared expert incomplete");
@@ -639,10 +679,15 @@ void chimere_moe_prefill(const chimere_moe_layer* L, const float* x, float* out,
     a.hq = w + p.hq; a.dn = (float*)(w + p.dn);
     a.xq_stride = p.xq_stride; a.hq_stride = p.hq_stride; a.max_tiles = p.max_tiles;
     const int te = L->expert_type, ts = has_sh ? L->shared_type : te;
-    if (te == T_Q4_0 && ts == T_Q4_0) launch_pf<T_Q4_0, T_Q4_0>(a, p, stream);
-    else if (te == T_Q4_0) launch_pf<T_Q4_0, T_Q8_0>(a, p, stream);
-    else if (ts == T_Q4_0) launch_pf<T_Q8_0, T_Q4_0>(a, p, stream);
-    else launch_pf<T_Q8_0, T_Q8_0>(a, p, stream);
+    auto with_ts = [&](auto te_tag) {
+        constexpr int TE = decltype(te_tag)::value;
+        if (ts == T_Q4_0) launch_pf<TE, T_Q4_0>(a, p, stream);
+        else if (ts == T_Q8_0) launch_pf<TE, T_Q8_0>(a, p, stream);
+        else launch_pf<TE, T_IQ3_S>(a, p, stream);
+    };
+    if (te == T_Q4_0) with_ts(std::integral_constant<int, T_Q4_0>{});
+    else if (te == T_Q8_0) with_ts(std::integral_constant<int, T_Q8_0>{});
+    else with_ts(std::integral_constant<int, T_IQ3_S>{});
     check_launch("moe_prefill");
 }
 

@@ -39,6 +39,10 @@ def prefill_check(layer, x, sample=None):
     (O.Q4_0, O.Q8_0, False, 2, 32, 5),
     (O.Q8_0, O.Q4_0, True, 8, 8, 9),        # K == E
     (O.Q4_0, None, False, 1, 4, 33),        # no shared expert, top-1
+    (O.IQ3_S, O.IQ3_S, True, 8, 64, 37),    # IQ3_S: one superblock per K chunk, unaligned staging
+    (O.IQ3_S, O.Q8_0, False, 4, 16, 70),    # the IQ3_S model layers' Q8_0 shared expert
+    (O.IQ3_S, O.Q4_0, True, 8, 8, 9),
+    (O.Q4_0, O.IQ3_S, False, 2, 32, 5),
 ])
 def test_prefill_small(dev, et, st, gate_vec, K, E, T):
     print(f"prefill et={et} st={st} gate={gate_vec} K={K} E={E} T={T}", flush=True)
@@ -69,6 +73,16 @@ def test_prefill_config5_512(dev):
     dec = host(layer.forward(x[:8]))
     for m in range(8):
         assert np.linalg.norm(dec[m] - og[m]) <= 2e-3 * np.linalg.norm(og[m])
+
+
+def test_prefill_iq3s_full_shape(dev):
+    """IQ3_S experts at the model's shape (H=2048, F=512, E=256, top-8) with the
+    Q8_0 shared expert, 96 tokens, uniform and Zipf(1.1) routing: every token
+    against the oracle."""
+    for zipf in (False, True):
+        layer = build(dev, 31 + zipf, et=O.IQ3_S, st=O.Q8_0, zipf=zipf)
+        g = torch.Generator(device=dev).manual_seed(77)
+        prefill_check(layer, torch.randn(96, 2048, generator=g, device=dev))
 
 
 def test_prefill_repeat_and_zero(dev):

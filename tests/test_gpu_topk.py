@@ -1,0 +1,47 @@
+"""GPU parity of the standalone softmax + top-k (chimere_topk_softmax,
+topk_softmax.rs:113 / cs/kernels/chimere_kernels.cu:1150-1223) against the
+CPU oracle, through the C ABI: indices and weights bit-exact, including
+exact probability ties that straddle the top-k boundary (lowest index
+first, as the reference's strict '>' arg-max rounds give)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from chimere_amd import ggml_gpu as G
+
+pytestmark = pytest.mark.gpu
+
+
+def _cases(E, seed):
+    rng = np.random.default_rng(seed)
+    yield rng.standard_normal(E).astype(np.float32)                     # distinct
+    yield np.zeros(E, np.float32)                                       # all tied
+    v = rng.standard_normal(E // 2).astype(np.float32)
+    yield np.repeat(v, 2)                                               # pairs tied
+    yield np.round(rng.standard_normal(E) * 2).astype(np.float32)       # few distinct values
+    v = np.full(E, -1.0, np.float32)
+    v[rng.choice(E, 3, replace=False)] = 2.0                            # 3 winners, then a tie of E-3
+    yield v
+    v = rng.standard_normal(E).astype(np.float32)
+    v[::7] = v.max()                                                    # many copies of the maximum
+    yield v
+    yield (rng.standard_normal(E) * 40).astype(np.float32)              # probabilities underflow to 0
+
+
+@pytest.mark.parametrize("E,K", [(256, 8), (256, 1), (256, 16), (200, 8), (64, 8), (8, 8), (512, 16), (1024, 8)])
+def test_topk_softmax_ties(E, K):
+    print(f"topk E={E} K={K}", flush=True)
+    rows = list(_cases(E, E * 100 + K))
+    logits = np.stack(rows)
+    n = len(rows)
+    dl = torch.from_numpy(logits).cuda()
+    ids = torch.empty(n, K, dtype=torch.int32, device="cuda")
+    wts = torch.empty(n, K, dtype=torch.float32, device="cuda")
+    G.gpu_topk_softmax(dl, ids, wts, E, K, ntok=n)
+    torch.cuda.synchronize()
+    gi, gw = ids.cpu().numpy(), wts.cpu().numpy()
+    for t in range(n):
+        oi, ow = O.topk_softmax(logits[t], K)
+        assert (gi[t] == oi).all(), (t, gi[t], oi)
+        assert (gw[t].view(np.uint32) == ow.view(np.uint32)).all(), (t, gw[t], ow)
