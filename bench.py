@@ -306,6 +306,25 @@ def main():
         del lp
         torch.cuda.empty_cache()
 
+        # the same chunk with IQ3_S experts (the reference model's quantization),
+        # IQ3_S or Q8_0 shared expert
+        for tag, st in (("prefill_iq3s_512", IQ3_S), ("prefill_iq3s_q8_0_shared_512", Q8_0)):
+            lp = [make_layer(310 + r, IQ3_S, st) for r in range(2)]
+            for lyr in lp:
+                lyr.prefill(xp, out=op, ids=ids, wts=torch.empty(T, K, device=dev))
+            ue = len(set(ids.cpu().numpy().reshape(-1).tolist()))
+            fns = [(lambda i=i: lp[i % 2].prefill(xp, out=op)) for i in range(16)]
+            tp, _ = graph_time(fns)
+            upf = tp / 16
+            eb = 2 * F * row_bytes(IQ3_S, H) + H * row_bytes(IQ3_S, F)
+            sb = 2 * F * row_bytes(st, H) + H * row_bytes(st, F)
+            pbytes = ue * eb + sb + E * H * 4 + 2 * T * H * 4
+            extra[tag] = {"us_per_chunk": round(upf * 1e6, 2), "tokens_per_s": round(T / upf, 1),
+                          "unique_experts": ue, "GBs_unique_weight_bytes": round(pbytes / upf / 1e9, 1),
+                          "int8_TOPs": round(ops / upf / 1e12, 2)}
+            del lp
+            torch.cuda.empty_cache()
+
         # ---------------- config 2: Q4_0 head 151936 x 2048, three copies rotated
         V = 151936
         g = torch.Generator(device=dev).manual_seed(2)

@@ -209,6 +209,12 @@ constexpr int pf_row_chunk_bytes() {
     return QTraits<T>::ELEMS == 256 ? PF_CHUNK / 8 * QTraits<T>::BYTES : PF_CHUNK * QTraits<T>::BYTES;
 }
 
+// LDS row stride of a staged chunk on the two-stage path: the chunk bytes,
+// or for IQ3_S the 16-byte aligned span that holds the superblock (it starts
+// at (110 c) % 16 inside the span: at most 14 + 110 bytes)
+template <int T>
+constexpr int pf_lds_row() { return T == T_IQ3_S ? 128 : pf_row_chunk_bytes<T>(); }
+
 __constant__ uint32_t c_iq3s_grid_pf[512] = CHIMERE_IQ3S_GRID_INIT;
 
 // 8 weight values of block b of an LDS row as int8, and f32(d); IQ3_S also
@@ -367,9 +373,9 @@ __device__ __forceinline__ void pf_gemm_k(const PfStage& s0, const PfStage& s1, 
                                           const uint8_t* w1, int64_t rb, int nbk, const uint8_t* xsrc,
                                           const int* xrows, int64_t xstride, int wrow0, const uint32_t* grid,
                                           float (&acc)[NTN][4]) {
-    constexpr int CB = pf_row_chunk_bytes<T>();
-    static_assert(!AL || CB % 16 == 0, "chunk rows in 16-byte pieces");
-    constexpr int PCB = CB / 16, PER = 36 * PF_CHUNK / 16;
+    constexpr int CB = pf_row_chunk_bytes<T>(), CBL = pf_lds_row<T>();
+    static_assert(!AL || CBL % 16 == 0, "chunk rows in 16-byte pieces");
+    constexpr int PCB = CBL / 16, PER = 36 * PF_CHUNK / 16;
     constexpr int TW = NR * PCB, TWP = (TW + 63) & ~63, TOT = TWP + PF_TILE * PER;
 #pragma unroll
     for (int n = 0; n < NTN; n++)
@@ -391,13 +397,15 @@ __device__ __forceinline__ void pf_gemm_k(const PfStage& s0, const PfStage& s1, 
         }
     } else {
         auto issue = [&](int c, const PfStage& s) {
-            const int64_t goff = (int64_t)c * CB, xoff = (int64_t)c * PF_CHUNK * 36;
+            const int64_t goff = (int64_t)c * CB & ~(int64_t)15, xoff = (int64_t)c * PF_CHUNK * 36;
             for (int c0 = wave * 64; c0 < TOT; c0 += PF_THREADS) {
                 const int cc = c0 + lane;
                 if (c0 < TWP) {
                     if (cc < TW) {
                         const int row = cc / PCB, col = cc - row * PCB;
-                        const uint8_t* src = (row < n0 ? w0 + row * rb : w1 + (row - n0) * rb) + goff + col * 16;
+                        int64_t o = goff + col * 16;
+                        if constexpr (CBL != CB) o = o < rb - 16 ? o : rb - 16;   // span pieces stay in the row
+                        const uint8_t* src = (row < n0 ? w0 + row * rb : w1 + (row - n0) * rb) + o;
                         copy16_lds_untracked(src, s.w + c0 * 16);
                     }
                 } else {
@@ -417,7 +425,7 @@ __device__ __forceinline__ void pf_gemm_k(const PfStage& s0, const PfStage& s1, 
             pf_xmeta(cur.x, cur.xd, cur.xs);
             if (c + 1 < nc) issue(c + 1, nxt);
             lds_barrier();   // metadata written
-            pf_mma_chunk<T, NTN>(cur.x, cur.xd, cur.xs, cur.w + wrow0 * CB, CB, PF_CHUNK, grid, acc);
+            pf_mma_chunk<T, NTN>(cur.x, cur.xd, cur.xs, cur.w + wrow0 * CBL + (c * CB & 15), CBL, PF_CHUNK, grid, acc);
         };
         issue(0, s0);
         for (int c = 0; c < nc; c += 2) {
@@ -429,16 +437,16 @@ __device__ __forceinline__ void pf_gemm_k(const PfStage& s0, const PfStage& s1, 
     lds_barrier();   // every wave is done with the stages (callers reuse them)
 }
 
-template <int T, int NTN, int NR>
+// TWO: allow the two-stage path (callers whose rows are never 16-byte aligned
+// pass false, so that the second stage's LDS is not allocated)
+template <int T, int NTN, int NR, bool TWO = true>
 __device__ __forceinline__ void pf_gemm(const PfStage& s0, const PfStage& s1, const uint8_t* w0, int n0,
                                         const uint8_t* w1, int64_t rb, int nbk, const uint8_t* xsrc,
                                         const int* xrows, int64_t xstride, int wrow0, const uint32_t* grid,
                                         float (&acc)[NTN][4]) {
-    // the two-stage path copies 16-byte pieces of the chunk rows: not for
-    // IQ3_S (110-byte superblock chunks)
-    const bool al16 = pf_row_chunk_bytes<T>() % 16 == 0 &&
-                      (((uintptr_t)w0 | (uintptr_t)w1 | (uintptr_t)rb | (uintptr_t)xsrc | (uintptr_t)xstride) & 15) == 0;
-    if constexpr (pf_row_chunk_bytes<T>() % 16 == 0)
+    // the two-stage path copies 16-byte pieces: rows and activations 16-byte aligned
+    const bool al16 = (((uintptr_t)w0 | (uintptr_t)w1 | (uintptr_t)rb | (uintptr_t)xsrc | (uintptr_t)xstride) & 15) == 0;
+    if constexpr (TWO)
         if (al16) {
             pf_gemm_k<T, NTN, NR, true>(s0, s1, w0, n0, w1, rb, nbk, xsrc, xrows, xstride, wrow0, grid, acc);
             return;
@@ -447,7 +455,7 @@ __device__ __forceinline__ void pf_gemm(const PfStage& s0, const PfStage& s1, co
 }
 
 template <int T>
-constexpr int pf_wst(int nrows) { return nrows * pf_row_chunk_bytes<T>() + 16; }
+constexpr int pf_wst(int nrows) { return nrows * pf_lds_row<T>() + 16; }
 constexpr int PF_XST = PF_TILE * PF_CHUNK * 36;
 
 // LDS arrays of the two pipeline stages (separate arrays) and their PfStage
@@ -549,7 +557,10 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_down(PfArgs a) {
         constexpr int T = decltype(tag)::value;
         const int64_t rb = row_bytes(T, a.F);
         const uint8_t* d = sh ? a.sh_down : a.down + (int64_t)e * a.sd;
-        pf_gemm<T, 2, 128>(s0, s1, d + r0 * rb, 128, d, rb, a.F / QK, a.hq, prs, a.hq_stride, wave * 32, grid, acc);
+        // IQ3_S down rows (F / 256 superblocks of 110 bytes) are 16-byte aligned
+        // only when F is a multiple of 2048: one stage
+        pf_gemm<T, 2, 128, T != T_IQ3_S>(s0, s1, d + r0 * rb, 128, d, rb, a.F / QK, a.hq, prs, a.hq_stride, wave * 32,
+                                         grid, acc);
     };
     if constexpr (TE == TS) run(std::integral_constant<int, TE>{});   // one instance of the K loop
     else if (!sh) run(std::integral_constant<int, TE>{});
