@@ -459,12 +459,22 @@ constexpr int pf_wst(int nrows) { return nrows * pf_lds_row<T>() + 16; }
 constexpr int PF_XST = PF_TILE * PF_CHUNK * 36;
 
 // LDS arrays of the two pipeline stages (separate arrays) and their PfStage
-#define PF_STAGE_ARRAYS(WS)                                                                           \
-    __shared__ __attribute__((aligned(16))) uint8_t wl0[WS], wl1[WS];                                 \
+#define PF_STAGE_ARRAYS(WS0, WS1)                                                                     \
+    __shared__ __attribute__((aligned(16))) uint8_t wl0[WS0], wl1[WS1];                               \
     __shared__ __attribute__((aligned(16))) uint8_t xl0[PF_XST], xl1[PF_XST];                         \
     __shared__ __attribute__((aligned(16))) float xd0[PF_TILE * PF_CHUNK], xd1[PF_TILE * PF_CHUNK];   \
     __shared__ __attribute__((aligned(16))) int xs0[PF_TILE * PF_CHUNK], xs1[PF_TILE * PF_CHUNK];     \
     const PfStage s0{wl0, xl0, xd0, xs0}, s1{wl1, xl1, xd1, xs1}
+
+// A Q8_0 shared expert next to narrower expert rows (Q4_0 / IQ3_S experts)
+// runs on one stage, so that the second stage is sized for the experts'
+// chunk rows (two stages of 128 Q8_0 chunk rows leave one work-group per CU)
+template <int TE, int TS>
+constexpr bool pf_sh_one() { return TS == T_Q8_0 && TE != T_Q8_0; }
+template <int TE, int TS>
+constexpr int pf_ws0(int nrows) { return pf_wst<TE>(nrows) > pf_wst<TS>(nrows) ? pf_wst<TE>(nrows) : pf_wst<TS>(nrows); }
+template <int TE, int TS>
+constexpr int pf_ws1(int nrows) { return pf_sh_one<TE, TS>() ? pf_wst<TE>(nrows) : pf_ws0<TE, TS>(nrows); }
 
 // Rows per gate_up work-group: PF_GU_NTN 16-row tiles per wave, half the
 // waves on gate rows and half on the same up rows
@@ -478,8 +488,8 @@ constexpr int PF_GU_ROWS = 32 * PF_GU_NTN;   // gate (and up) rows per work-grou
 template <int TE, int TS>
 __global__ __launch_bounds__(PF_THREADS) void k_pf_gate_up(PfArgs a) {
     constexpr int NTN = PF_GU_NTN, R = PF_GU_ROWS;
-    constexpr int WS = pf_wst<TE>(2 * R) > pf_wst<TS>(2 * R) ? pf_wst<TE>(2 * R) : pf_wst<TS>(2 * R);
-    PF_STAGE_ARRAYS(WS);
+    constexpr int WS = pf_ws0<TE, TS>(2 * R);
+    PF_STAGE_ARRAYS(WS, (pf_ws1<TE, TS>(2 * R)));
     __shared__ int prs[PF_TILE], xrows[PF_TILE];
     __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
     // gate / up results per (pair, row), in stage 0's weight buffer once the K loop is done
@@ -506,8 +516,9 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_gate_up(PfArgs a) {
         const int64_t rb = row_bytes(T, a.H);
         const uint8_t* g = sh ? a.sh_gate : a.gate + (int64_t)e * a.sg;
         const uint8_t* u = sh ? a.sh_up : a.up + (int64_t)e * a.su;
-        pf_gemm<T, NTN, 2 * R>(s0, s1, g + f0 * rb, R, u + f0 * rb, rb, a.H / QK, a.xq, xrows, a.xq_stride,
-                               mat * R + rh * 16 * NTN, grid, acc);
+        pf_gemm<T, NTN, 2 * R, !(T == TS && pf_sh_one<TE, TS>())>(s0, s1, g + f0 * rb, R, u + f0 * rb, rb, a.H / QK,
+                                                                 a.xq, xrows, a.xq_stride, mat * R + rh * 16 * NTN,
+                                                                 grid, acc);
     };
     if constexpr (TE == TS) run(std::integral_constant<int, TE>{});   // one instance of the K loop
     else if (!sh) run(std::integral_constant<int, TE>{});
@@ -538,8 +549,7 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_gate_up(PfArgs a) {
 // 16-row tiles) for the tile's 16 pairs; K = F.
 template <int TE, int TS>
 __global__ __launch_bounds__(PF_THREADS) void k_pf_down(PfArgs a) {
-    constexpr int WS = pf_wst<TE>(128) > pf_wst<TS>(128) ? pf_wst<TE>(128) : pf_wst<TS>(128);
-    PF_STAGE_ARRAYS(WS);
+    PF_STAGE_ARRAYS((pf_ws0<TE, TS>(128)), (pf_ws1<TE, TS>(128)));
     __shared__ int prs[PF_TILE];
     __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
     const int ti = blockIdx.y;
@@ -559,8 +569,9 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_down(PfArgs a) {
         const uint8_t* d = sh ? a.sh_down : a.down + (int64_t)e * a.sd;
         // IQ3_S down rows (F / 256 superblocks of 110 bytes) are 16-byte aligned
         // only when F is a multiple of 2048: one stage
-        pf_gemm<T, 2, 128, T != T_IQ3_S>(s0, s1, d + r0 * rb, 128, d, rb, a.F / QK, a.hq, prs, a.hq_stride, wave * 32,
-                                         grid, acc);
+        constexpr bool two = T != T_IQ3_S && !(T == TS && pf_sh_one<TE, TS>());
+        pf_gemm<T, 2, 128, two>(s0, s1, d + r0 * rb, 128, d, rb, a.F / QK, a.hq, prs, a.hq_stride, wave * 32, grid,
+                                acc);
     };
     if constexpr (TE == TS) run(std::integral_constant<int, TE>{});   // one instance of the K loop
     else if (!sh) run(std::integral_constant<int, TE>{});
