@@ -220,25 +220,40 @@ __constant__ uint32_t c_iq3s_grid_pf[512] = CHIMERE_IQ3S_GRID_INIT;
 // 8 weight values of block b of an LDS row as int8, and f32(d); IQ3_S also
 // sets *mult = 1 + 2 * (4-bit scale of sub-block b), the factor of its exact
 // block dot (cs/src/kernels/iq3s_gemv.rs:292-352)
+// Per-superblock fields of an IQ3_S chunk row (read once per chunk): f16 d,
+// the 8 qh bytes, the 4 scale bytes
+struct PfSb {
+    uint32_t d, qh0, qh1, sc;
+};
 template <int T>
+__device__ __forceinline__ void pf_sb(const uint8_t* row, PfSb& f) {
+    if constexpr (T == T_IQ3_S) {
+        f.d = lds_u16(row, 0);
+        f.qh0 = lds_u32(row, 66);
+        f.qh1 = lds_u32(row, 70);
+        f.sc = lds_u32(row, 106);
+    }
+}
+
+template <int T, bool PRE>
 __device__ __forceinline__ long pf_b_frag(const uint8_t* row, int b, int q, uint32_t* dw, int* mult,
-                                          const uint32_t* grid) {
+                                          const uint32_t* grid, const PfSb& f) {
     uint32_t lo, hi;
     if constexpr (T == T_IQ3_S) {
         // sub-block b of the superblock [f16 d][qs 64][qh 8][signs 32][scales 4];
         // lane group q holds elements 8q .. 8q+7: grid entries qs[8b+2q] and
         // qs[8b+2q+1] with high bits 2q and 2q+1 of qh[b], negated per byte by
         // bits 0..3 / 4..7 of signs[4b+q]
-        *dw = lds_u16(row, 0);
+        *dw = PRE ? f.d : lds_u16(row, 0);
         const uint32_t qs = lds_u16(row, 2 + 8 * b + 2 * q);
-        const uint32_t qh = row[66 + b] >> (2 * q);
+        const uint32_t qh = (PRE ? (b < 4 ? f.qh0 >> (8 * b) : f.qh1 >> (8 * (b - 4))) : row[66 + b]) >> (2 * q);
         const uint32_t i0 = (qs & 0xFFu) | ((qh & 1u) << 8), i1 = (qs >> 8) | ((qh & 2u) << 7);
         const uint32_t sg = row[74 + 4 * b + q];
         const uint32_t b0 = nib_bits(sg & 0xFu), b1 = nib_bits(sg >> 4);
         const uint32_t m0 = __builtin_amdgcn_perm(0u, 0u, b0 | 0x0C0C0C0Cu), m1 = __builtin_amdgcn_perm(0u, 0u, b1 | 0x0C0C0C0Cu);
         lo = (grid[i0] ^ m0) + b0;
         hi = (grid[i1] ^ m1) + b1;
-        *mult = 1 + 2 * (int)((row[106 + (b >> 1)] >> (4 * (b & 1))) & 0xFu);
+        *mult = 1 + 2 * (int)(((PRE ? f.sc >> (4 * b) : row[106 + (b >> 1)] >> (4 * (b & 1)))) & 0xFu);
     } else if constexpr (T == T_Q4_0) {
         // bytes o .. o+7 of the row hold the 16 nibbles (low nibbles for
         // q < 2, high for q >= 2); o is 2 mod 4 for even b, 0 mod 4 for odd
@@ -259,6 +274,7 @@ __device__ __forceinline__ long pf_b_frag(const uint8_t* row, int b, int q, uint
     }
     (void)mult;
     (void)grid;
+    (void)f;
     return (long)(((uint64_t)hi << 32) | lo);
 }
 
@@ -300,7 +316,9 @@ __device__ __forceinline__ void pf_issue(uint8_t* wl, const uint8_t* w, int64_t 
 // One staged K chunk for a wave's NTN 16-row column tiles (weight rows
 // wrows + 16*n, LDS row stride cbytes): acc[n][i] = output (pair 4*(l/16)+i,
 // row 16n + l%16), updated per block as fmaf(f32(d_w)*f32(d_x), sumi, acc).
-template <int T, int NTN>
+// PRE: read the per-superblock fields of the rows once per chunk (measured
+// faster on the two-stage gate/up path, slower on the one-stage down path)
+template <int T, int NTN, bool PRE>
 __device__ __forceinline__ void pf_mma_chunk(const uint8_t* xl, const float* xd, const int* xs8,
                                              const uint8_t* wrows, int cbytes, int nb, const uint32_t* grid,
                                              float (&acc)[NTN][4]) {
@@ -310,6 +328,10 @@ __device__ __forceinline__ void pf_mma_chunk(const uint8_t* xl, const float* xd,
     v4i r[NTN], rp[NTN];
     float dw[NTN], dwp[NTN];
     int mu[NTN], mup[NTN];   // IQ3_S sub-block factors
+    PfSb sb[NTN];
+#pragma unroll
+    for (int n = 0; n < NTN; n++)
+        if constexpr (PRE) pf_sb<T>(wrows + (16 * n + c) * cbytes, sb[n]);
     float4 dxp;
     for (int b = 0; b <= nb; b++) {
         float4 dx;
@@ -322,7 +344,7 @@ __device__ __forceinline__ void pf_mma_chunk(const uint8_t* xl, const float* xd,
 #pragma unroll
             for (int n = 0; n < NTN; n++) {
                 uint32_t dwb;
-                const long bf = pf_b_frag<T>(wrows + (16 * n + c) * cbytes, b, q, &dwb, &mu[n], grid);
+                const long bf = pf_b_frag<T, PRE>(wrows + (16 * n + c) * cbytes, b, q, &dwb, &mu[n], grid, sb[n]);
                 dw[n] = h2f(dwb);
                 r[n] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bf, c0, 0, 0, 0);
             }
@@ -392,7 +414,7 @@ __device__ __forceinline__ void pf_gemm_k(const PfStage& s0, const PfStage& s1, 
             __syncthreads();
             pf_xmeta(s0.x, s0.xd, s0.xs);
             __syncthreads();
-            pf_mma_chunk<T, NTN>(s0.x, s0.xd, s0.xs, s0.w + wrow0 * CB, CB, PF_CHUNK, grid, acc);
+            pf_mma_chunk<T, NTN, false>(s0.x, s0.xd, s0.xs, s0.w + wrow0 * CB, CB, PF_CHUNK, grid, acc);
             __syncthreads();
         }
     } else {
@@ -425,7 +447,7 @@ __device__ __forceinline__ void pf_gemm_k(const PfStage& s0, const PfStage& s1, 
             pf_xmeta(cur.x, cur.xd, cur.xs);
             if (c + 1 < nc) issue(c + 1, nxt);
             lds_barrier();   // metadata written
-            pf_mma_chunk<T, NTN>(cur.x, cur.xd, cur.xs, cur.w + wrow0 * CBL + (c * CB & 15), CBL, PF_CHUNK, grid, acc);
+            pf_mma_chunk<T, NTN, true>(cur.x, cur.xd, cur.xs, cur.w + wrow0 * CBL + (c * CB & 15), CBL, PF_CHUNK, grid, acc);
         };
         issue(0, s0);
         for (int c = 0; c < nc; c += 2) {
