@@ -45,7 +45,7 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--pmc", action="store_true", help="light mode for rocprofv3 --pmc runs")
-    ap.add_argument("--pmc-workload", choices=["m1", "m8", "prefill", "head"], default="m1",
+    ap.add_argument("--pmc-workload", choices=["m1", "m8", "prefill", "prefill_iq3s", "head"], default="m1",
                     help="workload of the --pmc light mode")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="run one device copy of this many MiB at the end (calibrates PMC byte counters)")
@@ -126,12 +126,12 @@ def main():
             for i in range(args.steps):
                 G.ggml_gpu_gemv_q4_0_q8(head, xq, y, V, H)
         else:
-            L = make_layer(100, *((IQ3_S, Q8_0) if wl == "m8" else (Q4_0, Q4_0)))
-            M = {"m1": 1, "m8": 8, "prefill": 512}[wl]
+            L = make_layer(100, *((IQ3_S, Q8_0) if wl in ("m8", "prefill_iq3s") else (Q4_0, Q4_0)))
+            M = {"m1": 1, "m8": 8, "prefill": 512, "prefill_iq3s": 512}[wl]
             xs = torch.randn(args.steps, M, H, device=dev)
             out = torch.empty(M, H, device=dev)
             for i in range(args.steps):
-                if wl == "prefill":
+                if wl.startswith("prefill"):
                     L.prefill(xs[i], out=out)
                 else:
                     L.forward(xs[i], out=out)
