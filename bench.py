@@ -363,14 +363,17 @@ def main():
             del wk
 
         # ---------------- attainable rates on this part (beside the datasheet peaks)
-        from chimere_amd._lib import lib as _clib
         import ctypes as _C
+        _probe = _C.CDLL(os.path.join(os.path.dirname(os.path.abspath(__file__)), "chimere_amd", "libchimere_probe.so"))
+        _probe.chimere_probe_stream_read.argtypes = [_C.c_void_p, _C.c_int64, _C.c_void_p, _C.c_int, _C.c_void_p]
+        _probe.chimere_probe_mfma_i8.argtypes = [_C.c_void_p, _C.c_int, _C.c_int, _C.c_void_p]
+        _clib = lambda: _probe  # noqa: E731
         big = torch.empty(2 << 30, dtype=torch.uint8, device=dev)
         big.fill_(1)
         fold = torch.empty(8192, dtype=torch.int32, device=dev)
         best_rd = 0.0
         for nb in (1024, 2048, 4096, 8192):
-            fns = [(lambda nb=nb: _clib().chimere_dbg_stream_read(_C.c_void_p(big.data_ptr()), big.numel(),
+            fns = [(lambda nb=nb: _clib().chimere_probe_stream_read(_C.c_void_p(big.data_ptr()), big.numel(),
                                                                   _C.c_void_p(fold.data_ptr()), nb, G._stream()))
                    for _ in range(3)]
             tr, _ = graph_time(fns)
@@ -378,7 +381,7 @@ def main():
         del big
         mo = torch.empty(1024 * 256, dtype=torch.int32, device=dev)
         iters = 4000
-        fns = [lambda: _clib().chimere_dbg_mfma_i8(_C.c_void_p(mo.data_ptr()), iters, 1024, G._stream())]
+        fns = [lambda: _clib().chimere_probe_mfma_i8(_C.c_void_p(mo.data_ptr()), iters, 1024, G._stream())]
         tm, _ = graph_time(fns)
         mops = 1024 * 4 * 4 * iters * 2 * 32 * 32 * 32 / tm / 1e12
         extra["attainable"] = {"hbm_read_GBs": round(best_rd, 1), "hbm_read_frac_of_peak": round(best_rd / HBM_PEAK_GBS, 4),

@@ -36,8 +36,6 @@ SIGNATURES = [
     ("chimere_mmvq_q6k_f32", None, [vp, vp, vp, i32, i32, i32, vp, vp]),
     ("chimere_mmvq_mxfp4_f32", None, [vp, vp, vp, vp, i32, i32, i32, vp]),
     ("chimere_mmvq_mxfp4_batched", None, [vp, vp, vp, vp, i32, i32, i32, i64, i64, i32, vp]),
-    ("chimere_dbg_stream_read", None, [vp, i64, vp, i32, vp]),
-    ("chimere_dbg_mfma_i8", None, [vp, i32, i32, vp]),
     ("chimere_mmvq_iq3s_batched", None, [vp, vp, vp, vp, i32, i32, i32, i64, i64, i32, vp]),
     ("chimere_mmvq_q8_0_batched", None, [vp, vp, vp, vp, i32, i32, i32, i64, i64, i32, vp]),
     ("chimere_mmvq_q4_0_batched", None, [vp, vp, vp, vp, i32, i32, i32, i64, i64, i32, vp]),

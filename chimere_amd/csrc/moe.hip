@@ -25,40 +25,6 @@
 #include "tile_gemv.h"
 #include "moe_common.h"
 
-// Phase timestamps for latency analysis (debug builds with
-// -DCHIMERE_PHASE_TIMING only): thread 0 of a work-group records the 100 MHz
-// real-time counter at numbered points into LDS (a global store per point
-// would add its acknowledgement to the next wait on vector memory), and
-// PHASE_END copies them to the workspace.
-#ifdef CHIMERE_PHASE_TIMING
-namespace chimere {
-__device__ __forceinline__ uint64_t* phase_lds() {
-    __shared__ uint64_t s_phase[32];
-    return s_phase;
-}
-}
-#define PHASE(kern, i)                                                                      \
-    do {                                                                                     \
-        if (threadIdx.x == 0) {                                                              \
-            if ((i) == 0)                                                                    \
-                for (int q_ = 1; q_ < 32; q_++) chimere::phase_lds()[q_] = 0;               \
-            chimere::phase_lds()[i] = __builtin_amdgcn_s_memrealtime();                     \
-        }                                                                                    \
-    } while (0)
-#define PHASE_PTR(kern, i) (chimere::phase_lds() + (i))
-#define PHASE_END(kern)                                                                     \
-    do {                                                                                     \
-        if (threadIdx.x == 0)                                                                \
-            for (int q_ = 0; q_ < 32; q_++)                                                  \
-                a.phase[((kern) * 4096 + blockIdx.x + blockIdx.y * gridDim.x) * 32 + q_] =     \
-                    chimere::phase_lds()[q_];                                                \
-    } while (0)
-#else
-#define PHASE(kern, i) do {} while (0)
-#define PHASE_PTR(kern, i) nullptr
-#define PHASE_END(kern) do {} while (0)
-#endif
-
 namespace chimere {
 
 __constant__ uint32_t c_iq3s_grid_moe[512] = CHIMERE_IQ3S_GRID_INIT;
@@ -90,7 +56,6 @@ struct MoeArgs {
     uint8_t* hq;        // M > 1: [M*K + M][hq_stride]  Q8_1(h) per pair
     float* dn;          // M > 1: [M*K + M][H]  down-projection output per pair (aliases terms)
     int64_t hq_stride;
-    uint64_t* phase;    // debug timestamps (CHIMERE_PHASE_TIMING builds)
 };
 
 constexpr int PLAN_UEXP = 1, PLAN_UNTOK = 1 + MAX_TOK * MAX_K, PLAN_UPAIR = 1 + 2 * MAX_TOK * MAX_K;
@@ -109,7 +74,6 @@ struct Plan {
 template <int NT>
 __global__ __launch_bounds__(256) void k_moe_route(MoeArgs a) {
     __shared__ float red[NT * 256];
-    PHASE(0, 0);
     const int row = blockIdx.x;
     const int ng = a.sh_gate_w ? 1 : 0;
     if (row >= a.E + ng) {
@@ -126,7 +90,6 @@ __global__ __launch_bounds__(256) void k_moe_route(MoeArgs a) {
                 blk[4 + i] = (uint8_t)(int8_t)q;
                 if (i == 0) *(uint32_t*)blk = f2h(d) | (f2h(sum) << 16);
             });
-        PHASE_END(0);
         return;
     }
     float v[NT];
@@ -138,8 +101,6 @@ __global__ __launch_bounds__(256) void k_moe_route(MoeArgs a) {
             else a.glogit[t] = v[t];
         }
     }
-    PHASE(0, 1);
-    PHASE_END(0);
 }
 
 constexpr int EX_RG = 64;                    // K2 row groups: 1024 threads
@@ -201,10 +162,8 @@ __device__ __forceinline__ void route_plan(const MoeArgs& a, int* first, Plan& p
     const int MK = a.M * a.K;
 
     const int wave = tid >> 6;
-    PHASE(1, 10);
     if (wave < a.M)
-        topk_wave_any(a.logits + wave * a.E, a.E, a.K, s_ids + wave * a.K, s_w + wave * a.K, PHASE_PTR(1, 11));
-    PHASE(1, 1);
+        topk_wave_any(a.logits + wave * a.E, a.E, a.K, s_ids + wave * a.K, s_w + wave * a.K);
     if (a.M == 1) {
         // one token: its K experts are distinct; unit k = the k-th selected
         __syncthreads();
@@ -287,12 +246,10 @@ __device__ __forceinline__ void expert_item(const MoeArgs& a, uint8_t* tile, XLd
     float acc[1][NT];
     const int64_t rb = row_bytes(T, a.H);
     tile_gemv<T, NT, EX_RG, 1>(tile, &xs[0][0], grid, gate + r0 * rb, QK, up + r0 * rb, QK, rb, a.H, a.xq, a.xq_stride, toks,
-                               ntok, acc, PHASE_PTR(1, 5));
-    PHASE(1, 3);
+                               ntok, acc);
     // the down column slice is requested only now, behind the gate/up rows
     // (its pieces are prefetched into L2 by the idle work-groups of this XCD)
     load_down_blocks<T>(db, down, row_bytes(T, a.F), w, a.H);
-    PHASE(1, 8);
     const int g = tid >> 4, j = tid & 15;
 #pragma unroll
     for (int t = 0; t < NT; t++) {
@@ -304,9 +261,7 @@ __device__ __forceinline__ void expert_item(const MoeArgs& a, uint8_t* tile, XLd
             }
         }
     }
-    PHASE(1, 19);
     __syncthreads();
-    PHASE(1, 14);
     // one half-wave per token: Q8_1 of the 32-row block of h (ggml
     // semantics), kept decoded in LDS for the down terms
     if ((tid >> 5) < ntok) {
@@ -327,7 +282,6 @@ __device__ __forceinline__ void expert_item(const MoeArgs& a, uint8_t* tile, XLd
         if (i == 0) { hx[t].d = h2f(f2h(d)); hx[t].sumq = sq; }
     }
     __syncthreads();
-    PHASE(1, 7);
     down_terms<T>(db, hx, pairs, ntok, grid, a, NB, w);
 }
 
@@ -368,11 +322,9 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert(MoeArgs a) {
     const int NB = a.F / QK;
     const int MK = a.M * a.K;
     const int tid = threadIdx.x;
-    PHASE(1, 0);
     route_plan(a, (int*)tile, pl, s_ids, s_w, blockIdx.x == 0);
     if constexpr (TE == T_IQ3_S || TS == T_IQ3_S)
         for (int i = tid; i < 512; i += EX_THREADS) grid[i] = c_iq3s_grid_moe[i];
-    PHASE(1, 2);
     // Items of XCD x (work-groups b with b % 8 == x): the row blocks of the
     // routed units u = x, x+8, ... then the shared unit's blocks w = x, x+8, ...
     // Work-groups without an item prefetch the down matrices those items read
@@ -382,7 +334,6 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert(MoeArgs a) {
     const int nr = pl.nu > x ? (pl.nu - 1 - x) / 8 + 1 : 0;
     const int ns = a.has_shared ? (NB > x ? (NB - 1 - x) / 8 + 1 : 0) : 0;
     const int nx = nr * NB + ns;
-    PHASE(1, 16);
     if (lb >= nx) {
         // helper: first the up rows of this XCD's items (requested by the items
         // right behind their gate rows), then the down matrices; each helper
@@ -413,18 +364,14 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert(MoeArgs a) {
             sink += *(const uint16_t*)(base + (off & ~(int64_t)1));
         }
         if (a.H < 0) a.plan[0] = (int)sink;   // never taken: keeps the loads
-        PHASE_END(1);
         return;
     }
-    PHASE(1, 17);
     for (int i = lb; i < nx; i += G8) {
         const bool shared = i >= nr * NB;
         const int u = shared ? MK : x + 8 * (i / NB);
         const int w = shared ? x + 8 * (i - nr * NB) : i % NB;
         const int ntok = shared ? a.M : pl.untok[u];
-        PHASE(1, 18);
         __syncthreads();   // the previous item's readers of toks / pairs / hx are done
-        PHASE(1, 13);
         if (tid < ntok) {
             toks[tid] = shared ? tid : pl.utok[u][tid];
             pairs[tid] = shared ? MK + tid : pl.upair[u][tid];
@@ -434,9 +381,7 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert(MoeArgs a) {
         else
             expert_item<TE, NT, CB>(a, tile, xs, grid, hg, hu, hx, toks, pairs, ntok, w, a.gate + pl.uexp[u] * a.sg,
                                     a.up + pl.uexp[u] * a.su, a.down + pl.uexp[u] * a.sd);
-        PHASE(1, 4);
     }
-    PHASE_END(1);
 }
 
 // ------------------------------------------ one token, common shapes: K2'
@@ -534,9 +479,7 @@ __device__ __forceinline__ void e1_item(const MoeArgs& a, uint8_t* bufA, uint8_t
         if (c + 1 < nc) wait_vm<E1_ROWS>();
         else wait_vm<0>();
         lds_barrier();
-        if (c == 0) PHASE(1, 10);
         acc = e1_dots<T>(bufA, preA, xs, grid, c, nbH, acc);
-        if (c == 0) PHASE(1, 11);
         if (c + 1 >= nc) break;
         lds_barrier();   // every wave is done with buffer A
         if (c + 2 < nc) {
@@ -546,14 +489,11 @@ __device__ __forceinline__ void e1_item(const MoeArgs& a, uint8_t* bufA, uint8_t
             wait_vm<0>();
         }
         lds_barrier();
-        if (c == 0) PHASE(1, 12);
         acc = e1_dots<T>(bufB, preB, xs, grid, c + 1, nbH, acc);
-        if (c == 0) PHASE(1, 13);
         if (c + 2 >= nc) break;
         lds_barrier();   // every wave is done with buffer B
         if (c + 3 < nc) preB = e1_issue<T>(bufB, gate, up, rb, c + 3, nbH);
     }
-    PHASE(1, 4);
     const int g = tid >> 4, j = tid & 15;
     const float v = slot_reduce16(acc);
     if (j == 0) {
@@ -561,7 +501,6 @@ __device__ __forceinline__ void e1_item(const MoeArgs& a, uint8_t* bufA, uint8_t
         else hu[0][g - QK] = v;
     }
     __syncthreads();
-    PHASE(1, 5);
     // one half-wave: Q8_1 of the 32-row block w of h (ggml semantics), to
     // the pair's row of hq for the down projection
     if (tid < 32) {
@@ -574,7 +513,6 @@ __device__ __forceinline__ void e1_item(const MoeArgs& a, uint8_t* bufA, uint8_t
         o[4 + i] = (uint8_t)(int8_t)q;
         if (i == 0) *(uint32_t*)o = f2h(d) | (f2h(sum) << 16);
     }
-    PHASE(1, 6);
 }
 
 // Helper work-groups of k_moe_expert1 (those without an item) prefetch the
@@ -614,7 +552,6 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert1(MoeArgs a) {
     __shared__ float hg[1][QK], hu[1][QK];
     __shared__ int s_ids[MAX_K];
     __shared__ float s_w[MAX_K];
-    PHASE(1, 0);
     const int tid = threadIdx.x, wave = tid >> 6;
     const int NB = a.F / QK, nbH = a.H / QK;
     const int x = blockIdx.x & 7, lb = blockIdx.x >> 3, G8 = gridDim.x >> 3;
@@ -630,7 +567,7 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert1(MoeArgs a) {
     if (!shared) {
         // wave 0: softmax / top-k; the other waves decode Q8_1(x) meanwhile
         if (wave == 0) {
-            topk_wave_any(a.logits, a.E, a.K, s_ids, s_w, PHASE_PTR(1, 8));
+            topk_wave_any(a.logits, a.E, a.K, s_ids, s_w);
             if (blockIdx.x == 0 && tid < a.K) {
                 a.wts[tid] = s_w[tid];
                 a.plan[PLAN_UEXP + tid] = s_ids[tid];
@@ -646,7 +583,6 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert1(MoeArgs a) {
             }
         }
         __syncthreads();
-        PHASE(1, 1);
         if (!routed) {
             const int nh = G8 - nx, hb = lb - nx;
             E1Prefetch p;
@@ -655,11 +591,9 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert1(MoeArgs a) {
             p.K = a.K; p.has_shared = a.has_shared;
             p.sink_dst = a.plan;
             e1_prefetch(p, s_ids, x, hb, nh);
-            PHASE_END(1);
             return;
         }
         const int e = s_ids[x];
-        PHASE(1, 2);
         e1_item<TE>(a, bufA, bufB, xs, grid, hg, hu, x, lb, a.gate + e * a.sg, a.up + e * a.su);
     } else {
         for (int i = tid; i < nbH; i += EX_THREADS) {
@@ -669,10 +603,8 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert1(MoeArgs a) {
 #pragma unroll
             for (int k = 0; k < 8; k++) xs[i].q[k] = xb.q[k];
         }
-        PHASE(1, 2);
         e1_item<TS>(a, bufA, bufB, xs, grid, hg, hu, a.K, x + 8 * (lb - nr * NB), a.sh_gate, a.sh_up);
     }
-    PHASE_END(1);
 }
 
 // K3: grid (ceil(H/16)), 256 threads: 16 down rows per work-group, 16 lanes
@@ -686,7 +618,6 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_combine(MoeArgs a) {
     __shared__ float s_w[MAX_TOK * MAX_K];
     __shared__ float s_g[MAX_TOK];
     __shared__ float dn[TILE_ROWS][MAX_TOK * MAX_K + MAX_TOK];
-    PHASE(2, 0);
     const int tid = threadIdx.x;
     const int rr = tid >> 4, j = tid & 15;
     // neighbouring 16-row tiles on one XCD (work-group b runs on XCD b % 8):
@@ -737,7 +668,6 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_combine(MoeArgs a) {
         }
     }
     __syncthreads();
-    PHASE(2, 1);
     // combine: one thread per (row, token)
     if (tid < TILE_ROWS * a.M) {
         const int row = tid % TILE_ROWS, t = tid / TILE_ROWS;
@@ -754,8 +684,6 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_combine(MoeArgs a) {
             a.out[(int64_t)t * a.H + rg] = o;
         }
     }
-    PHASE(2, 2);
-    PHASE_END(2);
 }
 
 // K3' (with k_moe_expert1): down projection and combine for one token.
@@ -822,12 +750,15 @@ __device__ __forceinline__ float dc1_row_lds(uint8_t* rows, const uint8_t* d0, i
     return slot_reduce16(v);
 }
 
+// k_moe_dc1 runs only where expert1_fits holds (top_k <= E1_MAX_K)
+constexpr int E1_MAX_K = 8;
+static_assert((E1_MAX_K + 1) * 64 <= 1024, "dc1 work-group size");
+
 template <int TE, int TS>
-__global__ __launch_bounds__((MAX_K + 1) * 64) void k_moe_dc1(MoeArgs a) {
-    __shared__ float dn[DC1_ROWS][MAX_K + 1];
+__global__ __launch_bounds__((E1_MAX_K + 1) * 64) void k_moe_dc1(MoeArgs a) {
+    __shared__ float dn[DC1_ROWS][E1_MAX_K + 1];
     __shared__ __attribute__((aligned(16))) uint8_t srows[is_kquant<TS>() ? DC1_ROWS * 2 * 256 : 1];   // F <= 512
     __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
-    PHASE(2, 0);
     const int tid = threadIdx.x, j = tid & 15, rr = (tid >> 4) & (DC1_ROWS - 1), p = tid >> 6;
     const int tile_i = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
     const int r = tile_i * DC1_ROWS + rr;
@@ -850,7 +781,6 @@ __global__ __launch_bounds__((MAX_K + 1) * 64) void k_moe_dc1(MoeArgs a) {
     }
     if (j == 0) dn[rr][p] = v;
     __syncthreads();
-    PHASE(2, 1);
     if (tid < DC1_ROWS) {
         const int rg = tile_i * DC1_ROWS + tid;
         if (rg < a.H) {
@@ -865,8 +795,6 @@ __global__ __launch_bounds__((MAX_K + 1) * 64) void k_moe_dc1(MoeArgs a) {
             a.out[rg] = o;
         }
     }
-    PHASE(2, 2);
-    PHASE_END(2);
 }
 
 // ------------------------------------------------ several tokens (M > 1)
@@ -926,7 +854,7 @@ __device__ __forceinline__ void kg_tile(uint8_t* tile, XLds* xs, uint8_t* xraw, 
         float a1[4][1];
         if constexpr (kg_db<T>())
             tile_gemv_db<T, 1, KG_RG, 4, KG_BLK, CPOL_STREAM>(tile, KG_BUF, xraw, grid, g, QK, u, QK, rb, a.H, a.xq, a.xq_stride,
-                                                 toks, 1, a1, PHASE_PTR(1, 10));
+                                                 toks, 1, a1);
         else
             tile_gemv<T, 1, KG_RG, 4, KG_BLK, CPOL_STREAM>(tile, xs, grid, g, QK, u, QK, rb, a.H, a.xq, a.xq_stride, toks, 1, a1);
 #pragma unroll
@@ -968,14 +896,12 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_gateup(MoeArgs a) {
         w = li % NB;
         if (u >= MK) return;
     }
-    PHASE(1, 0);
     int ntok;
     int64_t e;
     if (!load_unit(a, u, pairs, toks, ntok, e)) return;
     const int tid = threadIdx.x;
     if constexpr (TE == T_IQ3_S || TS == T_IQ3_S)
         for (int i = tid; i < 512; i += GEMV_THREADS) grid[i] = c_iq3s_grid_moe[i];
-    PHASE(1, 1);
     float acc[4][MAX_TOK];
     const int r0 = w * QK;
     if (e < 0) {
@@ -986,7 +912,6 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_gateup(MoeArgs a) {
         kg_tile<TE>(tile, xs, xraw, grid, a.gate + e * a.sg + r0 * rb, a.up + e * a.su + r0 * rb, rb, a, toks, ntok,
                     acc);
     }
-    PHASE(1, 2);
     // group g holds tile rows g, g+16 (gate rows) and g+32, g+48 (up rows)
     const int g = tid >> 4, j = tid & 15;
 #pragma unroll
@@ -1014,8 +939,6 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_gateup(MoeArgs a) {
         o[4 + i] = (uint8_t)(int8_t)q;
         if (i == 0) *(uint32_t*)o = f2h(d) | (f2h(sum) << 16);
     }
-    PHASE(1, 3);
-    PHASE_END(1);
 }
 
 template <int T>
@@ -1045,11 +968,9 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_down(MoeArgs a) {
     __shared__ int toks[MAX_TOK], pairs[MAX_TOK];
     int ntok;
     int64_t e;
-    PHASE(2, 0);
     // unit blockIdx.y - 1; y = 0: the shared expert (heaviest, dispatched first)
     if (!load_unit(a, blockIdx.y == 0 ? a.M * a.K : (int)blockIdx.y - 1, pairs, toks, ntok, e)) return;
     const int tid = threadIdx.x;
-    PHASE(2, 1);
     if constexpr (TE == T_IQ3_S || TS == T_IQ3_S)
         for (int i = tid; i < 512; i += GEMV_THREADS) grid[i] = c_iq3s_grid_moe[i];
     const int r0 = blockIdx.x * 4 * KG_RG, nr = min(4 * KG_RG, a.H - r0);
@@ -1062,7 +983,6 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_down(MoeArgs a) {
         const int64_t rb = row_bytes(TE, a.F);
         kd_tile<TE>(tile, xs, grid, a.down + e * a.sd + r0 * rb, nr, rb, a, pairs, ntok, acc);
     }
-    PHASE(2, 2);
     const int g = tid >> 4, j = tid & 15;
 #pragma unroll
     for (int r = 0; r < 4; r++)
@@ -1074,8 +994,6 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_down(MoeArgs a) {
                 if (j == 0 && row < nr) a.dn[(int64_t)pairs[t] * a.H + r0 + row] = v;
             }
         }
-    PHASE(2, 3);
-    PHASE_END(2);
 }
 
 // KC: grid (ceil(H/256), M): out = sum_k fmaf(w_k, dn_k, acc) in k order (+ shared expert)
@@ -1098,7 +1016,7 @@ __global__ __launch_bounds__(256) void k_moe_combine_dn(MoeArgs a) {
 // ------------------------------------------------------- workspace plan
 
 struct WsPlan {
-    size_t logits, glogit, wts, plan, xq, terms, hq, phase, total;
+    size_t logits, glogit, wts, plan, xq, terms, hq, total;
     int64_t xq_stride, hq_stride;
 };
 
@@ -1117,9 +1035,6 @@ static WsPlan plan_ws(int H, int F, int E, int K, int M) {
     p.terms = o; o += al256((size_t)P * H * (F / QK) * (F / QK <= SLOTS ? 4 : 8));
     p.hq_stride = pad_to(F, ROW_PAD) / QK * Q8_1_BYTES;
     p.hq = o; o += al256((size_t)P * p.hq_stride);
-#ifdef CHIMERE_PHASE_TIMING
-    p.phase = o; o += al256((size_t)3 * 4096 * 32 * 8);
-#endif
     p.total = o;
     return p;
 }
@@ -1151,7 +1066,7 @@ static bool expert1_fits(const MoeArgs& a, int te, int ts) {
                          (uintptr_t)a.su | (uintptr_t)a.sd | (uintptr_t)a.sh_gate | (uintptr_t)a.sh_up |
                          (uintptr_t)a.sh_down | (uintptr_t)a.xq | (uintptr_t)row_bytes(te, a.H) |
                          (uintptr_t)(a.has_shared ? row_bytes(ts, a.H) : 0);
-    return a.M == 1 && a.K <= 8 && a.H <= E1_MAX_H && NB <= SLOTS && (al & 15) == 0 &&
+    return a.M == 1 && a.K <= E1_MAX_K && a.H <= E1_MAX_H && NB <= SLOTS && (al & 15) == 0 &&
            NB + ns <= expert_grid(256) / 8;
 }
 
@@ -1334,7 +1249,6 @@ static void moe_decode(const chimere_moe_layer* L, const float* x, float* out, i
     a.xq = w + p.xq; a.terms = (uint2*)(w + p.terms); a.lane_acc = (float*)(w + p.terms);
     a.xq_stride = p.xq_stride;
     a.hq = w + p.hq; a.dn = (float*)(w + p.terms); a.hq_stride = p.hq_stride;
-    a.phase = (uint64_t*)(w + p.phase);
     dispatch_layer(L->expert_type, L->shared_type, a, stage, stream);
     check_launch("moe_ffn_decode");
 }

@@ -100,8 +100,7 @@ __device__ __forceinline__ void f32_row_dot(const float* __restrict__ a, const f
 // order).  Lane k < K writes entry k.  Requires E <= 1024, K <= min(E, 64).
 template <int NV>
 __device__ __forceinline__ void topk_wave(const float* __restrict__ logits, int E, int K,
-                                          int* __restrict__ idx_out, float* __restrict__ w_out,
-                                          uint64_t* ph = nullptr) {
+                                          int* __restrict__ idx_out, float* __restrict__ w_out) {
     const int lane = threadIdx.x & 63;
     float p[NV], ev[NV];
     float mx = -__builtin_huge_valf();
@@ -112,9 +111,6 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ logits, int 
         mx = __builtin_fmaxf(mx, p[i]);
     }
     mx = bfly32_max(__builtin_fmaxf(mx, xlane<32>(mx)));
-#ifdef CHIMERE_PHASE_TIMING
-    if (ph && lane == 0) ph[0] = __builtin_amdgcn_s_memrealtime();
-#endif
 #pragma unroll
     for (int i = 0; i < NV; i++) {
         ev[i] = (lane + 64 * i) < E ? det_exp(p[i] - mx) : 0.0f;
@@ -134,9 +130,6 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ logits, int 
         p[i] = s > 0.0f ? ev[i] / s : 1.0f / (float)E;
         key[i] = j < E ? __builtin_bit_cast(uint32_t, p[i]) + 1u : 0u;
     }
-#ifdef CHIMERE_PHASE_TIMING
-    if (ph && lane == 0) ph[1] = __builtin_amdgcn_s_memrealtime();
-#endif
     int my_idx = 0;
     float my_w = 0.0f;
     if constexpr (NV == 4) {
@@ -221,9 +214,8 @@ static __device__ __noinline__ void topk_wave_other(const float* logits, int E, 
     else topk_wave<16>(logits, E, K, idx, w);
 }
 
-__device__ __forceinline__ void topk_wave_any(const float* logits, int E, int K, int* idx, float* w,
-                                              uint64_t* ph = nullptr) {
-    if (E > 128 && E <= 256) topk_wave<4>(logits, E, K, idx, w, ph);
+__device__ __forceinline__ void topk_wave_any(const float* logits, int E, int K, int* idx, float* w) {
+    if (E > 128 && E <= 256) topk_wave<4>(logits, E, K, idx, w);
     else topk_wave_other(logits, E, K, idx, w);
 }
 

@@ -1,6 +1,6 @@
 // prefill.hip -- routed MoE FFN for a chunk of tokens (prefill): tokens are
 // routed, grouped by expert, and each expert's gate/up and down projections
-// run as int8 MFMA grouped GEMMs (v_mfma_i32_32x32x32_i8: one 32-element
+// run as int8 MFMA grouped GEMMs (v_mfma_i32_16x16x32_i8: one 32-element
 // quantization block per instruction, so every block's int32 dot is exact),
 // with the per-block fp32 rescale acc = fmaf(f32(d_w) * f32(d_x), (float)sumi,
 // acc) applied in ascending block order (the L=1 order).  No counterpart in

@@ -65,7 +65,7 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds* __re
                                           const uint8_t* base1, int n1, const uint8_t* base2, int n2,
                                           int64_t rb, int ncols, const uint8_t* __restrict__ X,
                                           int64_t x_tok_stride, const int* toks, int ntok,
-                                          float (&acc)[RPG][NT], uint64_t* ph = nullptr) {
+                                          float (&acc)[RPG][NT]) {
     constexpr int NTH = RG * SLOTS;
     static_assert(CBLK % SLOTS == 0 && (QTraits<T>::ELEMS != 256 || CBLK % 8 == 0) && CBLK <= MAX_CHUNK_BLOCKS, "chunk");
     const int tid = threadIdx.x;
@@ -81,15 +81,9 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds* __re
         const int seg = chunk_bytes<T>(cb);
         const int64_t goff = (int64_t)b0 / (QTraits<T>::ELEMS / QK) * QTraits<T>::BYTES;
         __syncthreads();   // previous users of tile / xs are done
-#ifdef CHIMERE_PHASE_TIMING
-        if (ph && tid == 0) ph[10] = __builtin_amdgcn_s_memrealtime();
-#endif
         // rows are packed with stride seg (== CB except in a ragged last chunk)
         if (n1) stage_rows<stage_dw<T>(), CPOL>(tile, base1 + goff, rb, n1, seg, tid, NTH);
         if (n2) stage_rows<stage_dw<T>(), CPOL>(tile + n1 * seg, base2 + goff, rb, n2, seg, tid, NTH);
-#ifdef CHIMERE_PHASE_TIMING
-        if (ph && tid == 0) ph[4] = __builtin_amdgcn_s_memrealtime();
-#endif
         for (int i = tid; i < ntok * cb; i += NTH) {
             const int t = i / cb, b = i - t * cb;
             const int tk = toks ? toks[t] : t;
@@ -101,14 +95,8 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds* __re
             o.d = xb.d;
             o.sumq = xb.sumq;
         }
-#ifdef CHIMERE_PHASE_TIMING
-        if (ph && tid == 0) ph[0] = __builtin_amdgcn_s_memrealtime();
-#endif
         lds_copy_wait();
         __syncthreads();
-#ifdef CHIMERE_PHASE_TIMING
-        if (ph && tid == 0) ph[1] = __builtin_amdgcn_s_memrealtime();
-#endif
         const uint8_t* tl = tile;
         if constexpr (NT == 1) {
             // one token: the activation block is read once for all RPG rows
@@ -179,7 +167,7 @@ __device__ __forceinline__ void tile_gemv_db(uint8_t* __restrict__ tile, int TB,
                                              const uint32_t* __restrict__ grid, const uint8_t* base1, int n1,
                                              const uint8_t* base2, int n2, int64_t rb, int ncols,
                                              const uint8_t* __restrict__ X, int64_t x_tok_stride, const int* toks,
-                                             int ntok, float (&acc)[RPG][NT], uint64_t* ph = nullptr) {
+                                             int ntok, float (&acc)[RPG][NT]) {
     constexpr int NTH = RG * SLOTS, XB = NT * CBLK * Q8_1_BYTES;
     static_assert(CBLK % SLOTS == 0 && (QTraits<T>::ELEMS != 256 || CBLK % 8 == 0) && CBLK <= MAX_CHUNK_BLOCKS, "chunk");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -234,9 +222,6 @@ __device__ __forceinline__ void tile_gemv_db(uint8_t* __restrict__ tile, int TB,
         const int buf = c & 1, cb = min(CBLK, nb - c * CBLK);
         lds_copy_wait();
         __syncthreads();   // chunk c landed; every wave is done with chunk c-1
-#ifdef CHIMERE_PHASE_TIMING
-        if (ph && tid == 0 && c < 4) ph[2 * c] = __builtin_amdgcn_s_memrealtime();
-#endif
         if (c + 1 < nc) issue(c + 1, buf ^ 1);
         const uint8_t* tb = tile + buf * TB + (buf ? pre1 : pre0);
         const int seg = buf ? rs1 : rs0;   // LDS row stride of this chunk
@@ -278,9 +263,6 @@ __device__ __forceinline__ void tile_gemv_db(uint8_t* __restrict__ tile, int TB,
                 }
             }
         }
-#ifdef CHIMERE_PHASE_TIMING
-        if (ph && tid == 0 && c < 4) ph[2 * c + 1] = __builtin_amdgcn_s_memrealtime();
-#endif
     }
 }
 

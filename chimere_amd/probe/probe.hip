@@ -1,8 +1,10 @@
-// probe.hip -- attainable-rate microbenchmarks that the measurement reports
+// probe.hip -- attainable-rate microbenchmarks that the benchmark reports
 // beside the datasheet peaks: a streaming HBM read and a dense int8 MFMA
-// loop.  Debug entry points; no part of the decode path calls them.
-#include "api_internal.h"
-#include "common.h"
+// loop.  Built as its own library (libchimere_probe.so) that only the
+// benchmark loads; the product library exports no measurement kernels.
+// Entry points return 0 on success, -1 on bad arguments, -2 on a failed launch.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
 
 namespace chimere {
 
@@ -62,22 +64,20 @@ using namespace chimere;
 
 extern "C" {
 
-void chimere_dbg_stream_read(const void* buf, int64_t bytes, uint32_t* out, int nblocks, hipStream_t s) {
-    if (!buf || !out || bytes < 16 || (bytes & 15) || ((uintptr_t)buf & 15) || nblocks <= 0) {
-        set_error(CHIMERE_ERR_ARG, "dbg_stream_read: need a 16-byte aligned buffer, bytes %% 16 == 0, nblocks > 0");
-        return;
-    }
+// nblocks work-groups of 256 threads read `bytes` (16-byte aligned) once;
+// out[nblocks] receives an xor fold.
+int chimere_probe_stream_read(const void* buf, int64_t bytes, uint32_t* out, int nblocks, hipStream_t s) {
+    if (!buf || !out || bytes < 16 || (bytes & 15) || ((uintptr_t)buf & 15) || nblocks <= 0) return -1;
     hipLaunchKernelGGL(k_stream_read, dim3((unsigned)nblocks), dim3(256), 0, s, (const v4i_p*)buf, bytes / 16, out);
-    check_launch("dbg_stream_read");
+    return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
-void chimere_dbg_mfma_i8(int32_t* out, int iters, int nblocks, hipStream_t s) {
-    if (!out || iters <= 0 || nblocks <= 0) {
-        set_error(CHIMERE_ERR_ARG, "dbg_mfma_i8: need out, iters > 0, nblocks > 0");
-        return;
-    }
+// nblocks x 4 waves, each 4 x iters v_mfma_i32_32x32x32_i8 (65536 int8 ops
+// each); out[nblocks * 256].
+int chimere_probe_mfma_i8(int32_t* out, int iters, int nblocks, hipStream_t s) {
+    if (!out || iters <= 0 || nblocks <= 0) return -1;
     hipLaunchKernelGGL(k_mfma_i8, dim3((unsigned)nblocks), dim3(256), 0, s, iters, out);
-    check_launch("dbg_mfma_i8");
+    return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
 }  // extern "C"

@@ -244,15 +244,6 @@ void chimere_quantize_weights(int type, const float *x, void *out, int64_t n,
 void chimere_dbg_block_dots(int type, const void *weights, const void *input_q8,
                             int32_t *out, int ncols, int nrows, hipStream_t stream);
 
-/* Attainable-rate probes (no counterpart in the reference; reported by the
- * benchmark beside the datasheet peaks).  stream_read: nblocks work-groups of
- * 256 threads read `bytes` (16-byte aligned) once, out[nblocks] receives an
- * xor fold.  mfma_i8: nblocks x 4 waves, each 4 x iters
- * v_mfma_i32_32x32x32_i8 (65536 int8 ops each); out[nblocks*256]. */
-void chimere_dbg_stream_read(const void *buf, int64_t bytes, uint32_t *out, int nblocks,
-                             hipStream_t stream);
-void chimere_dbg_mfma_i8(int32_t *out, int iters, int nblocks, hipStream_t stream);
-
 /* ------------------------------------------------------------ errors */
 /* Last error on the calling host thread (CHIMERE_OK if none); clears it. */
 int chimere_hip_get_last_error(void);

@@ -116,6 +116,53 @@ float orc_exp(float x) {
 
 float orc_silu(float g) { return g / (1.0f + orc_exp(-g)); }
 
+/* Check of orc_exp over every float in [lo, hi] (lo <= hi <= 0): returns the
+ * number of adjacent float pairs x < y with orc_exp(x) > orc_exp(y);
+ * *max_step receives the largest such excess in units in the last place of
+ * the result, *max_rel the largest |orc_exp(x) - e^x| / e^x over x >= -86
+ * (the flush-to-zero bound), with e^x from libm's double exp. */
+int64_t orc_exp_scan(float lo, float hi, int *max_step, double *max_rel) {
+    uint32_t ulo, uhi;
+    memcpy(&ulo, &lo, 4);
+    memcpy(&uhi, &hi, 4);
+    /* negative floats: bit patterns increase as values decrease */
+    const uint32_t a = uhi == 0 ? 0x80000000u : uhi, b = ulo;   /* [a, b] covers hi down to lo */
+    int64_t bad = 0;
+    int step = 0;
+    double worst = 0.0;
+#pragma omp parallel for schedule(static) reduction(+ : bad) reduction(max : worst, step)
+    for (int64_t c = 0; c < 4096; c++) {
+        const uint64_t n = (uint64_t)(b - a) + 1;
+        const uint32_t s0 = a + (uint32_t)(n * (uint64_t)c / 4096), s1 = a + (uint32_t)(n * (uint64_t)(c + 1) / 4096);
+        float prev_x;
+        uint32_t u0 = s0;
+        memcpy(&prev_x, &u0, 4);
+        float prev = orc_exp(prev_x);
+        /* walk from larger values (s0) to smaller ones: exp must not increase */
+        for (uint32_t u = s0 + 1; u <= s1 && u <= b; u++) {
+            float x;
+            memcpy(&x, &u, 4);
+            const float e = orc_exp(x);
+            if (e > prev) {
+                uint32_t ue, up;
+                memcpy(&ue, &e, 4);
+                memcpy(&up, &prev, 4);
+                bad++;
+                if ((int)(ue - up) > step) step = (int)(ue - up);
+            }
+            if (x >= -86.0f) {
+                const double t = exp((double)x);
+                const double r = fabs((double)e - t) / t;
+                if (r > worst) worst = r;
+            }
+            prev = e;
+        }
+    }
+    if (max_step) *max_step = step;
+    if (max_rel) *max_rel = worst;
+    return bad;
+}
+
 /* ------------------------------------------------------------- formats */
 
 int64_t orc_row_bytes(int type, int64_t ncols) {

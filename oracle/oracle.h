@@ -45,6 +45,9 @@ enum { ORC_Q4_0 = 2, ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q5_K = 13, ORC_Q6_K = 14, 
 uint16_t orc_f32_to_f16(float x);
 float    orc_f16_to_f32(uint16_t h);
 float    orc_exp(float x);
+/* every float in [lo, hi] <= 0: count of monotonicity violations, their
+ * largest size in ulps, worst relative error against libm exp (x >= -86) */
+int64_t  orc_exp_scan(float lo, float hi, int *max_step, double *max_rel);
 float    orc_silu(float g);
 
 int64_t  orc_row_bytes(int type, int64_t ncols);

@@ -14,7 +14,7 @@ import torch
 
 import oracle as O
 from chimere_amd.moe import MoeLayer
-from test_gpu_moe import build, qmat
+from test_gpu_moe import build, host, oracle_run, qmat
 
 pytestmark = pytest.mark.gpu
 
@@ -33,7 +33,7 @@ def _capture(fn):
     return g
 
 
-def _check_replays(layer, call, M, H, K, dev, seed):
+def _check_replays(layer, call, M, H, K, dev, seed, order=16):
     gx = torch.Generator(device=dev).manual_seed(seed)
     inputs = [torch.randn(M, H, generator=gx, device=dev) for _ in range(3)]
     want = []
@@ -58,6 +58,10 @@ def _check_replays(layer, call, M, H, K, dev, seed):
         got = (os_.cpu().numpy(), ids_s.cpu().numpy(), wts_s.cpu().numpy())
         for name, a, b in zip(("out", "ids", "wts"), got, want[i]):
             assert np.array_equal(a, b), f"replay {rep} (input {i}): {name} differs from the eager call"
+        if rep < 3:   # the first replay of each input against the oracle too
+            oo, io, wo = oracle_run(layer, inputs[i], L=order)
+            assert (got[1] == io).all() and (got[2].view(np.uint32) == wo.view(np.uint32)).all()
+            assert (got[0].view(np.uint32) == oo.view(np.uint32)).all(), f"replay {rep}: output differs from the oracle"
         call(layer, other, torch.empty_like(other), None, None)   # eager work between replays
         torch.cuda.synchronize()
 
@@ -104,7 +108,7 @@ def test_prefill_graph_replays(dev):
     layer = build(dev, 930, E=64, et=O.Q4_0, st=O.Q4_0)
     T = 96
     layer.prefill(torch.zeros(T, layer.H, device=dev))   # sizes the workspace before capture
-    _check_replays(layer, _prefill, T, layer.H, layer.K, dev, 931)
+    _check_replays(layer, _prefill, T, layer.H, layer.K, dev, 931, order=1)
 
 
 def test_gemv_sequence_graph_replays(dev):

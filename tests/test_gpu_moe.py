@@ -14,6 +14,7 @@ import torch
 import oracle as O
 from chimere_amd import ggml_gpu as G
 from chimere_amd.moe import MoeLayer
+from routing_margin import assert_topk_margin
 
 pytestmark = pytest.mark.gpu
 
@@ -61,8 +62,22 @@ def oracle_run(layer, x, L=16):
                  logit_bias=None if bias is None else host(bias), L=L, G=1)
 
 
-def run_and_check(layer, x, exact=True):
+def routing_logits(layer, x):
+    """Router logits of every token by the oracle (reference order), plus the bias."""
+    r, bias = host(layer.tensors[0]), layer.tensors[5]
+    lg = np.stack([O.router(r, xm) for xm in host(x)])
+    return lg + host(bias)[None, :] if bias is not None else lg
+
+
+def check_margin(layer, x, what=""):
+    """The selection is independent of the exponential used (top-k gap rule)."""
+    assert_topk_margin(routing_logits(layer, x), layer.K, what)
+
+
+def run_and_check(layer, x, exact=True, margin=True):
     M = x.shape[0]
+    if margin:
+        check_margin(layer, x)
     ids = torch.zeros(M, layer.K, dtype=torch.int32, device=x.device)
     wts = torch.zeros(M, layer.K, dtype=torch.float32, device=x.device)
     out = layer.forward(x, ids=ids, wts=wts)
@@ -134,7 +149,7 @@ def test_moe_zero_input_finite(dev, M):
     """All logits equal: every probability ties, the lowest indices win."""
     layer = build(dev, 9, H=1024, F=256, E=32, K=4)
     x = torch.zeros(M, 1024, device=dev)
-    og, ig, wg = run_and_check(layer, x)
+    og, ig, wg = run_and_check(layer, x, margin=False)
     assert np.isfinite(og).all() and (ig == np.arange(4)).all()
 
 
@@ -146,7 +161,7 @@ def test_moe_m1_tied_logits(dev):
     r[1::2] = r[0::2]            # experts 2i and 2i+1 get identical logits
     g = torch.Generator(device=dev).manual_seed(4)
     for _ in range(3):
-        og, ig, wg = run_and_check(layer, torch.randn(1, 1024, generator=g, device=dev))
+        og, ig, wg = run_and_check(layer, torch.randn(1, 1024, generator=g, device=dev), margin=False)
         assert len(set(ig[0])) == 7
 
 

@@ -12,13 +12,15 @@ import pytest
 import torch
 
 import oracle as O
-from test_gpu_moe import build, host, oracle_run
+from test_gpu_moe import build, check_margin, host, oracle_run
 
 pytestmark = pytest.mark.gpu
 
 
-def prefill_check(layer, x, sample=None):
+def prefill_check(layer, x, sample=None, margin=True):
     T = x.shape[0]
+    if margin:
+        check_margin(layer, x if sample is None else x[sample])
     ids = torch.full((T, layer.K), -1, dtype=torch.int32, device=x.device)
     wts = torch.zeros(T, layer.K, dtype=torch.float32, device=x.device)
     out = layer.prefill(x, ids=ids, wts=wts)
@@ -51,13 +53,29 @@ def test_prefill_small(dev, et, st, gate_vec, K, E, T):
     prefill_check(layer, torch.randn(T, 1024, generator=g, device=dev))
 
 
+@pytest.mark.parametrize("et,st,gate_vec", [
+    (O.IQ3_S, O.IQ3_S, True),
+    (O.IQ3_S, O.Q4_0, False),
+    (O.Q4_0, O.IQ3_S, True),
+])
+def test_prefill_aligned_rows(dev, et, st, gate_vec):
+    """H = 2048: 880-byte IQ3_S rows are 16-byte aligned, so the gate/up GEMM
+    runs the two-stage aligned-span path; 37 tokens leave partially filled
+    16-pair tiles."""
+    print(f"prefill aligned et={et} st={st} gate={gate_vec}", flush=True)
+    layer = build(dev, 400 + et + st, H=2048, F=512, E=64, K=8, et=et, st=st, gate_vec=gate_vec)
+    g = torch.Generator(device=dev).manual_seed(37)
+    prefill_check(layer, torch.randn(37, 2048, generator=g, device=dev))
+
+
 def test_prefill_config5_512(dev):
     """512 tokens, H=2048, F=512, E=256, top-8, Q4_0 experts + Q4_0 shared."""
     layer = build(dev, 5)
     g = torch.Generator(device=dev).manual_seed(55)
     x = torch.randn(512, 2048, generator=g, device=dev)
     sample = [0, 1, 63, 64, 200, 311, 510, 511]
-    og, ig, wg = prefill_check(layer, x, sample=sample)
+    check_margin(layer, x, "config 5")
+    og, ig, wg = prefill_check(layer, x, sample=sample, margin=False)
     assert np.isfinite(og).all()
     # routing of every token equals the decode entry point's, bit for bit
     for t0 in range(0, 512, 8):

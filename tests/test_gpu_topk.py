@@ -45,3 +45,24 @@ def test_topk_softmax_ties(E, K):
         oi, ow = O.topk_softmax(logits[t], K)
         assert (gi[t] == oi).all(), (t, gi[t], oi)
         assert (gw[t].view(np.uint32) == ow.view(np.uint32)).all(), (t, gw[t], ow)
+
+
+def test_device_exp_equals_oracle_over_softmax_range():
+    """K = E = 16: every probability is returned, so the device exponential
+    is compared with the oracle's on 61440 arguments spread over [-87, 0]
+    (the softmax range; one logit per row is the maximum, 0)."""
+    E = K = 16
+    rng = np.random.default_rng(16)
+    n = 4096
+    logits = rng.uniform(-87.0, 0.0, (n, E)).astype(np.float32)
+    logits[:, 0] = 0.0
+    logits[: n // 2, 1:] = rng.uniform(-1.0, 0.0, (n // 2, E - 1)).astype(np.float32)   # dense near 0
+    dl = torch.from_numpy(logits).cuda()
+    ids = torch.empty(n, K, dtype=torch.int32, device="cuda")
+    wts = torch.empty(n, K, dtype=torch.float32, device="cuda")
+    G.gpu_topk_softmax(dl, ids, wts, E, K, ntok=n)
+    torch.cuda.synchronize()
+    gi, gw = ids.cpu().numpy(), wts.cpu().numpy()
+    for t in range(n):
+        oi, ow = O.topk_softmax(logits[t], K)
+        assert (gi[t] == oi).all() and (gw[t].view(np.uint32) == ow.view(np.uint32)).all(), t
