@@ -545,8 +545,9 @@ __device__ __forceinline__ void e1_prefetch(const E1Prefetch& p, const int* uexp
 template <int TE, int TS>
 __global__ __launch_bounds__(EX_THREADS) void k_moe_expert1(MoeArgs a) {
     constexpr int CB = e1_stride<TE>() > e1_stride<TS>() ? e1_stride<TE>() : e1_stride<TS>();
-    __shared__ __attribute__((aligned(16))) uint8_t bufA[2 * QK * CB];
-    __shared__ __attribute__((aligned(16))) uint8_t bufB[2 * QK * CB];
+    // + 16: lds_u32 of a row's last block reads up to 4 bytes past the row
+    __shared__ __attribute__((aligned(16))) uint8_t bufA[2 * QK * CB + 16];
+    __shared__ __attribute__((aligned(16))) uint8_t bufB[2 * QK * CB + 16];
     __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
     __shared__ XLds xs[E1_MAX_H / QK];
     __shared__ float hg[1][QK], hu[1][QK];

@@ -165,6 +165,25 @@ def test_moe_m1_tied_logits(dev):
         assert len(set(ig[0])) == 7
 
 
+@pytest.mark.parametrize("et,st", [(O.Q4_0, O.Q4_0), (O.IQ3_S, O.Q8_0)])
+def test_moe_m1_ties_model_shape(dev, et, st):
+    """One token at the model's shape (E=256, top-8) on the one-token kernels
+    (ranking top-k): all logits tied (zero input: the 8 lowest indices win,
+    equal weights), router rows tied in pairs (ties straddle the top-8
+    boundary), and four-way ties."""
+    print(f"moe m1 ties et={et} st={st}", flush=True)
+    layer = build(dev, 60 + et, et=et, st=st, gate_vec=True)
+    og, ig, wg = run_and_check(layer, torch.zeros(1, 2048, device=dev), margin=False)
+    assert (ig[0] == np.arange(8)).all() and (wg[0] == wg[0][0]).all()
+    r = layer.tensors[0]
+    g = torch.Generator(device=dev).manual_seed(61)
+    for group in (2, 4):
+        r.copy_(r[::group].repeat_interleave(group, dim=0))
+        for _ in range(2):
+            og, ig, wg = run_and_check(layer, torch.randn(1, 2048, generator=g, device=dev), margin=False)
+            assert len(set(ig[0])) == 8
+
+
 def test_moe_repeat_calls_reuse_workspace(dev):
     """Counters left at zero: many calls on one workspace stay bit-identical."""
     layer = build(dev, 11, H=1024, F=256, E=64, K=8)
