@@ -52,6 +52,7 @@ SIGNATURES = [
     ("chimere_moe_workspace_init", None, [vp, szt, vp]),
     ("chimere_moe_ffn_decode", None, [vp, vp, vp, i32, vp, vp, vp, szt, vp]),
     ("chimere_moe_ffn_decode_stage", None, [vp, vp, vp, i32, vp, szt, i32, vp]),
+    ("chimere_moe_ffn_decode_noalloc", None, [vp, vp, vp, i32, vp, vp, vp]),
     ("chimere_moe_prefill_workspace_size", szt, [vp, i32]),
     ("chimere_moe_prefill", None, [vp, vp, vp, i32, vp, vp, vp, szt, vp]),
     ("chimere_quantize_weights", None, [i32, vp, vp, i64, vp]),

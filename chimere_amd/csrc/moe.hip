@@ -20,6 +20,8 @@
 //                     the router-weighted sum in k order plus the shared
 //                     expert.
 // Every row dot uses the (L=16, G=1) order of tile_gemv.h.
+#include <mutex>
+
 #include "api_internal.h"
 #include "common.h"
 #include "tile_gemv.h"
@@ -1193,6 +1195,29 @@ __global__ void k_fill_zero(uint32_t* p, size_t n) {
         p[i] = 0;
 }
 
+// ---- no-allocation variant: the workspace is a file-scope device array.
+// Each GPU the library runs on holds its own copy (16 MiB) until the process
+// ends.  Host code never passes `scratch` itself (in host code the name is a
+// stand-in, not a device address): the array's address on each device comes
+// from hipGetSymbolAddress, taken once per device with that device current.
+constexpr size_t MOE_STATIC_SCRATCH_BYTES = (size_t)16 << 20;
+static __device__ __attribute__((aligned(256))) uint8_t scratch[MOE_STATIC_SCRATCH_BYTES];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[64];
+
+// Device address of this device's scratch (nullptr on failure).
+static void* scratch_ptr(int dev) {
+    if (dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+        g_scratch_ptr[dev] = ptr;
+    }
+    return g_scratch_ptr[dev];
+}
+
 }  // namespace chimere
 
 using namespace chimere;
@@ -1258,6 +1283,23 @@ void chimere_moe_ffn_decode(const chimere_moe_layer* L, const float* x, float* o
                             int* ids_out, float* w_out, void* workspace, size_t ws_bytes,
                             hipStream_t stream) {
     moe_decode(L, x, out, ntok, ids_out, w_out, workspace, ws_bytes, -1, stream);
+}
+
+void chimere_moe_ffn_decode_noalloc(const chimere_moe_layer* L, const float* x, float* out, int ntok,
+                                    int* ids_out, float* w_out, hipStream_t stream) {
+    CHIMERE_REQUIRE(L, CHIMERE_ERR_ARG, "moe_ffn_decode_noalloc: null layer");
+    CHIMERE_REQUIRE(ntok >= 1 && ntok <= MAX_TOK, CHIMERE_ERR_ARG, "moe_ffn_decode_noalloc: ntok=%d not in 1..8",
+                    ntok);
+    const size_t need = chimere_moe_workspace_size(L, ntok);
+    CHIMERE_REQUIRE(need > 0, CHIMERE_ERR_ARG, "moe_ffn_decode_noalloc: layer shape rejected");
+    CHIMERE_REQUIRE(need <= MOE_STATIC_SCRATCH_BYTES, CHIMERE_ERR_WORKSPACE,
+                    "moe_ffn_decode_noalloc: layer needs %zu scratch bytes > the static %zu", need,
+                    MOE_STATIC_SCRATCH_BYTES);
+    int dev = -1;
+    CHIMERE_REQUIRE(hipGetDevice(&dev) == hipSuccess, CHIMERE_ERR_LAUNCH, "moe_ffn_decode_noalloc: no device");
+    void* ws = scratch_ptr(dev);
+    CHIMERE_REQUIRE(ws, CHIMERE_ERR_LAUNCH, "moe_ffn_decode_noalloc: hipGetSymbolAddress failed on device %d", dev);
+    moe_decode(L, x, out, ntok, ids_out, w_out, ws, MOE_STATIC_SCRATCH_BYTES, -1, stream);
 }
 
 void chimere_moe_ffn_decode_stage(const chimere_moe_layer* L, const float* x, float* out, int ntok,

@@ -76,6 +76,17 @@ class MoeLayer:
         check()
         return out
 
+    def forward_noalloc(self, x, out=None, ids=None, wts=None):
+        """forward() through chimere_moe_ffn_decode_noalloc (the library's static
+        per-device scratch instead of this layer's workspace)."""
+        if out is None:
+            out = torch.empty_like(x)
+        lib().chimere_moe_ffn_decode_noalloc(C.byref(self.c), C.c_void_p(x.data_ptr()), C.c_void_p(out.data_ptr()),
+                                             x.shape[0], C.c_void_p(ids.data_ptr()) if ids is not None else None,
+                                             C.c_void_p(wts.data_ptr()) if wts is not None else None, G._stream())
+        check()
+        return out
+
     def prefill(self, x, out=None, ids=None, wts=None):
         """x [T, H] f32, any T >= 1 -> out [T, H] through chimere_moe_prefill
         (int8 matrix-core grouped GEMMs; Q4_0 / Q8_0 / IQ3_S weights).  The prefill

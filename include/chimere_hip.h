@@ -204,6 +204,18 @@ void chimere_moe_ffn_decode(const chimere_moe_layer *layer, const float *x, floa
                             int ntok, int *ids_out, float *w_out, void *workspace,
                             size_t workspace_bytes, hipStream_t stream);
 
+/* No-allocation variant of chimere_moe_ffn_decode (no counterpart in the
+ * reference): for callers that cannot allocate -- code under HIP-graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  Same
+ * arguments and results without the workspace: the scratch is a static
+ * 16 MiB device array per GPU (enough for H <= 2048, F <= 512, E <= 256,
+ * top-8 at 8 tokens); larger layers are rejected with CHIMERE_ERR_WORKSPACE.
+ * Nothing is allocated or freed; no scratch field needs clearing (every call
+ * writes what it reads).  Calls that overlap on one GPU (other streams, other
+ * host threads) share that scratch and race: serialise them. */
+void chimere_moe_ffn_decode_noalloc(const chimere_moe_layer *layer, const float *x, float *out,
+                                    int ntok, int *ids_out, float *w_out, hipStream_t stream);
+
 /* Profiling variant (no reference counterpart): launches only kernel `stage`
  * of chimere_moe_ffn_decode (0 router/top-k, 1 gate/up + SiLU, 2 down +
  * combine; -1 all) on a workspace that a full call with the same layer, x and
