@@ -43,7 +43,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=6.0, help="CPU baseline budget (about a tenth per figure)")
     ap.add_argument("--pmc", action="store_true", help="light mode for rocprofv3 --pmc runs")
     ap.add_argument("--pmc-workload", choices=["m1", "m8", "prefill", "prefill_iq3s", "head"], default="m1",
                     help="workload of the --pmc light mode")
@@ -245,6 +245,17 @@ def main():
              "frac_of_peak_selected_m1": round(value / HBM_PEAK_GBS, 4), "per_kernel_m1": per_kernel}
     del wss
 
+    # host copies of one instance of each config and the GPU's outputs on it,
+    # for the CPU baseline leg at the end (which times the reference's CPU
+    # path structure on the same weights and checks it against the GPU)
+    cpu_in = {}
+    h = lambda t: t.detach().cpu().numpy()  # noqa: E731
+    if not args.no_cpu:
+        L0 = layers[0]
+        o3 = L0.forward(xs[0])
+        cpu_in["c3"] = ([h(t) for t in L0.tensors[:4]], tuple(h(t) for t in L0.tensors[6:9]), h(xs[0]), h(o3), Q4_0,
+                        Q4_0)
+
     if not args.no_extra:
         # ---------------- config 4: M=8, IQ3_S experts + Q8_0 shared, uniform and Zipf routing
         rng = np.random.default_rng(5)
@@ -264,6 +275,10 @@ def main():
             for i in range(32):
                 l8[i % R8].forward(x8[i], out=o8, ids=ids, wts=torch.empty(8, K, device=dev))
                 uniq.append(len(set(ids.cpu().numpy().reshape(-1).tolist())))
+            if bias is None and not args.no_cpu:
+                o8c = l8[0].forward(x8[0])
+                cpu_in["c4"] = ([h(t) for t in l8[0].tensors[:4]], tuple(h(t) for t in l8[0].tensors[6:9]), h(x8[0]),
+                                h(o8c), IQ3_S, Q8_0)
             fns = [(lambda i=i: l8[i % R8].forward(x8[i % 32], out=o8)) for i in range(96)]
             t8, _ = graph_time(fns)
             us8 = t8 / 96 * 1e6
@@ -307,6 +322,9 @@ def main():
         for lyr in lp:
             lyr.prefill(xp, out=op, ids=ids, wts=torch.empty(T, K, device=dev))
         ue = len(set(ids.cpu().numpy().reshape(-1).tolist()))
+        if not args.no_cpu:
+            cpu_in["c5"] = ([h(t) for t in lp[1].tensors[:4]], tuple(h(t) for t in lp[1].tensors[6:9]), h(xp[:16]),
+                            h(op[:16]), Q4_0, Q4_0)
         fns = [(lambda i=i: lp[i % 2].prefill(xp, out=op)) for i in range(16)]
         tp, _ = graph_time(fns)
         upf = tp / 16
@@ -351,6 +369,9 @@ def main():
         hb = V * row_bytes(Q4_0, H) + V * 4 + (H // 32) * 36
         extra["head_q4_0_151936x2048"] = {"us": round(th / 30 * 1e6, 2), "GBs": round(hb / (th / 30) / 1e9, 1),
                                           "frac": round(hb / (th / 30) / 1e9 / HBM_PEAK_GBS, 4)}
+        if not args.no_cpu:
+            G.ggml_gpu_gemv_q4_0_q8(heads[0], xq, y, V, H)
+            cpu_in["c2"] = (h(heads[0]), h(xq), h(y), Q4_0, V)
         del heads
         # ---------------- config 1: Q8_0 4096 x 2048, 64 copies rotated (570 MB)
         q8w = qmat(Q8_0, 4096, H, 64, g)
@@ -359,6 +380,9 @@ def main():
         t1, _ = graph_time(fns)
         b1 = 4096 * row_bytes(Q8_0, H) + 4096 * 4 + (H // 32) * 36
         extra["dense_q8_0_4096x2048"] = {"us": round(t1 / 256 * 1e6, 2), "GBs": round(b1 / (t1 / 256) / 1e9, 1)}
+        if not args.no_cpu:
+            G.ggml_gpu_gemv_q8_0_q8(q8w[0], xq, y1, 4096, H)
+            cpu_in["c1"] = (h(q8w[0]), h(xq), h(y1), Q8_0, 4096)
         del q8w
         # ---------------- ggml K-quant / MXFP4 GEMV, 16384 x 4096, four copies rotated (timing
         # only: random block bytes)
@@ -403,28 +427,60 @@ def main():
                                "method": "2 GiB non-temporal dwordx4 read, best of 1024-8192 work-groups; "
                                          "1024 WGs x 4 waves x 4 chains of v_mfma_i32_32x32x32_i8"}
 
-    # ---------------- CPU baseline: the oracle (C restatement, OpenMP) on this host, M=1 Q4_0 layer
+    # ---------------- CPU baseline: the reference's CPU path structure
+    # (oracle/cpu_path.c: Q8_1 activations once per call, OpenMP row-parallel
+    # AVX2 vec_dots, cs/ffi/ggml_iq3s_gemv.c:84-127) on this host, for each
+    # config, with all host threads of this GPU's share and with one thread;
+    # each figure is the median call time over a bounded sample
     cpu = None
     if not args.no_cpu:
         import oracle as O
-        L = layers[0]
-        h = lambda t: t.cpu().numpy()  # noqa: E731
-        hw = [h(t) for t in L.tensors[:4]]
-        hsh = tuple(h(t) for t in L.tensors[6:9])
-        nthreads = min(16, os.cpu_count() or 1)
-        xh = h(xs[:, 0])
-        O.moe(xh[0:1], *hw, O.Q4_0, K, sh=hsh, sh_type=O.Q4_0, nthreads=nthreads)   # warm
-        n, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < args.cpu_seconds and n < 2000:
-            O.moe(xh[n % NSLOT:n % NSLOT + 1], *hw, O.Q4_0, K, sh=hsh, sh_type=O.Q4_0, nthreads=nthreads)
-            n += 1
-        dt = (time.perf_counter() - t0) / n
-        # single-thread figure on a shorter sample
-        n1, t1c = 0, time.perf_counter()
-        while time.perf_counter() - t1c < max(1.0, args.cpu_seconds / 4) and n1 < 500:
-            O.moe(xh[n1 % NSLOT:n1 % NSLOT + 1], *hw, O.Q4_0, K, sh=hsh, sh_type=O.Q4_0, nthreads=1)
-            n1 += 1
-        dt1 = (time.perf_counter() - t1c) / n1
+        nthr = min(16, os.cpu_count() or 1)
+
+        def ctime(fn, budget=args.cpu_seconds / 10):
+            fn()
+            ts, t_end = [], time.perf_counter() + budget
+            while len(ts) < 3 or (time.perf_counter() < t_end and len(ts) < 200):
+                t0 = time.perf_counter()
+                fn()
+                ts.append(time.perf_counter() - t0)
+            return float(np.median(ts)), len(ts)
+
+        def rel(a, b):
+            return float(np.linalg.norm(np.ravel(a) - np.ravel(b)) / max(np.linalg.norm(np.ravel(b)), 1e-30))
+
+        configs = {}
+        for key, name in (("c1", "config1_dense_q8_0_4096x2048"), ("c2", "config2_head_q4_0_151936x2048")):
+            if key not in cpu_in:
+                continue
+            W, xqh, yg, t, R = cpu_in[key]
+            rec = {}
+            for tag, n in (("threads", nthr), ("single_thread", 1)):
+                dt, calls = ctime(lambda: O.cpu_gemv(t, W, xqh, H, R, nthreads=n))
+                rec[tag] = {"n": n, "us": round(dt * 1e6, 1), "GBs": round((W.size + R * 4 + xqh.size) / dt / 1e9, 2),
+                            "calls": calls}
+            rec["rel_err_vs_gpu"] = rel(O.cpu_gemv(t, W, xqh, H, R, nthreads=nthr), yg)
+            configs[name] = rec
+        for key, name, M in (("c3", "config3_moe_m1_q4_0", 1), ("c4", "config4_moe_m8_iq3s_uniform", 8),
+                             ("c5", "config5_prefill_q4_0_sample16", 16)):
+            if key not in cpu_in:
+                continue
+            (r_, gt, ut, dt_), sh, xh, og, et, st = cpu_in[key]
+            xh = xh.reshape(-1, H)[:M]
+            run = lambda n: O.cpu_moe(xh, r_, gt, ut, dt_, et, K, sh=sh, sh_type=st, nthreads=n)  # noqa: E731
+            rec = {"tokens": M}
+            for tag, n in (("threads", nthr), ("single_thread", 1)):
+                dtm, calls = ctime(lambda: run(n))
+                ent = {"n": n, "us_per_call": round(dtm * 1e6, 1), "calls": calls}
+                if key == "c3":
+                    ent["GBs_selected"] = round(sel_bytes / dtm / 1e9, 3)
+                else:
+                    ent["tokens_per_s"] = round(M / dtm, 1)
+                rec[tag] = ent
+            oc, _, _ = run(nthr)
+            rec["rel_err_vs_gpu"] = max(rel(oc[m], og.reshape(-1, H)[m]) for m in range(M))
+            configs[name] = rec
+        c3 = configs.get("config3_moe_m1_q4_0")
         model = ""
         try:
             for ln in open("/proc/cpuinfo"):
@@ -433,10 +489,13 @@ def main():
                     break
         except OSError:
             pass
-        cpu = {"value": round(sel_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
-               "sample": f"{n} M=1 Q4_0 MoE layer calls of config 3 (oracle/oracle.c, OpenMP row-parallel), "
-                         f"{dt * 1e6:.0f} us/layer",
-               "single_thread_GBs": round(sel_bytes / dt1 / 1e9, 3), "nproc": os.cpu_count(), "cpu_model": model}
+        cpu = {"value": c3["threads"]["GBs_selected"], "unit": "GB/s", "cores": nthr, "kind": "port",
+               "sample": f"config 3 (M=1 Q4_0 MoE layer) on the CPU path restatement oracle/cpu_path.c "
+                         f"({c3['threads']['calls']} calls, median {c3['threads']['us_per_call']} us/layer); "
+                         f"configs 1-5 in 'configs' (config 5: 16 tokens of the 512-token chunk, one token at a "
+                         f"time as the reference's prefill does)",
+               "single_thread_GBs": c3["single_thread"]["GBs_selected"], "nproc": os.cpu_count(),
+               "cpu_model": model, "configs": configs}
 
     if args.calib_copy_mb:
         src = torch.empty(args.calib_copy_mb << 18, dtype=torch.float32, device=dev).fill_(1.0)

@@ -47,6 +47,8 @@ def lib():
         L.orc_router.argtypes = [vp, vp, vp, i32, i32]
         L.orc_topk_softmax.argtypes = [vp, i32, i32, vp, vp]
         L.orc_moe.argtypes = [vp, vp, vp, vp, vp, i32]
+        L.cpb_gemv.argtypes = [i32, vp, vp, vp, i32, i32, i32]
+        L.cpb_moe.argtypes = [vp, vp, vp, vp, vp, i32]
         _LIB = L
     return _LIB
 
@@ -155,7 +157,7 @@ class _MoeParams(_C.Structure):
 
 
 def moe(x, router_w, gate, up, down, exp_type, K, sh=None, sh_type=-1, sh_gate_w=None,
-        logit_bias=None, L=16, G=1, nthreads=0):
+        logit_bias=None, L=16, G=1, nthreads=0, fn="orc_moe"):
     """MoE FFN for x [M, H]; gate/up [E, F*rowbytes(H)] down [E, H*rowbytes(F)]
     (uint8, one row per expert).  sh = (gate, up, down) or None.
     Returns (out [M,H], ids [M,K], wts [M,K])."""
@@ -181,5 +183,18 @@ def moe(x, router_w, gate, up, down, exp_type, K, sh=None, sh_type=-1, sh_gate_w
     out = np.zeros((M, H), np.float32)
     ids = np.zeros((M, K), np.int32)
     wts = np.zeros((M, K), np.float32)
-    lib().orc_moe(_C.byref(p), _p(x), _p(out), _p(ids), _p(wts), nthreads)
+    getattr(lib(), fn)(_C.byref(p), _p(x), _p(out), _p(ids), _p(wts), nthreads)
     return out, ids, wts
+
+
+def cpu_moe(*args, nthreads=1, **kw):
+    """The CPU baseline (cpu_path.c): same arguments and results as moe(),
+    to the fp32 tolerance."""
+    return moe(*args, nthreads=nthreads, fn="cpb_moe", **kw)
+
+
+def cpu_gemv(t, W, xq, ncols, nrows, nthreads=1):
+    """CPU baseline GEMV of one Q8_1 row (cpu_path.c)."""
+    y = np.zeros(nrows, np.float32)
+    lib().cpb_gemv(t, _p(np.ascontiguousarray(W)), _p(np.ascontiguousarray(xq)), _p(y), ncols, nrows, nthreads)
+    return y

@@ -96,6 +96,13 @@ typedef struct {
 void orc_moe(const orc_moe_params *p, const float *x, float *out,
              int32_t *ids, float *wts, int nthreads);
 
+/* CPU baseline (cpu_path.c): the reference's CPU path structure with AVX2
+ * vec_dots (Q8_0 / Q4_0 / IQ3_S weights, Q8_1 activations), OpenMP
+ * row-parallel with nthreads threads; agrees with the oracle to the fp32
+ * tolerance, not bit for bit. */
+void cpb_gemv(int type, const uint8_t *W, const uint8_t *xq, float *y, int ncols, int nrows, int nthreads);
+void cpb_moe(const orc_moe_params *p, const float *x, float *out, int32_t *ids, float *wts, int nthreads);
+
 #ifdef __cplusplus
 }
 #endif
