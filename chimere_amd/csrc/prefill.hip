@@ -235,11 +235,44 @@ __device__ __forceinline__ void pf_sb(const uint8_t* row, PfSb& f) {
     }
 }
 
+template <int T>
+constexpr bool pf_kq() { return T == T_Q4_K || T == T_Q5_K; }
+
+// K-quant superblock fields of block b (Q4_K / Q5_K, 4-byte aligned LDS row):
+// f32(dmin) and the 6-bit min m of sub-block b (gguf_loader.rs:1150-1163)
+struct PfMin {
+    float dm;
+    int m;
+};
+
 template <int T, bool PRE>
 __device__ __forceinline__ long pf_b_frag(const uint8_t* row, int b, int q, uint32_t* dw, int* mult,
-                                          const uint32_t* grid, const PfSb& f) {
+                                          const uint32_t* grid, const PfSb& f, PfMin* mn = nullptr) {
     uint32_t lo, hi;
-    if constexpr (T == T_IQ3_S) {
+    if constexpr (pf_kq<T>()) {
+        // sub-block b of the superblock [f16 d][f16 dmin][scales 12]([qh 32])[qs 128]:
+        // lane group q holds elements 8q .. 8q+7 = nibble (b & 1) of qs[32 (b/2) + l]
+        // (Q5_K: plus bit b of qh[l] as bit 4), unsigned; the MFMA gives
+        // sum q * q_x, the scale multiplies it and the min term is added apart
+        const uint32_t* u = (const uint32_t*)row;
+        const uint32_t w0 = u[0];
+        *dw = w0 & 0xFFFFu;
+        int sc, m;
+        kq_scale_min(u[1], u[2], u[3], b, sc, m);
+        *mult = sc;
+        mn->dm = h2f(w0 >> 16);
+        mn->m = m;
+        constexpr int QS = T == T_Q5_K ? 48 : 16;
+        const uint32_t* qs = (const uint32_t*)(row + QS + 32 * (b >> 1) + 8 * q);
+        const int sh = 4 * (b & 1);
+        lo = (qs[0] >> sh) & 0x0F0F0F0Fu;
+        hi = (qs[1] >> sh) & 0x0F0F0F0Fu;
+        if constexpr (T == T_Q5_K) {
+            const uint32_t* qh = (const uint32_t*)(row + 16 + 8 * q);
+            lo |= ((qh[0] >> b) & 0x01010101u) << 4;
+            hi |= ((qh[1] >> b) & 0x01010101u) << 4;
+        }
+    } else if constexpr (T == T_IQ3_S) {
         // sub-block b of the superblock [f16 d][qs 64][qh 8][signs 32][scales 4];
         // lane group q holds elements 8q .. 8q+7: grid entries qs[8b+2q] and
         // qs[8b+2q+1] with high bits 2q and 2q+1 of qh[b], negated per byte by
@@ -275,6 +308,7 @@ __device__ __forceinline__ long pf_b_frag(const uint8_t* row, int b, int q, uint
     (void)mult;
     (void)grid;
     (void)f;
+    (void)mn;
     return (long)(((uint64_t)hi << 32) | lo);
 }
 
@@ -327,7 +361,9 @@ __device__ __forceinline__ void pf_mma_chunk(const uint8_t* xl, const float* xd,
     // b-1's results are rescaled, so the MFMA latency overlaps VALU work
     v4i r[NTN], rp[NTN];
     float dw[NTN], dwp[NTN];
-    int mu[NTN], mup[NTN];   // IQ3_S sub-block factors
+    int mu[NTN], mup[NTN];   // IQ3_S / K-quant sub-block factors
+    PfMin mn[NTN], mnp[NTN];   // K-quant min terms
+    int4 sqp;                  // K-quant: sum of the pairs' quants of the previous block
     PfSb sb[NTN];
 #pragma unroll
     for (int n = 0; n < NTN; n++)
@@ -344,13 +380,14 @@ __device__ __forceinline__ void pf_mma_chunk(const uint8_t* xl, const float* xd,
 #pragma unroll
             for (int n = 0; n < NTN; n++) {
                 uint32_t dwb;
-                const long bf = pf_b_frag<T, PRE>(wrows + (16 * n + c) * cbytes, b, q, &dwb, &mu[n], grid, sb[n]);
+                const long bf =
+                    pf_b_frag<T, PRE>(wrows + (16 * n + c) * cbytes, b, q, &dwb, &mu[n], grid, sb[n], &mn[n]);
                 dw[n] = h2f(dwb);
                 r[n] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bf, c0, 0, 0, 0);
             }
         }
         if (b > 0) {
-            if constexpr (T == T_IQ3_S) {
+            if constexpr (T == T_IQ3_S || pf_kq<T>()) {
 #pragma unroll
                 for (int n = 0; n < NTN; n++)
 #pragma unroll
@@ -362,11 +399,25 @@ __device__ __forceinline__ void pf_mma_chunk(const uint8_t* xl, const float* xd,
                 acc[n][1] = __builtin_fmaf(dwp[n] * dxp.y, (float)rp[n][1], acc[n][1]);
                 acc[n][2] = __builtin_fmaf(dwp[n] * dxp.z, (float)rp[n][2], acc[n][2]);
                 acc[n][3] = __builtin_fmaf(dwp[n] * dxp.w, (float)rp[n][3], acc[n][3]);
+                if constexpr (pf_kq<T>()) {
+                    // the min term of the block: fmaf(-(f32(dmin) * f32(d_x)), (float)(m * sum q_x), acc)
+                    acc[n][0] = __builtin_fmaf(-(mnp[n].dm * dxp.x), (float)__mul24(mnp[n].m, sqp.x), acc[n][0]);
+                    acc[n][1] = __builtin_fmaf(-(mnp[n].dm * dxp.y), (float)__mul24(mnp[n].m, sqp.y), acc[n][1]);
+                    acc[n][2] = __builtin_fmaf(-(mnp[n].dm * dxp.z), (float)__mul24(mnp[n].m, sqp.z), acc[n][2]);
+                    acc[n][3] = __builtin_fmaf(-(mnp[n].dm * dxp.w), (float)__mul24(mnp[n].m, sqp.w), acc[n][3]);
+                }
             }
         }
 #pragma unroll
-        for (int n = 0; n < NTN; n++) { rp[n] = r[n]; dwp[n] = dw[n]; mup[n] = mu[n]; }
+        for (int n = 0; n < NTN; n++) { rp[n] = r[n]; dwp[n] = dw[n]; mup[n] = mu[n]; mnp[n] = mn[n]; }
         dxp = dx;
+        if constexpr (pf_kq<T>()) {
+            // sum q_x = -(xs8 / 8) of the block just issued (xs8 = -8 * sum q_x)
+            if (b < nb) {
+                const int4 s8 = *(const int4*)(xs8 + b * PF_TILE + 4 * q);
+                sqp = make_int4(-(s8.x >> 3), -(s8.y >> 3), -(s8.z >> 3), -(s8.w >> 3));
+            }
+        }
     }
 }
 
@@ -488,11 +539,12 @@ constexpr int PF_XST = PF_TILE * PF_CHUNK * 36;
     __shared__ __attribute__((aligned(16))) int xs0[PF_TILE * PF_CHUNK], xs1[PF_TILE * PF_CHUNK];     \
     const PfStage s0{wl0, xl0, xd0, xs0}, s1{wl1, xl1, xd1, xs1}
 
-// A Q8_0 shared expert next to narrower expert rows (Q4_0 / IQ3_S experts)
-// runs on one stage, so that the second stage is sized for the experts'
-// chunk rows (two stages of 128 Q8_0 chunk rows leave one work-group per CU)
+// A Q8_0 or K-quant shared expert next to narrower expert rows (Q4_0 / IQ3_S
+// experts) runs on one stage, so that the second stage is sized for the
+// experts' chunk rows (two stages of 128 Q8_0 chunk rows leave one work-group
+// per CU)
 template <int TE, int TS>
-constexpr bool pf_sh_one() { return TS == T_Q8_0 && TE != T_Q8_0; }
+constexpr bool pf_sh_one() { return (TS == T_Q8_0 || pf_kq<TS>()) && TE != TS; }
 template <int TE, int TS>
 constexpr int pf_ws0(int nrows) { return pf_wst<TE>(nrows) > pf_wst<TS>(nrows) ? pf_wst<TE>(nrows) : pf_wst<TS>(nrows); }
 template <int TE, int TS>
@@ -690,9 +742,11 @@ void chimere_moe_prefill(const chimere_moe_layer* L, const float* x, float* out,
                     "moe_prefill: n_experts=%d top_k=%d out of range", E, K);
     const bool has_sh = L->shared_type >= 0;
     auto pf_type = [](int t) { return t == T_Q4_0 || t == T_Q8_0 || t == T_IQ3_S; };
-    CHIMERE_REQUIRE(pf_type(L->expert_type) && (!has_sh || pf_type(L->shared_type)), CHIMERE_ERR_ARG,
-                    "moe_prefill: Q4_0 / Q8_0 / IQ3_S weights only (expert %d, shared %d)", L->expert_type,
-                    L->shared_type);
+    CHIMERE_REQUIRE(pf_type(L->expert_type) &&
+                        (!has_sh || pf_type(L->shared_type) || L->shared_type == T_Q4_K || L->shared_type == T_Q5_K),
+                    CHIMERE_ERR_ARG,
+                    "moe_prefill: Q4_0 / Q8_0 / IQ3_S experts, shared expert also Q4_K / Q5_K (expert %d, shared %d)",
+                    L->expert_type, L->shared_type);
     CHIMERE_REQUIRE(!has_sh || (L->sh_gate && L->sh_up && L->sh_down), CHIMERE_ERR_ARG,
                     "moe_prefill: shared expert incomplete");
     CHIMERE_REQUIRE(L->router_w && L->gate_exps && L->up_exps && L->down_exps, CHIMERE_ERR_ARG,
@@ -727,6 +781,8 @@ void chimere_moe_prefill(const chimere_moe_layer* L, const float* x, float* out,
         constexpr int TE = decltype(te_tag)::value;
         if (ts == T_Q4_0) launch_pf<TE, T_Q4_0>(a, p, stream);
         else if (ts == T_Q8_0) launch_pf<TE, T_Q8_0>(a, p, stream);
+        else if (ts == T_Q4_K) launch_pf<TE, T_Q4_K>(a, p, stream);
+        else if (ts == T_Q5_K) launch_pf<TE, T_Q5_K>(a, p, stream);
         else launch_pf<TE, T_IQ3_S>(a, p, stream);
     };
     if (te == T_Q4_0) with_ts(std::integral_constant<int, T_Q4_0>{});

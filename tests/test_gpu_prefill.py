@@ -12,7 +12,8 @@ import pytest
 import torch
 
 import oracle as O
-from test_gpu_moe import build, check_margin, host, oracle_run
+from chimere_amd.moe import MoeLayer
+from test_gpu_moe import build, check_margin, host, oracle_run, qmat
 
 pytestmark = pytest.mark.gpu
 
@@ -112,3 +113,41 @@ def test_prefill_repeat_and_zero(dev):
         assert (host(layer.prefill(x[:T].contiguous())) == first[:T]).all()
     z = host(layer.prefill(torch.zeros(4, 1024, device=dev)))
     assert np.isfinite(z).all()
+
+
+def kq_layer(dev, seed, et, st, H, F, E, K, gate_vec=True):
+    """Experts of type et (device quantizer), a K-quant shared expert of type
+    st from the independent packer (valid random blocks)."""
+    import npref
+    g = torch.Generator(device=dev).manual_seed(seed)
+    router = torch.randn(E, H, generator=g, device=dev) * 0.02
+    gate, up, down = qmat(et, F, H, E, g, dev), qmat(et, F, H, E, g, dev), qmat(et, H, F, E, g, dev)
+    rng = np.random.default_rng(seed)
+    sh = tuple(torch.from_numpy(np.ascontiguousarray(npref.rand_kq(st, r, c, rng).reshape(-1))).to(dev)
+               for r, c in ((F, H), (F, H), (H, F)))
+    gw = torch.randn(H, generator=g, device=dev) * 0.02 if gate_vec else None
+    return MoeLayer(router, gate, up, down, et, K, shared=sh, shared_type=st, sh_gate_w=gw)
+
+
+@pytest.mark.parametrize("et,st,H,F,E,K,T", [
+    (O.Q4_0, O.Q5_K, 1024, 256, 32, 4, 37),
+    (O.Q8_0, O.Q4_K, 1024, 256, 16, 8, 20),
+    (O.IQ3_S, O.Q5_K, 1024, 256, 64, 8, 9),
+])
+def test_prefill_kquant_shared_small(dev, et, st, H, F, E, K, T):
+    """K-quant shared expert on the MFMA path (scale on the int32 result, the
+    min term added per block), bit-exact against the oracle's L=1 order."""
+    print(f"prefill kquant shared et={et} st={st} H={H} F={F} E={E} K={K} T={T}", flush=True)
+    layer = kq_layer(dev, 800 + et + st + T, et, st, H, F, E, K)
+    g = torch.Generator(device=dev).manual_seed(T)
+    prefill_check(layer, torch.randn(T, H, generator=g, device=dev))
+
+
+def test_prefill_model_layer_types_full_shape(dev):
+    """The reference model's layer types at its shape: IQ3_S experts (H=2048,
+    F=512, E=256, top-8) with the Q5_K shared expert and its sigmoid gate,
+    96 tokens, every token bit-exact against the oracle."""
+    print("prefill IQ3_S + Q5_K shared, full shape, 96 tokens", flush=True)
+    layer = kq_layer(dev, 880, O.IQ3_S, O.Q5_K, 2048, 512, 256, 8)
+    g = torch.Generator(device=dev).manual_seed(88)
+    prefill_check(layer, torch.randn(96, 2048, generator=g, device=dev))
