@@ -746,6 +746,19 @@ __device__ __forceinline__ int wave_max_nonneg(int v) {
     return __builtin_amdgcn_readlane(v, 63);
 }
 
+// Inclusive prefix sum of a non-negative int over the wave (Hillis-Steele:
+// row_shr 1, 2, 4, 8 inside each 16-lane row, then row_bcast 15 / 31 carry
+// the row totals forward).
+__device__ __forceinline__ int wave_incl_scan(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);   // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);   // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);   // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);   // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);   // row_bcast:15
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);   // row_bcast:31
+    return v;
+}
+
 // Sum over the 16 lanes of a row group in the halving-tree order
 // (xor 8, 4, 2, 1); every lane of the group ends with the same value.
 __device__ __forceinline__ float slot_reduce16(float v) {

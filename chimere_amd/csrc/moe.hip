@@ -159,13 +159,13 @@ __device__ __forceinline__ void down_terms(const RegBlk<T> (&rb)[EX_MAX_RPT], co
 // `first` is LDS scratch of E ints.  With `publish`, the routing weights
 // (and ids_out / w_out) and the plan are written to global memory.
 __device__ __forceinline__ void route_plan(const MoeArgs& a, int* first, Plan& pl, int* s_ids, float* s_w,
-                                           bool publish) {
+                                           bool publish, uint64_t (*tk)[128]) {
     const int tid = threadIdx.x;
     const int MK = a.M * a.K;
 
     const int wave = tid >> 6;
     if (wave < a.M)
-        topk_wave_any(a.logits + wave * a.E, a.E, a.K, s_ids + wave * a.K, s_w + wave * a.K);
+        topk_wave_any(a.logits + wave * a.E, a.E, a.K, s_ids + wave * a.K, s_w + wave * a.K, tk[wave]);
     if (a.M == 1) {
         // one token: its K experts are distinct; unit k = the k-th selected
         __syncthreads();
@@ -320,11 +320,12 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert(MoeArgs a) {
     __shared__ int s_ids[MAX_TOK * MAX_K];
     __shared__ float s_w[MAX_TOK * MAX_K];
     __shared__ Plan pl;
+    __shared__ uint64_t s_tk[NT][128];
 
     const int NB = a.F / QK;
     const int MK = a.M * a.K;
     const int tid = threadIdx.x;
-    route_plan(a, (int*)tile, pl, s_ids, s_w, blockIdx.x == 0);
+    route_plan(a, (int*)tile, pl, s_ids, s_w, blockIdx.x == 0, s_tk);
     if constexpr (TE == T_IQ3_S || TS == T_IQ3_S)
         for (int i = tid; i < 512; i += EX_THREADS) grid[i] = c_iq3s_grid_moe[i];
     // Items of XCD x (work-groups b with b % 8 == x): the row blocks of the
@@ -555,6 +556,7 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert1(MoeArgs a) {
     __shared__ float hg[1][QK], hu[1][QK];
     __shared__ int s_ids[MAX_K];
     __shared__ float s_w[MAX_K];
+    __shared__ uint64_t s_tk[128];
     const int tid = threadIdx.x, wave = tid >> 6;
     const int NB = a.F / QK, nbH = a.H / QK;
     const int x = blockIdx.x & 7, lb = blockIdx.x >> 3, G8 = gridDim.x >> 3;
@@ -570,7 +572,7 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert1(MoeArgs a) {
     if (!shared) {
         // wave 0: softmax / top-k; the other waves decode Q8_1(x) meanwhile
         if (wave == 0) {
-            topk_wave_any(a.logits, a.E, a.K, s_ids, s_w);
+            topk_wave_any(a.logits, a.E, a.K, s_ids, s_w, s_tk);
             if (blockIdx.x == 0 && tid < a.K) {
                 a.wts[tid] = s_w[tid];
                 a.plan[PLAN_UEXP + tid] = s_ids[tid];
@@ -813,7 +815,8 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_plan(MoeArgs a) {
     __shared__ Plan pl;
     __shared__ int s_ids[MAX_TOK * MAX_K];
     __shared__ float s_w[MAX_TOK * MAX_K];
-    route_plan(a, first, pl, s_ids, s_w, true);
+    __shared__ uint64_t s_tk[MAX_TOK][128];
+    route_plan(a, first, pl, s_ids, s_w, true, s_tk);
 }
 
 // unit u of the published plan (u == M*K: the shared expert); false if none
@@ -1167,8 +1170,9 @@ __global__ __launch_bounds__(256) void k_f32_gemv(const float* A, const float* x
 }
 
 __global__ __launch_bounds__(64) void k_topk(const float* logits, int* idx, float* w, int E, int K) {
+    __shared__ uint64_t s_tk[128];
     const int t = blockIdx.x;
-    topk_wave_any(logits + (int64_t)t * E, E, K, idx + t * K, w + t * K);
+    topk_wave_any(logits + (int64_t)t * E, E, K, idx + t * K, w + t * K, s_tk);
 }
 
 __global__ void k_silu_mul(float* g, const float* u, int n) {

@@ -85,6 +85,112 @@ __device__ __forceinline__ void f32_row_dot(const float* __restrict__ a, const f
 
 // ---------------------------------------------------------------- top-k
 
+// Fast exact selection of the K largest of 4 keys per lane (E <= 256,
+// K <= 16), wave-local through `sc` (128 u64 of LDS owned by this wave; a
+// wave's LDS accesses complete in issue order, so no barrier is needed).
+// Composite c = key << 32 | ~index orders entries as the k rounds of arg-max
+// do (larger p first, lower index on equal p); all composites differ.
+//  1. candidates: the entries with key >= a threshold, the largest of four
+//     fractions of the top probability for which at least K entries pass
+//     (the four counts are kept in two packed lane values and summed over
+//     the wave by butterflies); every entry above a candidate is a candidate,
+//     so a candidate's round is the number of candidates above it;
+//  2. the n candidates (K <= n <= 64) are compacted into sc[64..64+n) at
+//     offsets from a prefix sum of the lanes' candidate counts (the rest of
+//     sc[64..128) is zero, below every composite), and lane l < n counts the
+//     candidates above candidate l;
+//  3. the candidate of round r is written to sc[r]; lane k < K takes round
+//     k and every lane sums rounds 0..K-1 in order (the renormalisation sum).
+// The single-lane steps of the k rounds of arg-max (maximum, ballot, scalar
+// round trips) are what make those slow on one wave; this path has none in
+// its chain except the three butterfly / scan reductions.
+// Returns false (nothing written) when no threshold leaves between K and 64
+// candidates (e.g. many exactly equal probabilities): the caller then runs
+// the k rounds of arg-max.  Otherwise lane k < K gets round k's index and
+// renormalised weight in my_idx / my_w.
+__device__ __forceinline__ bool topk4_select(const uint32_t (&key)[4], uint32_t kmax, int K, uint64_t* sc,
+                                             int& my_idx, float& my_w) {
+    const int lane = threadIdx.x & 63;
+    const float pmax = __builtin_bit_cast(float, kmax - 1u);
+    uint32_t kt[4];
+    kt[0] = __builtin_bit_cast(uint32_t, pmax * 0.6f) + 1u;
+    kt[1] = __builtin_bit_cast(uint32_t, pmax * 0.4f) + 1u;
+    kt[2] = __builtin_bit_cast(uint32_t, pmax * 0.25f) + 1u;
+    kt[3] = __builtin_bit_cast(uint32_t, pmax * 0.1f) + 1u;
+    // per-lane counts of the four thresholds, two 16-bit fields per int
+    int pa = 0, pb = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        pa += (key[i] >= kt[0] ? 1 : 0) + (key[i] >= kt[1] ? 1 << 16 : 0);
+        pb += (key[i] >= kt[2] ? 1 : 0) + (key[i] >= kt[3] ? 1 << 16 : 0);
+    }
+    int ta = pa, tb = pb;
+    ta += xlane<1>(ta); tb += xlane<1>(tb);
+    ta += xlane<2>(ta); tb += xlane<2>(tb);
+    ta += xlane<4>(ta); tb += xlane<4>(tb);
+    ta += xlane<8>(ta); tb += xlane<8>(tb);
+    ta += xlane<16>(ta); tb += xlane<16>(tb);
+    ta += xlane<32>(ta); tb += xlane<32>(tb);
+    const int c0 = ta & 0xFFFF, c1 = ta >> 16, c2 = tb & 0xFFFF, c3 = tb >> 16;
+    const int t = c0 >= K ? 0 : (c1 >= K ? 1 : (c2 >= K ? 2 : 3));
+    const int n = t == 0 ? c0 : (t == 1 ? c1 : (t == 2 ? c2 : c3));
+    if (n < K || n > 64) return false;
+    const uint32_t thr = kt[t];
+    const int mine_n = ((t < 2 ? pa : pb) >> (t & 1 ? 16 : 0)) & 0xFFFF;
+    int off = wave_incl_scan(mine_n) - mine_n;
+    sc[64 + lane] = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if (key[i] >= thr) {
+            sc[64 + off] = ((uint64_t)key[i] << 32) | (uint32_t)~(uint32_t)(lane + 64 * i);
+            off++;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const ulonglong2* c2p = (const ulonglong2*)(sc + 64);
+    const uint64_t mine = sc[64 + lane];
+    int r0 = 0, r1 = 0;
+    for (int j0 = 0; j0 < n; j0 += 8) {   // chunks of 8 candidates (the zeros past n count nothing)
+        ulonglong2 v[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[j] = c2p[j0 / 2 + j];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            r0 += v[j].x > mine ? 1 : 0;
+            r1 += v[j].y > mine ? 1 : 0;
+        }
+    }
+    const int rank = r0 + r1;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < n && rank < K) sc[rank] = mine;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float ws = 0.0f, w = 0.0f;
+    int id = 0;
+    for (int k0 = 0; k0 < K; k0 += 8) {
+        uint64_t r[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) r[k] = sc[k0 + k];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            if (k0 + k < K) {
+                const float p = __builtin_bit_cast(float, (uint32_t)(r[k] >> 32) - 1u);
+                ws += p;
+                if (k0 + k == lane) { w = p; id = (int)~(uint32_t)r[k]; }
+            }
+        }
+    }
+    my_idx = id;
+    my_w = ws > 0.0f ? w * (1.0f / ws) : w;
+    __builtin_amdgcn_wave_barrier();
+    return true;
+}
+
 // Softmax + top-k + renormalisation of one logits row by ONE wavefront, in
 // registers (cs/kernels/chimere_kernels.cu:1150-1223): lane l holds logits
 // l, l+64, ... (NV = ceil(E/64) values, zero-padded).  p = exp(l - max) / sum
@@ -98,9 +204,12 @@ __device__ __forceinline__ void f32_row_dot(const float* __restrict__ a, const f
 // holding it (ballots of key == max, slot by slot), and clears that entry.  Weights are
 // renormalised by the sequential sum of the selected probabilities (round
 // order).  Lane k < K writes entry k.  Requires E <= 1024, K <= min(E, 64).
+// With `sc` (128 u64 of the wave's LDS), 128 < E <= 256 and K <= 16, the
+// selection and renormalisation run as topk4_select above (same results).
 template <int NV>
 __device__ __forceinline__ void topk_wave(const float* __restrict__ logits, int E, int K,
-                                          int* __restrict__ idx_out, float* __restrict__ w_out) {
+                                          int* __restrict__ idx_out, float* __restrict__ w_out,
+                                          uint64_t* sc = nullptr) {
     const int lane = threadIdx.x & 63;
     float p[NV], ev[NV];
     float mx = -__builtin_huge_valf();
@@ -132,7 +241,12 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ logits, int 
     }
     int my_idx = 0;
     float my_w = 0.0f;
+    bool fast = false;
     if constexpr (NV == 4) {
+      // the top key: p_max = 1 / s (the maximum's exponential is exactly 1)
+      const uint32_t kmax = __builtin_bit_cast(uint32_t, s > 0.0f ? 1.0f / s : 1.0f / (float)E) + 1u;
+      fast = sc != nullptr && K <= 16 && topk4_select(key, kmax, K, sc, my_idx, my_w);
+      if (!fast) {
         // Each lane's keys sorted once, descending, equal keys by index (the
         // order (key, -index) is total, so any sorting network gives it).
         // A round is then a maximum over the lanes' heads: the winner is the
@@ -171,6 +285,7 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ logits, int 
             }
             if (lane == k) { my_idx = win; my_w = __builtin_bit_cast(float, (uint32_t)m - 1u); }
         }
+      }
     } else
     for (int k = 0; k < K; k++) {
         int m = (int)key[0];
@@ -196,12 +311,15 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ logits, int 
             if (lane + 64 * i == win) key[i] = 0u;
         if (lane == k) { my_idx = win; my_w = __builtin_bit_cast(float, (uint32_t)m - 1u); }
     }
-    float ws = 0.0f;
-    for (int k = 0; k < K; k++)
-        ws += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_w), k));
+    if (!fast) {
+        float ws = 0.0f;
+        for (int k = 0; k < K; k++)
+            ws += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_w), k));
+        my_w = ws > 0.0f ? my_w * (1.0f / ws) : my_w;
+    }
     if (lane < K) {
         idx_out[lane] = my_idx;
-        w_out[lane] = ws > 0.0f ? my_w * (1.0f / ws) : my_w;
+        w_out[lane] = my_w;
     }
 }
 
@@ -214,8 +332,11 @@ static __device__ __noinline__ void topk_wave_other(const float* logits, int E, 
     else topk_wave<16>(logits, E, K, idx, w);
 }
 
-__device__ __forceinline__ void topk_wave_any(const float* logits, int E, int K, int* idx, float* w) {
-    if (E > 128 && E <= 256) topk_wave<4>(logits, E, K, idx, w);
+// sc: 128 u64 of LDS owned by the calling wave (the fast selection for
+// 128 < E <= 256), or nullptr
+__device__ __forceinline__ void topk_wave_any(const float* logits, int E, int K, int* idx, float* w,
+                                              uint64_t* sc = nullptr) {
+    if (E > 128 && E <= 256) topk_wave<4>(logits, E, K, idx, w, sc);
     else topk_wave_other(logits, E, K, idx, w);
 }
 

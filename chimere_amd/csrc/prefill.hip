@@ -119,8 +119,9 @@ __global__ __launch_bounds__(256) void k_pf_router(PfArgs a) {
 
 // P2: one wave per token
 __global__ __launch_bounds__(64) void k_pf_topk(PfArgs a) {
+    __shared__ uint64_t s_tk[128];
     const int t = blockIdx.x;
-    topk_wave_any(a.logits + (int64_t)t * a.E, a.E, a.K, a.ids + t * a.K, a.wts + t * a.K);
+    topk_wave_any(a.logits + (int64_t)t * a.E, a.E, a.K, a.ids + t * a.K, a.wts + t * a.K, s_tk);
 }
 
 // exclusive prefix sum of one int per thread over a 1024-thread group

@@ -29,7 +29,8 @@ def _cases(E, seed):
     yield (rng.standard_normal(E) * 40).astype(np.float32)              # probabilities underflow to 0
 
 
-@pytest.mark.parametrize("E,K", [(256, 8), (256, 1), (256, 16), (200, 8), (64, 8), (8, 8), (512, 16), (1024, 8)])
+@pytest.mark.parametrize("E,K", [(256, 8), (256, 1), (256, 4), (256, 16), (200, 8), (130, 16), (64, 8), (8, 8),
+                                 (512, 16), (1024, 8)])
 def test_topk_softmax_ties(E, K):
     print(f"topk E={E} K={K}", flush=True)
     rows = list(_cases(E, E * 100 + K))
@@ -66,3 +67,25 @@ def test_device_exp_equals_oracle_over_softmax_range():
     for t in range(n):
         oi, ow = O.topk_softmax(logits[t], K)
         assert (gi[t] == oi).all() and (gw[t].view(np.uint32) == ow.view(np.uint32)).all(), t
+
+
+@pytest.mark.parametrize("E,K", [(256, 8), (256, 16), (256, 2), (160, 8)])
+def test_topk_softmax_many_tied_rows(E, K):
+    """2048 rows of logits on a coarse grid (many exact ties at every rank,
+    including the K-th) and 2048 of continuous logits, against the oracle."""
+    print(f"topk many rows E={E} K={K}", flush=True)
+    rng = np.random.default_rng(E * 7 + K)
+    n = 4096
+    logits = np.empty((n, E), np.float32)
+    logits[: n // 2] = rng.integers(-3, 4, (n // 2, E)).astype(np.float32) * 0.5
+    logits[n // 2:] = rng.standard_normal((n - n // 2, E)).astype(np.float32)
+    dl = torch.from_numpy(logits).cuda()
+    ids = torch.empty(n, K, dtype=torch.int32, device="cuda")
+    wts = torch.empty(n, K, dtype=torch.float32, device="cuda")
+    G.gpu_topk_softmax(dl, ids, wts, E, K, ntok=n)
+    torch.cuda.synchronize()
+    gi, gw = ids.cpu().numpy(), wts.cpu().numpy()
+    for t in range(n):
+        oi, ow = O.topk_softmax(logits[t], K)
+        assert (gi[t] == oi).all(), (t, gi[t], oi)
+        assert (gw[t].view(np.uint32) == ow.view(np.uint32)).all(), (t, gw[t], ow)
