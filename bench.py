@@ -453,13 +453,13 @@ def main():
         for key, name in (("c1", "config1_dense_q8_0_4096x2048"), ("c2", "config2_head_q4_0_151936x2048")):
             if key not in cpu_in:
                 continue
-            W, xqh, yg, t, R = cpu_in[key]
+            W, xqh, yg, t, nrows = cpu_in[key]
             rec = {}
             for tag, n in (("threads", nthr), ("single_thread", 1)):
-                dt, calls = ctime(lambda: O.cpu_gemv(t, W, xqh, H, R, nthreads=n))
-                rec[tag] = {"n": n, "us": round(dt * 1e6, 1), "GBs": round((W.size + R * 4 + xqh.size) / dt / 1e9, 2),
-                            "calls": calls}
-            rec["rel_err_vs_gpu"] = rel(O.cpu_gemv(t, W, xqh, H, R, nthreads=nthr), yg)
+                dt, calls = ctime(lambda: O.cpu_gemv(t, W, xqh, H, nrows, nthreads=n))
+                rec[tag] = {"n": n, "us": round(dt * 1e6, 1),
+                            "GBs": round((W.size + nrows * 4 + xqh.size) / dt / 1e9, 2), "calls": calls}
+            rec["rel_err_vs_gpu"] = rel(O.cpu_gemv(t, W, xqh, H, nrows, nthreads=nthr), yg)
             configs[name] = rec
         for key, name, M in (("c3", "config3_moe_m1_q4_0", 1), ("c4", "config4_moe_m8_iq3s_uniform", 8),
                              ("c5", "config5_prefill_q4_0_sample16", 16)):
