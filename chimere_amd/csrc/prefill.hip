@@ -470,24 +470,50 @@ __device__ __forceinline__ void pf_gemm_k(const PfStage& s0, const PfStage& s1, 
             __syncthreads();
         }
     } else {
+        // Each thread copies the same pieces of every chunk (piece cc of the
+        // loop below: weight row cc / PCB, column cc % PCB, or activation row
+        // r, column col): their source addresses are formed once here and a
+        // chunk only adds its byte offset.
+        constexpr int NIT = (TOT + PF_THREADS - 1) / PF_THREADS;
+        const uint8_t* psrc[NIT];
+        bool pval[NIT];
+        int pcol[NIT];   // column byte of a weight piece (used by the span clamp)
+#pragma unroll
+        for (int k = 0; k < NIT; k++) {
+            const int c0 = wave * 64 + k * PF_THREADS, cc = c0 + lane;
+            psrc[k] = nullptr;
+            pval[k] = false;
+            pcol[k] = 0;
+            if (c0 < TWP) {
+                if (cc < TW) {
+                    const int row = cc / PCB, col = cc - row * PCB;
+                    psrc[k] = (row < n0 ? w0 + row * rb : w1 + (row - n0) * rb) + col * 16;
+                    pcol[k] = col * 16;
+                    pval[k] = true;
+                }
+            } else if (c0 < TOT) {
+                const int xc = cc - TWP;
+                if (xc < PF_TILE * PER) {
+                    const int r = xc / PER, col = xc - r * PER;
+                    psrc[k] = xsrc + xrows[r] * xstride + col * 16;
+                    pval[k] = true;
+                }
+            }
+        }
         auto issue = [&](int c, const PfStage& s) {
             const int64_t goff = (int64_t)c * CB & ~(int64_t)15, xoff = (int64_t)c * PF_CHUNK * 36;
-            for (int c0 = wave * 64; c0 < TOT; c0 += PF_THREADS) {
-                const int cc = c0 + lane;
+#pragma unroll
+            for (int k = 0; k < NIT; k++) {
+                const int c0 = wave * 64 + k * PF_THREADS;
                 if (c0 < TWP) {
-                    if (cc < TW) {
-                        const int row = cc / PCB, col = cc - row * PCB;
-                        int64_t o = goff + col * 16;
-                        if constexpr (CBL != CB) o = o < rb - 16 ? o : rb - 16;   // span pieces stay in the row
-                        const uint8_t* src = (row < n0 ? w0 + row * rb : w1 + (row - n0) * rb) + o;
-                        copy16_lds_untracked(src, s.w + c0 * 16);
+                    if (pval[k]) {
+                        int64_t o = goff;
+                        // span pieces stay in the row: column byte + chunk offset <= rb - 16
+                        if constexpr (CBL != CB) o = goff + pcol[k] < rb - 16 ? goff : rb - 16 - pcol[k];
+                        copy16_lds_untracked(psrc[k] + o, s.w + c0 * 16);
                     }
-                } else {
-                    const int xc = cc - TWP;
-                    if (xc < PF_TILE * PER) {
-                        const int r = xc / PER, col = xc - r * PER;
-                        copy16_lds_untracked(xsrc + xrows[r] * xstride + xoff + col * 16, s.x + (c0 - TWP) * 16);
-                    }
+                } else if (c0 < TOT) {
+                    if (pval[k]) copy16_lds_untracked(psrc[k] + xoff, s.x + (c0 - TWP) * 16);
                 }
             }
         };
