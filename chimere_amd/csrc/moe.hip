@@ -1019,6 +1019,153 @@ __global__ __launch_bounds__(256) void k_moe_combine_dn(MoeArgs a) {
     a.out[(int64_t)t * a.H + h] = o;
 }
 
+// KDC: down projection and combine in one launch (M > 1, F == KDC_F), used
+// where every unit's rows fit: grid H / DR work-groups of 1024 threads, each
+// owning DR output rows.  All selected units' DR down rows (one contiguous
+// run of DR * row_bytes per unit) and every pair's Q8_1(h) row are copied to
+// LDS, so the whole layer's down bytes are in flight at once (one work-group
+// per CU).  Then the tasks -- the shared expert's (row, token) pairs first,
+// then the routed (unit, row) pairs -- are dealt to the 64 groups of 16 lanes:
+// lane j decodes weight block j of the row and, for each of the unit's
+// tokens, forms fmaf(d_w * d_h, sumi, 0) against h block j, summed over the 16
+// lanes by the halving tree (the L=16 order with one block per lane, F = 512).
+// Last, each (token, row) output is the router-weighted sum in k order plus
+// the shared expert, as in k_moe_combine_dn.
+constexpr int KDC_F = 512, KDC_THREADS = 1024, KDC_MAX_UNITS = 64;
+constexpr int KDC_HQ = KDC_F / QK * Q8_1_BYTES;   // bytes of one pair's Q8_1(h) row (the hq stride)
+template <int T>
+constexpr int kdc_rb() { return KDC_F / QTraits<T>::ELEMS * QTraits<T>::BYTES; }
+// rows per work-group: the routed runs of KDC_MAX_UNITS units within ~110 KB
+template <int T>
+constexpr int kdc_rows() { return KDC_MAX_UNITS * 8 * kdc_rb<T>() <= 112640 ? 8 : (KDC_MAX_UNITS * 4 * kdc_rb<T>() <= 112640 ? 4 : 2); }
+
+// both runs (routed and shared) whole 16-byte pieces
+template <int TE, int TS>
+constexpr bool kdc_types() {
+    return (TE == T_IQ3_S || TE == T_Q4_0 || TE == T_Q8_0) && kdc_rows<TE>() * kdc_rb<TE>() % 16 == 0 &&
+           kdc_rows<TE>() * kdc_rb<TS>() % 16 == 0;
+}
+
+template <int TE, int TS>
+__global__ __launch_bounds__(KDC_THREADS) void k_moe_down_comb(MoeArgs a) {
+    constexpr int DR = kdc_rows<TE>();
+    constexpr int RUNE = DR * kdc_rb<TE>(), RUNS = DR * kdc_rb<TS>();
+    static_assert(RUNE % 16 == 0 && RUNS % 16 == 0 && KDC_HQ % 16 == 0, "16-byte runs");
+    constexpr int PE = RUNE / 16, PS = RUNS / 16, PH = KDC_HQ / 16;
+    // weights: the shared run at 0, routed run u at RUNS + u * RUNE; + 16:
+    // lds_u32 of a row's last block reads up to 4 bytes past the row
+    __shared__ __attribute__((aligned(16))) uint8_t wl[RUNS + KDC_MAX_UNITS * RUNE + 16];
+    __shared__ __attribute__((aligned(16))) uint8_t hl[(KDC_MAX_UNITS + MAX_TOK) * KDC_HQ];
+    __shared__ float dn[(KDC_MAX_UNITS + MAX_TOK) * DR];
+    __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
+    __shared__ int s_uexp[KDC_MAX_UNITS];
+    __shared__ uint8_t s_untok[KDC_MAX_UNITS], s_upair[KDC_MAX_UNITS][MAX_TOK];   // pair ids < 128
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r0 = blockIdx.x * DR;
+    const int MK = a.M * a.K, NP = MK + (a.has_shared ? a.M : 0);
+    // Copies in three regions, each starting on a 64-piece round so that a
+    // wave's 64 pieces never straddle two (the LDS base of a copy instruction
+    // is wave-uniform; lanes past a region's end skip).  Wave 0 reads the plan
+    // and the IQ3_S codebook into LDS while waves 1.. issue the pairs' h rows
+    // (contiguous in hq) and the shared run; after an LDS-only barrier every
+    // wave issues the routed runs.  The copies are untracked (their wait is
+    // the explicit vmcnt(0) below): a tracked copy would make each later wait
+    // of the same wave -- and __syncthreads() -- wait for all of them, since
+    // the counter is in order.
+    const int nh = NP * PH, nsp = a.has_shared ? PS : 0;
+    const int th = (nh + 63) & ~63, ts = th + ((nsp + 63) & ~63);
+    constexpr int NW = KDC_THREADS / 64;
+    if (wave == 0) {
+        // the plan's first KDC_MAX_UNITS units, read without waiting for its count
+        s_uexp[lane] = a.plan[PLAN_UEXP + lane];
+        s_untok[lane] = (uint8_t)a.plan[PLAN_UNTOK + lane];
+#pragma unroll
+        for (int i = lane; i < KDC_MAX_UNITS * MAX_TOK; i += 64)
+            s_upair[i / MAX_TOK][i % MAX_TOK] = (uint8_t)a.plan[PLAN_UPAIR + i];
+        if constexpr (TE == T_IQ3_S || TS == T_IQ3_S)
+#pragma unroll
+            for (int i = lane; i < 512; i += 64) grid[i] = c_iq3s_grid_moe[i];
+    } else {
+        for (int c0 = (wave - 1) * 64; c0 < ts; c0 += (NW - 1) * 64) {
+            const int i = c0 + lane;
+            if (c0 < th) {
+                if (i < nh) copy16_lds_untracked(a.hq + (int64_t)i * 16, hl + c0 * 16);
+            } else if (i - th < nsp) {
+                copy16_lds_untracked(a.sh_down + (int64_t)r0 * kdc_rb<TS>() + (i - th) * 16, wl + (c0 - th) * 16);
+            }
+        }
+    }
+    lds_barrier();
+    const int nu = a.plan[0];
+    // routed runs: wave w copies units w, w + NW, ... (a unit's source and
+    // destination bases are wave-uniform; lane l copies pieces l, l + 64, ...)
+    for (int u = wave; u < nu; u += NW) {
+        const uint8_t* src = a.down + (int64_t)s_uexp[u] * a.sd + (int64_t)r0 * kdc_rb<TE>();
+        uint8_t* dst = wl + RUNS + u * RUNE;
+#pragma unroll
+        for (int c0 = 0; c0 < PE; c0 += 64)
+            if (c0 + lane < PE) copy16_lds_untracked(src + (c0 + lane) * 16, dst + c0 * 16);
+    }
+    wait_vm<0>();
+    lds_barrier();
+    const int g = tid >> 4, j = tid & 15;
+    // one (weight row, tokens) task: pairs pr[0..ntok) against row r
+    auto task = [&](auto tag, const uint8_t* row, int r, int ntok, auto pair_of) {
+        constexpr int T = decltype(tag)::value;
+        WBlk wb;
+        block_decode<T>(row, j, grid, wb);
+#pragma unroll
+        for (int t = 0; t < MAX_TOK; t++) {
+            if (t < ntok) {
+                const int p = pair_of(t);
+                XBlk xb;
+                load_xblk(hl + p * KDC_HQ + j * Q8_1_BYTES, xb);
+                const float v = slot_reduce16(wacc<T>(wb, xb, 0.0f));
+                if (j == 0) dn[p * DR + r] = v;
+            }
+        }
+    };
+    // tasks: the shared expert's (row, token) pairs first (every token of the
+    // chunk uses it), then the routed (unit, row) pairs
+    const int nsh = a.has_shared ? DR * a.M : 0, ntask = nsh + nu * DR;
+    for (int k = g; k < ntask; k += KDC_THREADS / 16) {
+        if (k < nsh) {
+            const int r = k / a.M, t = k - r * a.M;
+            task(std::integral_constant<int, TS>{}, wl + r * kdc_rb<TS>(), r, 1, [&](int) { return MK + t; });
+        } else {
+            const int u = (k - nsh) / DR, r = (k - nsh) - u * DR;
+            task(std::integral_constant<int, TE>{}, wl + RUNS + u * RUNE + r * kdc_rb<TE>(), r, (int)s_untok[u],
+                 [&](int t) { return (int)s_upair[u][t]; });
+        }
+    }
+    __syncthreads();
+    if (tid < a.M * DR) {
+        const int t = tid / DR, r = tid - t * DR, h = r0 + r;
+        if (h < a.H) {
+            float acc = 0.0f;
+            for (int k = 0; k < a.K; k++) acc = __builtin_fmaf(a.wts[t * a.K + k], dn[(t * a.K + k) * DR + r], acc);
+            float o = acc;
+            if (a.has_shared) {
+                const float sh = dn[(MK + t) * DR + r];
+                if (a.sh_gate_w) o = __builtin_fmaf(sh, 1.0f / (1.0f + det_exp(-a.glogit[t])), acc);
+                else o = sh + acc;
+            }
+            a.out[(int64_t)t * a.H + h] = o;
+        }
+    }
+}
+
+// k_moe_down_comb's conditions: F == 512, at most KDC_MAX_UNITS units, H a
+// multiple of the row count, 16-byte aligned runs
+static bool kdc_fits(const MoeArgs& a, int te, int ts) {
+    if (a.F != KDC_F || a.M * a.K > KDC_MAX_UNITS || a.M > MAX_TOK) return false;
+    const int rbe = (int)row_bytes(te, KDC_F), rbs = (int)row_bytes(ts, KDC_F);
+    const int dr = te == T_IQ3_S ? 8 : (te == T_Q4_0 ? 4 : 2);   // kdc_rows<TE>()
+    const uintptr_t al = (uintptr_t)a.down | (uintptr_t)a.sd | (uintptr_t)(dr * rbe) |
+                         (a.has_shared ? ((uintptr_t)a.sh_down | (uintptr_t)(dr * rbs)) : 0);
+    return a.H % dr == 0 && (al & 15) == 0 && a.hq_stride == KDC_HQ && ((uintptr_t)a.hq & 15) == 0;
+}
+
 // ------------------------------------------------------- workspace plan
 
 struct WsPlan {
@@ -1111,6 +1258,12 @@ static void launch_layer_multi(const MoeArgs& a, int stage, hipStream_t s) {
     if (stage < 0 || stage == 1)
         hipLaunchKernelGGL((k_moe_gateup<TE, TS>), dim3(NB + 8 * ((NU - 1 + 7) / 8) * NB), dim3(GEMV_THREADS), 0, s, a);
     if (stage < 0 || stage == 2) {
+        if constexpr (kdc_types<TE, TS>()) {
+            if (kdc_fits(a, TE, TS)) {
+                hipLaunchKernelGGL((k_moe_down_comb<TE, TS>), dim3(a.H / kdc_rows<TE>()), dim3(KDC_THREADS), 0, s, a);
+                return;
+            }
+        }
         hipLaunchKernelGGL((k_moe_down<TE, TS>), dim3((a.H + 4 * KG_RG - 1) / (4 * KG_RG), NU), dim3(GEMV_THREADS), 0,
                            s, a);
         hipLaunchKernelGGL(k_moe_combine_dn, dim3((a.H + 255) / 256, a.M), dim3(256), 0, s, a);

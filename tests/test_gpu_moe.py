@@ -258,3 +258,33 @@ def test_moe_kquant_shared(dev, et, st, M, H, F):
     layer = MoeLayer(router, gate, up, down, et, K, shared=sh, shared_type=st, sh_gate_w=gw)
     x = torch.randn(M, H, generator=g, device=dev)
     run_and_check(layer, x)
+
+
+@pytest.mark.parametrize("et,st,M,K,gate_vec", [
+    (O.IQ3_S, O.Q8_0, 8, 8, False), (O.IQ3_S, O.IQ3_S, 3, 8, True), (O.IQ3_S, O.Q5_K, 5, 8, False),
+    (O.IQ3_S, None, 4, 8, False), (O.Q4_0, O.Q4_0, 8, 8, True), (O.Q4_0, O.Q6_K, 2, 8, False),
+    (O.Q8_0, O.Q8_0, 6, 4, False), (O.Q8_0, O.Q4_0, 8, 8, False),
+    (O.IQ3_S, O.Q8_0, 8, 10, False),   # 80 units: the two-launch down / combine path
+])
+def test_moe_down_combine_fused(dev, et, st, M, K, gate_vec):
+    """F = 512 layers of several tokens (the fused down-projection + combine
+    launch where the units fit), bit-exact against the oracle."""
+    print(f"fused down/combine et={et} st={st} M={M} K={K}", flush=True)
+    H, F, E = 1024, 512, 64
+    if st in (O.Q4_K, O.Q5_K, O.Q6_K):
+        # K-quant shared expert: valid random blocks from the independent packer
+        import npref
+        g = torch.Generator(device=dev).manual_seed(40 + M + K)
+        router = torch.randn(E, H, generator=g, device=dev) * 0.02
+        gate, up, down = qmat(et, F, H, E, g, dev), qmat(et, F, H, E, g, dev), qmat(et, H, F, E, g, dev)
+        rng = np.random.default_rng(740 + st)
+        sh = tuple(torch.from_numpy(np.ascontiguousarray(npref.rand_kq(st, r, c, rng).reshape(-1))).to(dev)
+                   for r, c in ((F, H), (F, H), (H, F)))
+        gw = torch.randn(H, generator=g, device=dev) * 0.02 if gate_vec else None
+        layer = MoeLayer(router, gate, up, down, et, K, shared=sh, shared_type=st, sh_gate_w=gw)
+    else:
+        layer = build(dev, 40 + M + K, H=H, F=F, E=E, K=K, et=et, st=st, gate_vec=gate_vec)
+    g = torch.Generator(device=dev).manual_seed(41 + M)
+    for _ in range(2):
+        x = torch.randn(M, 1024, generator=g, device=dev)
+        run_and_check(layer, x, margin=False)
