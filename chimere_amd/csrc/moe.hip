@@ -908,6 +908,9 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_gateup(MoeArgs a) {
     const int tid = threadIdx.x;
     if constexpr (TE == T_IQ3_S || TS == T_IQ3_S)
         for (int i = tid; i < 512; i += GEMV_THREADS) grid[i] = c_iq3s_grid_moe[i];
+    // toks / pairs (written by the first ntok threads) are read by every wave
+    // in the tile's first copy, which precedes the tile's first barrier
+    __syncthreads();
     float acc[4][MAX_TOK];
     const int r0 = w * QK;
     if (e < 0) {
