@@ -30,11 +30,20 @@ struct MmvqArgs {
     int64_t y_slot_stride;  // floats between slots' outputs
 };
 
+// Blocks per K chunk of the GEMV tile: 64 for every type, which puts a
+// 2048-column Q8_0 row in one chunk (one exposed round trip per work-group
+// instead of two: 4096 x 2048 5.45 -> 4.75 us).  Larger chunks for the
+// K-quants / MXFP4 (a 4096-column row in one) and the double-buffered tile
+// with 32- or 64-block chunks were measured slower: fewer work-groups fit a
+// CU, and at 64 blocks four are resident per CU already.
+constexpr int MMVQ_BLOCKS = 64;
+
 template <int T, int NTOK>
 __global__ __launch_bounds__(GEMV_THREADS) void k_mmvq(MmvqArgs a) {
-    constexpr int CB = ChunkGeom<T>::BYTES;
+    constexpr int CBLK = MMVQ_BLOCKS;
+    constexpr int CB = chunk_bytes<T>(CBLK);
     __shared__ __attribute__((aligned(16))) uint8_t tile[TILE_ROWS * CB + 16];
-    __shared__ XLds xs[NTOK][MAX_CHUNK_BLOCKS];
+    __shared__ XLds xs[NTOK][CBLK];
     __shared__ uint32_t grid[T == T_IQ3_S ? 512 : 1];
 
     const int tid = threadIdx.x;
@@ -48,7 +57,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_mmvq(MmvqArgs a) {
         for (int i = tid; i < 512; i += GEMV_THREADS) grid[i] = c_iq3s_grid_mmvq[i];
 
     float acc[1][NTOK];
-    tile_gemv<T, NTOK, TILE_ROWS, 1, ChunkGeom<T>::BLOCKS, CPOL_STREAM>(tile, &xs[0][0], grid, a.W + e * a.w_slot_stride + (int64_t)r0 * rb, nr,
+    tile_gemv<T, NTOK, TILE_ROWS, 1, CBLK, CPOL_STREAM>(tile, &xs[0][0], grid,
+                                     a.W + e * a.w_slot_stride + (int64_t)r0 * rb, nr,
                                      nullptr, 0, rb, a.ncols, a.x + slot * a.x_slot_stride, a.x_tok_stride,
                                      nullptr, a.ntok, acc);
     if (g < nr) {
