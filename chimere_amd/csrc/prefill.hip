@@ -77,16 +77,30 @@ __global__ __launch_bounds__(256) void k_pf_router(PfArgs a) {
     for (int t = 0; t < PF_RT; t++)
 #pragma unroll
         for (int e = 0; e < PF_RE; e++) acc[t][e] = 0.0f;
+    // the loads of column step h + 256 are issued before step h's products
+    const float* xr[PF_RT];
+#pragma unroll
+    for (int t = 0; t < PF_RT; t++) xr[t] = a.x + (int64_t)min(t0 + t, a.T - 1) * a.H;
+    float rv[PF_RE], xv[PF_RT];
+#pragma unroll
+    for (int e = 0; e < PF_RE; e++) rv[e] = rows[e][tid];
+#pragma unroll
+    for (int t = 0; t < PF_RT; t++) xv[t] = xr[t][tid];
     for (int h = tid; h < a.H; h += 256) {
-        float rv[PF_RE], xv[PF_RT];
+        float rn[PF_RE], xn[PF_RT];
+        const int hn = h + 256 < a.H ? h + 256 : h;
 #pragma unroll
-        for (int e = 0; e < PF_RE; e++) rv[e] = rows[e][h];
+        for (int e = 0; e < PF_RE; e++) rn[e] = rows[e][hn];
 #pragma unroll
-        for (int t = 0; t < PF_RT; t++) xv[t] = a.x[(int64_t)min(t0 + t, a.T - 1) * a.H + h];
+        for (int t = 0; t < PF_RT; t++) xn[t] = xr[t][hn];
 #pragma unroll
         for (int t = 0; t < PF_RT; t++)
 #pragma unroll
             for (int e = 0; e < PF_RE; e++) acc[t][e] = __builtin_fmaf(rv[e], xv[t], acc[t][e]);
+#pragma unroll
+        for (int e = 0; e < PF_RE; e++) rv[e] = rn[e];
+#pragma unroll
+        for (int t = 0; t < PF_RT; t++) xv[t] = xn[t];
     }
     const int o = tid >> 3, q = tid & 7;
 #pragma unroll
