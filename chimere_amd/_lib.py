@@ -24,6 +24,7 @@ SIGNATURES = [
     ("chimere_mmvq_iq3s", None, [vp, vp, vp, i32, i32, i32, vp]),
     ("chimere_mmvq_q8_0", None, [vp, vp, vp, i32, i32, i32, vp]),
     ("chimere_mmvq_q4_0", None, [vp, vp, vp, i32, i32, i32, vp]),
+    ("chimere_mmvq_q4_0_sform", None, [vp, vp, vp, i32, i32, i32, vp]),
     ("chimere_mmvq_iq3s_f32", None, [vp, vp, vp, i32, i32, i32, vp, vp]),
     ("chimere_mmvq_q8_0_f32", None, [vp, vp, vp, i32, i32, i32, vp, vp]),
     ("chimere_mmvq_q4_0_f32", None, [vp, vp, vp, i32, i32, i32, vp, vp]),

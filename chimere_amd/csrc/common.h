@@ -15,6 +15,10 @@ namespace chimere {
 
 // ggml type ids
 enum : int { T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ3_S = 21, T_MXFP4 = 39 };
+// Internal id, not a ggml type: Q4_0 blocks with ggml's block term
+// d_w * (sum(nib * q_x) * d_x - 8 * s_x) (the "s-form", s_x = the Q8_1 block's
+// f16 sum of x) instead of the exact integer form; chimere_mmvq_q4_0_sform only.
+constexpr int T_Q4_0S = 102;
 
 constexpr int QK = 32;             // elements per Q8_0 / Q4_0 / Q8_1 block
 constexpr int Q8_1_BYTES = 36;     // [f16 d][f16 s][i8 q[32]]
@@ -29,6 +33,7 @@ __host__ __device__ inline int64_t pad_to(int64_t n, int64_t a) { return (n + a 
 template <int T> struct QTraits;
 template <> struct QTraits<T_Q8_0>  { static constexpr int BYTES = 34;  static constexpr int ELEMS = 32; };
 template <> struct QTraits<T_Q4_0>  { static constexpr int BYTES = 18;  static constexpr int ELEMS = 32; };
+template <> struct QTraits<T_Q4_0S> { static constexpr int BYTES = 18;  static constexpr int ELEMS = 32; };
 template <> struct QTraits<T_IQ3_S> { static constexpr int BYTES = 110; static constexpr int ELEMS = 256; };
 template <> struct QTraits<T_Q4_K>  { static constexpr int BYTES = 144; static constexpr int ELEMS = 256; };
 template <> struct QTraits<T_Q5_K>  { static constexpr int BYTES = 176; static constexpr int ELEMS = 256; };
@@ -119,13 +124,15 @@ __device__ __forceinline__ uint32_t lds_u16(const uint8_t* base, int off) {
 struct XBlk {
     int q[8];
     float d;
-    int sumq;   // sum of the 32 quants (used by Q4_0's "- 8" term)
+    int sumq;        // sum of the 32 quants (used by Q4_0's "- 8" term)
+    uint32_t sbits;  // the block's f16 s = sum of x (used by the Q4_0 s-form only)
 };
 
 __device__ __forceinline__ void load_xblk(const uint8_t* __restrict__ p, XBlk& x) {
     const uint32_t* w = (const uint32_t*)p;   // 36-byte blocks are 4-byte aligned
     uint32_t w0 = w[0];
     x.d = h2f(w0 & 0xFFFFu);
+    x.sbits = w0 >> 16;
     int s = 0;
 #pragma unroll
     for (int i = 0; i < 8; i++) { x.q[i] = (int)w[1 + i]; s = dot4(x.q[i], 0x01010101, s); }
@@ -261,6 +268,14 @@ __device__ __forceinline__ int wdot(const WBlk& w, const XBlk& x) {
 // (Q4_K, Q5_K) then add fmaf(-(f32(dmin)*f32(d_x)), (float)(m * sum q_x), acc).
 template <int T>
 __device__ __forceinline__ float wacc(const WBlk& w, const XBlk& x, float acc) {
+    if constexpr (T == T_Q4_0S) {
+        // ggml's Q4_0 block term d_w * (sumi * d_x - 8 * s_x) with unsigned
+        // nibbles in sumi, contracted as nvcc's default would: the inner
+        // expression one fma, the product with d_w fused into the sum.  The
+        // s field rides in sumq's slot of the decoded activation block.
+        const float inner = __builtin_fmaf((float)wdot<T>(w, x), x.d, -(8.0f * h2f((uint32_t)x.sumq)));
+        return __builtin_fmaf(w.dw, inner, acc);
+    }
     acc = __builtin_fmaf(w.dw * x.d, (float)wdot<T>(w, x), acc);
     if constexpr (T == T_Q4_K || T == T_Q5_K) acc = __builtin_fmaf(-(w.dm * x.d), (float)__mul24(w.mmin, x.sumq), acc);
     return acc;
@@ -410,7 +425,7 @@ __device__ __forceinline__ void block_decode(const uint8_t* row, int b, const ui
 #pragma unroll
         for (int i = 0; i < 8; i++) q[i] = lds_u32(row, off + 2 + 4 * i);
         wdec_q8_0_core(lds_u16(row, off), q, w);
-    } else if constexpr (T == T_Q4_0) {
+    } else if constexpr (T == T_Q4_0 || T == T_Q4_0S) {
         const int off = b * 18;
         uint32_t qs[4];
 #pragma unroll

@@ -52,7 +52,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_mmvq(MmvqArgs a) {
     const int r0 = blockIdx.x * TILE_ROWS;
     const int nr = min(TILE_ROWS, a.nrows - r0);
     const int64_t e = a.ids ? (int64_t)a.ids[slot] : (int64_t)slot;
-    const int64_t rb = row_bytes(T, a.ncols);
+    const int64_t rb = row_bytes(T == T_Q4_0S ? T_Q4_0 : T, a.ncols);
     if constexpr (T == T_IQ3_S)
         for (int i = tid; i < 512; i += GEMV_THREADS) grid[i] = c_iq3s_grid_mmvq[i];
 
@@ -87,6 +87,7 @@ bool launch_mmvq(int type, const MmvqArgs& a, int nslots, hipStream_t s) {
     switch (type) {
     case T_Q8_0: launch_t<T_Q8_0>(a, nslots, s); break;
     case T_Q4_0: launch_t<T_Q4_0>(a, nslots, s); break;
+    case T_Q4_0S: launch_t<T_Q4_0S>(a, nslots, s); break;
     case T_IQ3_S: launch_t<T_IQ3_S>(a, nslots, s); break;
     case T_Q4_K: launch_t<T_Q4_K>(a, nslots, s); break;
     case T_Q5_K: launch_t<T_Q5_K>(a, nslots, s); break;
@@ -125,7 +126,8 @@ static bool check_gemv(const char* who, int type, const void* W, const void* x, 
 
 static void gemv_entry(const char* who, int type, const void* W, const void* x, float* y, int ncols,
                        int nrows, int nrows_y_padded, int ntok, hipStream_t s) {
-    if (!check_gemv(who, type, W, x, y, ncols, nrows, nrows_y_padded, ntok)) return;
+    // the s-form GEMV reads plain Q4_0 blocks
+    if (!check_gemv(who, type == T_Q4_0S ? T_Q4_0 : type, W, x, y, ncols, nrows, nrows_y_padded, ntok)) return;
     MmvqArgs a{(const uint8_t*)W, (const uint8_t*)x, y, ncols, nrows, ntok,
                (int64_t)nrows_y_padded * Q8_1_BYTES, nrows, nullptr, 0, 0, 0};
     launch_mmvq(type, a, 1, s);
@@ -211,6 +213,10 @@ void chimere_mmvq_q8_0(const void* w, const void* x, float* y, int ncols, int nr
 }
 void chimere_mmvq_q4_0(const void* w, const void* x, float* y, int ncols, int nrows, int nyp, hipStream_t s) {
     gemv_entry("mmvq_q4_0", T_Q4_0, w, x, y, ncols, nrows, nyp, 1, s);
+}
+void chimere_mmvq_q4_0_sform(const void* w, const void* x, float* y, int ncols, int nrows, int nyp,
+                             hipStream_t s) {
+    gemv_entry("mmvq_q4_0_sform", T_Q4_0S, w, x, y, ncols, nrows, nyp, 1, s);
 }
 
 void chimere_mmvq_iq3s_f32(const void* w, const float* x, float* y, int ncols, int nrows, int ncp,

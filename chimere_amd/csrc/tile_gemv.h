@@ -93,7 +93,7 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds* __re
 #pragma unroll
             for (int k = 0; k < 8; k++) o.q[k] = xb.q[k];
             o.d = xb.d;
-            o.sumq = xb.sumq;
+            o.sumq = T == T_Q4_0S ? (int)xb.sbits : xb.sumq;   // the s-form needs s, not the quant sum
         }
         lds_copy_wait();
         __syncthreads();

@@ -72,6 +72,12 @@ def ggml_gpu_gemv_q4_0_q8(weights, q8_input, output, nrows, ncols):
     _gemv_q8("chimere_mmvq_q4_0", weights, q8_input, output, nrows, ncols)
 
 
+def ggml_gpu_gemv_q4_0_sform_q8(weights, q8_input, output, nrows, ncols):
+    """Q4_0 GEMV with ggml's s-form block term d_w*(sum(nib*q_x)*d_x - 8*s_x)
+    (ggml-parity experiments; the default Q4_0 GEMV uses the exact integer form)."""
+    _gemv_q8("chimere_mmvq_q4_0_sform", weights, q8_input, output, nrows, ncols)
+
+
 def _gemv_f32(name, weights, input, output, q8_scratch, nrows, ncols):
     getattr(lib(), name)(_ptr(weights), _ptr(input), _ptr(output), ncols, nrows,
                          pad(ncols, MATRIX_ROW_PADDING), _ptr(q8_scratch), _stream())

@@ -67,6 +67,18 @@ void chimere_mmvq_q8_0(const void *weights, const void *input_q8, float *output,
 void chimere_mmvq_q4_0(const void *weights, const void *input_q8, float *output,
                        int ncols, int nrows, int nrows_y_padded, hipStream_t stream);
 
+/* The same Q4_0 GEMV with ggml's block term (mul_mat_vec_q4_0_q8_1, reached
+ * in the reference only through libllama, out of tree): per block
+ * d_w * (sum(nib * q_x) * d_x - 8 * s_x), s_x = the Q8_1 block's f16 sum of
+ * x, contracted as inner = fmaf(sum, d_x, -8 s_x), acc = fmaf(d_w, inner,
+ * acc).  For ggml-parity experiments: it differs from chimere_mmvq_q4_0's
+ * exact integer form by at most 8 |d_w| |s_x - d_x * sum(q_x)| per block plus
+ * fp32 rounding.  Block terms are combined in this library's order (16 lanes
+ * per row, halving tree); ggml's own split of a block over threads is not
+ * reproduced. */
+void chimere_mmvq_q4_0_sform(const void *weights, const void *input_q8, float *output,
+                             int ncols, int nrows, int nrows_y_padded, hipStream_t stream);
+
 /* Fused F32 -> Q8_1 -> GEMV (ggml_cuda_gemv.cu:302-387): quantizes input_f32
  * into q8_scratch (pad(ncols,512)/32*36 bytes) then runs the GEMV. */
 void chimere_mmvq_iq3s_f32(const void *weights, const float *input_f32, float *output,

@@ -11,6 +11,7 @@ import subprocess as _sp
 import numpy as np
 
 Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, IQ3_S, MXFP4 = 2, 8, 12, 13, 14, 21, 39
+Q4_0_SFORM = 102   # not a ggml type: Q4_0 blocks with ggml's s-form block term (gemv only)
 _HERE = _os.path.dirname(_os.path.abspath(__file__))
 _LIB = None
 
@@ -62,7 +63,8 @@ def pad512(n):
 
 
 def row_bytes(t, ncols):
-    return {Q8_0: ncols // 32 * 34, Q4_0: ncols // 32 * 18, IQ3_S: ncols // 256 * 110, Q4_K: ncols // 256 * 144,
+    return {Q8_0: ncols // 32 * 34, Q4_0: ncols // 32 * 18, Q4_0_SFORM: ncols // 32 * 18, IQ3_S: ncols // 256 * 110,
+            Q4_K: ncols // 256 * 144,
             Q5_K: ncols // 256 * 176, Q6_K: ncols // 256 * 210, MXFP4: ncols // 32 * 17}[t]
 
 

@@ -168,7 +168,7 @@ int64_t orc_exp_scan(float lo, float hi, int *max_step, double *max_rel) {
 int64_t orc_row_bytes(int type, int64_t ncols) {
     switch (type) {
     case ORC_Q8_0: return ncols / 32 * 34;
-    case ORC_Q4_0: return ncols / 32 * 18;
+    case ORC_Q4_0: case ORC_Q4_0_SFORM: return ncols / 32 * 18;
     case ORC_IQ3_S: return ncols / 256 * 110;
     case ORC_Q4_K: return ncols / 256 * 144;
     case ORC_Q5_K: return ncols / 256 * 176;
@@ -438,6 +438,15 @@ static inline int32_t block_dot2(int type, const uint8_t *row, const uint8_t *xq
             s += ((o[2 + j] >> 4) - 8) * qx[j + 16];
         }
         *scale = orc_f16_to_f32(rd16(o)) * dx;
+    } else if (type == ORC_Q4_0_SFORM) {
+        /* unsigned nibbles; the caller forms ggml's term (row_dot) */
+        const uint8_t *o = row + (int64_t)b * 18;
+        for (int j = 0; j < 16; j++) {
+            s += (o[2 + j] & 0xF) * qx[j];
+            s += (o[2 + j] >> 4) * qx[j + 16];
+        }
+        *scale = orc_f16_to_f32(rd16(o));                    /* d_w */
+        *scale2 = -(8.0f * orc_f16_to_f32(rd16(xb + 2)));   /* -8 s_x */
     } else if (type == ORC_IQ3_S) {
         const uint8_t *o = row + (int64_t)(b >> 3) * 110;
         int ib = b & 7;
@@ -494,6 +503,13 @@ static float row_dot(int type, const uint8_t *row, const uint8_t *xq, int nb, in
         int32_t s2;
         int32_t s = block_dot2(type, row, xq, b, &sc, &s2, &sc2);
         int j = (b / G) % L;
+        if (type == ORC_Q4_0_SFORM) {
+            /* ggml mul_mat_vec_q4_0_q8_1's block term (out of tree; the
+             * contraction nvcc's default fmad gives it) */
+            const float dx = orc_f16_to_f32(rd16(xq + (int64_t)b * 36));
+            acc[j] = fmaf(sc, fmaf((float)s, dx, sc2), acc[j]);
+            continue;
+        }
         acc[j] = fmaf(sc, (float)s, acc[j]);
         if (type == ORC_Q4_K || type == ORC_Q5_K) acc[j] = fmaf(sc2, (float)s2, acc[j]);
     }

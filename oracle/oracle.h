@@ -41,6 +41,11 @@ extern "C" {
 #endif
 
 enum { ORC_Q4_0 = 2, ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q5_K = 13, ORC_Q6_K = 14, ORC_IQ3_S = 21, ORC_MXFP4 = 39 };
+/* Not a ggml type: Q4_0 blocks with ggml's block term (the "s-form")
+ * d_w * (sum(nib * q_x) * d_x - 8 * s_x), s_x = f32 of the Q8_1 block's f16
+ * sum of x, evaluated as inner = fmaf((float)sum, d_x, -(8 * s_x)),
+ * acc = fmaf(d_w, inner, acc); sum uses the unsigned nibbles. */
+enum { ORC_Q4_0_SFORM = 102 };
 
 uint16_t orc_f32_to_f16(float x);
 float    orc_f16_to_f32(uint16_t h);

@@ -244,3 +244,29 @@ def test_mxfp4_batched_device_ids(dev):
         for k in range(K):
             yo = O.gemv(O.MXFP4, w[ids[k]], xq[k] if stride else xq[0], H, F)
             assert (yg[k].view(np.uint32) == yo.view(np.uint32)).all()
+
+
+@pytest.mark.parametrize("nrows,ncols", [(4096, 2048), (37, 2048), (2048, 512), (300, 8192)])
+def test_gemv_q4_0_sform_bit_exact(dev, nrows, ncols):
+    """ggml's s-form Q4_0 block term (chimere_mmvq_q4_0_sform) against the
+    oracle's restatement, bit for bit; and within the bound of the exact form."""
+    print(f"gemv q4_0 s-form {nrows}x{ncols}", flush=True)
+    w, x, xq = _case(O.Q4_0, nrows, ncols, nrows * 11 + ncols)
+    wd, xqd = dev_t(w, dev), dev_t(xq, dev)
+    ys = torch.zeros(nrows, dtype=torch.float32, device=dev)
+    ye = torch.zeros(nrows, dtype=torch.float32, device=dev)
+    G.ggml_gpu_gemv_q4_0_sform_q8(wd, xqd, ys, nrows, ncols)
+    G.ggml_gpu_gemv_q4_0_q8(wd, xqd, ye, nrows, ncols)
+    gs, ge = host(ys), host(ye)
+    assert (gs.view(np.uint32) == O.gemv(O.Q4_0_SFORM, w, xq, ncols, nrows).view(np.uint32)).all()
+    assert (ge.view(np.uint32) == O.gemv(O.Q4_0, w, xq, ncols, nrows).view(np.uint32)).all()
+    # the forms differ by at most sum_b 8 |d_w| |s_x - d_x * sum(q_x)| per row (+ fp32 rounding)
+    nb = ncols // 32
+    xb = xq[:nb * 36].reshape(nb, 36)
+    f16 = lambda b: np.frombuffer(np.ascontiguousarray(b).tobytes(), np.float16).astype(np.float64)  # noqa: E731
+    dx, sx = f16(xb[:, 0:2]), f16(xb[:, 2:4])
+    sq = xb[:, 4:].view(np.int8).astype(np.int64).sum(axis=1)
+    dw = f16(w.reshape(nrows, nb, 18)[:, :, :2]).reshape(nrows, nb)
+    bound = (8 * np.abs(dw) * np.abs(sx - dx * sq)[None, :]).sum(axis=1)
+    diff = np.abs(gs.astype(np.float64) - ge)
+    assert (diff <= bound + 1e-5 * np.abs(ge).max()).all() and diff.max() > 0
