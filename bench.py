@@ -43,6 +43,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
+    ap.add_argument("--no-ncmoe", action="store_true", help="skip the host expert path (ncmoe) figures")
     ap.add_argument("--cpu-seconds", type=float, default=6.0, help="CPU baseline budget (about a tenth per figure)")
     ap.add_argument("--pmc", action="store_true", help="light mode for rocprofv3 --pmc runs")
     ap.add_argument("--pmc-workload", choices=["m1", "m8", "prefill", "prefill_iq3s", "head"], default="m1",
@@ -309,6 +310,39 @@ def main():
                     t1m, _ = graph_time(fns)
                     u1 = t1m / 192 * 1e6
                     extra[tag] = {"us_per_layer": round(u1, 2), "GBs_selected": round(sel3 / (u1 * 1e-6) / 1e9, 1)}
+                if not args.no_ncmoe:
+                    # the same layer with its routed experts on the host (the
+                    # reference's ncmoe path): device router + top-k, host expert
+                    # loop (libchimere_cpu.so), device shared expert; one token
+                    # per call, wall clock, experts rotated over the 64 inputs
+                    from chimere_amd import cpu as CPU
+                    ln = l5[0]
+                    ln.attach_cpu_experts(*(t.cpu().numpy() for t in ln.tensors[1:4]))
+                    nc = {}
+                    for nt in (4, min(16, os.cpu_count() or 1)):
+                        ln.forward_ncmoe(x1[0, 0], nthreads=nt)
+                        torch.cuda.synchronize()
+                        ts = []
+                        for i in range(24):
+                            t0 = time.perf_counter()
+                            ln.forward_ncmoe(x1[i % 64, 0], nthreads=nt)
+                            torch.cuda.synchronize()
+                            ts.append(time.perf_counter() - t0)
+                        g_, u_, d_ = ln.cpu_experts
+                        ids_h = np.arange(K, dtype=np.int32) * 7 % E
+                        w_h = np.full(K, 1.0 / K, np.float32)
+                        xh_ = x1[0, 0].cpu().numpy()
+                        te = []
+                        for i in range(24):
+                            t0 = time.perf_counter()
+                            CPU.ncmoe_experts(g_, u_, d_, (ids_h + 11 * i) % E, w_h, xh_, H, F, nthreads=nt)
+                            te.append(time.perf_counter() - t0)
+                        nc[f"threads_{nt}"] = {"us_per_token": round(float(np.median(ts)) * 1e6, 1),
+                                               "us_cpu_experts": round(float(np.median(te)) * 1e6, 1),
+                                               "GBs_cpu_selected": round(sel3 / float(np.median(te)) / 1e9, 2)}
+                    nc["avx2"] = int(CPU.lib().chimere_cpu_has_avx2())
+                    extra["ncmoe_m1_iq3s_q5k"] = nc
+                    del ln.cpu_experts
                 del l5, sh5
             del l8
             torch.cuda.empty_cache()

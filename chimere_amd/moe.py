@@ -6,6 +6,10 @@ reference's GGUF block layout) and a preallocated workspace, and runs
 weighted sum + shared expert) for 1..8 tokens, or ``chimere_moe_prefill``
 for a chunk of tokens.
 
+``forward_ncmoe`` runs one token with the routed experts on the host
+(``chimere_amd.cpu``, the reference's "ncmoe" path) and the rest on the
+device.
+
 ``forward_moe_v3`` replays the reference's own launch sequence
 (``chimere-server/src/qwen35_model/moe_ffn.rs:1094-1384`` V3 batched path and
 ``:1597-1761`` shared expert) through the ``ggml_gpu`` mirror; it computes the
@@ -16,7 +20,7 @@ import ctypes as C
 import torch
 
 from . import ggml_gpu as G
-from ._lib import IQ3_S, Q4_0, Q8_0, MoeLayerC, check, lib
+from ._lib import IQ3_S, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, MoeLayerC, check, lib
 
 _BLOCK = {Q8_0: (32, 34), Q4_0: (32, 18), IQ3_S: (256, 110)}
 
@@ -108,37 +112,32 @@ class MoeLayer:
         return out
 
     # ------------------------------------------------------------------
-    def forward_moe_v3(self, x):
-        """One token through the reference's 7-launch V3 sequence + shared expert."""
-        assert x.numel() == self.H
-        H, F, E, K, t = self.H, self.F, self.E, self.K, self.expert_type
-        dev = self.device
-        router_w, gate, up, down, sh_gate_w, logit_bias = self.tensors[:6]
-        bufs = G.GgmlGpuBuffers.with_moe(max(H, F), max(H, F), F, H, K, device=dev)
+    def _route(self, x, bufs):
+        """Router GEMV (+ bias) and top-k softmax on the device (moe_ffn.rs:1094-1140)."""
+        E, K, dev = self.E, self.K, self.device
+        router_w, logit_bias = self.tensors[0], self.tensors[5]
         router_out = torch.empty(E, dtype=torch.float32, device=dev)
         ids = torch.empty(K, dtype=torch.int32, device=dev)
         w = torch.empty(K, dtype=torch.float32, device=dev)
-        G.raw_f32_gemv(router_w, x, router_out, E, H)
+        G.raw_f32_gemv(router_w, x, router_out, E, self.H)
         if logit_bias is not None:
             router_out += logit_bias
         G.gpu_topk_softmax(router_out, ids, w, E, K)
-        G.ggml_gpu_quantize_q8_1(x, bufs.q8_input, H)
-        bat = {Q8_0: G.ggml_gpu_gemv_q8_0_batched, Q4_0: G.ggml_gpu_gemv_q4_0_batched,
-               IQ3_S: G.ggml_gpu_gemv_iq3s_batched}[t]
-        bat(gate, bufs.q8_input, bufs.batched_gate, ids, F, H, gate.numel() // E, 0, K)
-        bat(up, bufs.q8_input, bufs.batched_up, ids, F, H, up.numel() // E, 0, K)
-        G.silu_mul_inplace(bufs.batched_gate, bufs.batched_up, K * F)
-        G.ggml_gpu_quantize_q8_1_batched(bufs.batched_gate, bufs.batched_q8_inter, F, K)
-        bat(down, bufs.batched_q8_inter, bufs.batched_down, ids, H, F, down.numel() // E,
-            G.q8_1_row_bytes(F), K)
-        accum = torch.empty(H, dtype=torch.float32, device=dev)
-        G.weighted_combine_gpu(bufs.batched_down, w, accum, H, K)
+        return ids, w
+
+    def _shared_tail(self, x, accum, bufs):
+        """Shared expert on the device, combined with the routed sum `accum`
+        (moe_ffn.rs:1597-1761); returns `accum` alone without a shared expert."""
         if self.shared_type < 0:
-            return accum, ids, w
+            return accum
+        H, F, dev = self.H, self.F, self.device
+        sh_gate_w = self.tensors[4]
         sg, su, sd = self.tensors[6:9]
         st = self.shared_type
-        f32 = {Q8_0: G.ggml_gpu_gemv_q8_0_f32, Q4_0: G.ggml_gpu_gemv_q4_0_f32, IQ3_S: G.ggml_gpu_gemv_iq3s_f32}[st]
-        q8 = {Q8_0: G.ggml_gpu_gemv_q8_0_q8, Q4_0: G.ggml_gpu_gemv_q4_0_q8, IQ3_S: G.ggml_gpu_gemv_iq3s_q8}[st]
+        f32 = {Q8_0: G.ggml_gpu_gemv_q8_0_f32, Q4_0: G.ggml_gpu_gemv_q4_0_f32, IQ3_S: G.ggml_gpu_gemv_iq3s_f32,
+               Q4_K: G.ggml_gpu_gemv_q4k_f32, Q5_K: G.ggml_gpu_gemv_q5k_f32, Q6_K: G.ggml_gpu_gemv_q6k_f32}[st]
+        q8 = {Q8_0: G.ggml_gpu_gemv_q8_0_q8, Q4_0: G.ggml_gpu_gemv_q4_0_q8, IQ3_S: G.ggml_gpu_gemv_iq3s_q8,
+              Q4_K: G.ggml_gpu_gemv_q4k_q8, Q5_K: G.ggml_gpu_gemv_q5k_q8, Q6_K: G.ggml_gpu_gemv_q6k_q8}[st]
         shg = torch.empty(F, dtype=torch.float32, device=dev)
         shu = torch.empty(F, dtype=torch.float32, device=dev)
         shd = torch.empty(H, dtype=torch.float32, device=dev)
@@ -152,4 +151,73 @@ class MoeLayer:
             G.raw_sigmoid_gate_add_inplace(shd, glogit, accum, H)
         else:
             shd += accum
-        return shd, ids, w
+        return shd
+
+    def forward_moe_v3(self, x):
+        """One token through the reference's 7-launch V3 sequence + shared expert."""
+        assert x.numel() == self.H
+        H, F, E, K, t = self.H, self.F, self.E, self.K, self.expert_type
+        dev = self.device
+        gate, up, down = self.tensors[1:4]
+        bufs = G.GgmlGpuBuffers.with_moe(max(H, F), max(H, F), F, H, K, device=dev)
+        ids, w = self._route(x, bufs)
+        G.ggml_gpu_quantize_q8_1(x, bufs.q8_input, H)
+        bat = {Q8_0: G.ggml_gpu_gemv_q8_0_batched, Q4_0: G.ggml_gpu_gemv_q4_0_batched,
+               IQ3_S: G.ggml_gpu_gemv_iq3s_batched}[t]
+        bat(gate, bufs.q8_input, bufs.batched_gate, ids, F, H, gate.numel() // E, 0, K)
+        bat(up, bufs.q8_input, bufs.batched_up, ids, F, H, up.numel() // E, 0, K)
+        G.silu_mul_inplace(bufs.batched_gate, bufs.batched_up, K * F)
+        G.ggml_gpu_quantize_q8_1_batched(bufs.batched_gate, bufs.batched_q8_inter, F, K)
+        bat(down, bufs.batched_q8_inter, bufs.batched_down, ids, H, F, down.numel() // E,
+            G.q8_1_row_bytes(F), K)
+        accum = torch.empty(H, dtype=torch.float32, device=dev)
+        G.weighted_combine_gpu(bufs.batched_down, w, accum, H, K)
+        return self._shared_tail(x, accum, bufs), ids, w
+
+    # ------------------------------------------------------------------
+    def attach_cpu_experts(self, gate, up, down):
+        """Host copies of the routed expert tensors for forward_ncmoe (the
+        reference's gate_exps_cpu / up_exps_cpu / down_exps_cpu): numpy uint8
+        [E, expert_bytes] in the device tensors' layout; IQ3_S only."""
+        import numpy as np
+        if self.expert_type != IQ3_S:
+            raise ValueError("the CPU expert path takes IQ3_S experts only")
+        arrs = tuple(np.ascontiguousarray(a, np.uint8).reshape(self.E, -1) for a in (gate, up, down))
+        for a, t in zip(arrs, self.tensors[1:4]):
+            if a.size != t.numel():
+                raise ValueError("host expert tensor size differs from the device tensor")
+        self.cpu_experts = arrs
+        pin = torch.cuda.is_available()
+        self._h_x = torch.empty(self.H, dtype=torch.float32, pin_memory=pin)
+        self._h_ids = torch.empty(self.K, dtype=torch.int32, pin_memory=pin)
+        self._h_w = torch.empty(self.K, dtype=torch.float32, pin_memory=pin)
+        self._h_acc = torch.empty(self.H, dtype=torch.float32, pin_memory=pin)
+
+    def forward_ncmoe(self, x, nthreads=4):
+        """One token with the routed experts on the host (moe_ffn.rs:1507-1591):
+        router and top-k on the device, then hidden state, ids and weights to
+        the host, libchimere_cpu.so's expert loop, the sum back to the device
+        and the shared expert there.  Returns (out [H], ids [K], weights [K]);
+        without a shared expert `out` is a buffer the next call overwrites."""
+        from . import cpu
+        if not hasattr(self, "cpu_experts"):
+            raise RuntimeError("attach_cpu_experts() first")
+        assert x.numel() == self.H
+        x = x.reshape(self.H)
+        H, F, K, dev = self.H, self.F, self.K, self.device
+        if not hasattr(self, "_nc_bufs"):
+            self._nc_bufs = G.GgmlGpuBuffers.with_moe(max(H, F), max(H, F), F, H, K, device=dev)
+            self._nc_accum = torch.empty(H, dtype=torch.float32, device=dev)
+        bufs = self._nc_bufs
+        ids, w = self._route(x, bufs)
+        self._h_ids.copy_(ids, non_blocking=True)
+        self._h_w.copy_(w, non_blocking=True)
+        self._h_x.copy_(x, non_blocking=True)
+        torch.cuda.current_stream(dev).synchronize()     # the host reads these next
+        g, u, d = self.cpu_experts
+        cpu.ncmoe_experts(g, u, d, self._h_ids.numpy(), self._h_w.numpy(), self._h_x.numpy(), H, F,
+                          out=self._h_acc.numpy(), nthreads=nthreads)
+        # stream-ordered: the next call's synchronize also covers this copy
+        # before _h_acc is written again
+        self._nc_accum.copy_(self._h_acc, non_blocking=True)
+        return self._shared_tail(x, self._nc_accum, bufs), ids, w

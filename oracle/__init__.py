@@ -50,6 +50,12 @@ def lib():
         L.orc_moe.argtypes = [vp, vp, vp, vp, vp, i32]
         L.cpb_gemv.argtypes = [i32, vp, vp, vp, i32, i32, i32]
         L.cpb_moe.argtypes = [vp, vp, vp, vp, vp, i32]
+        L.orc_quantize_q8_K.argtypes = [vp, i64, vp]
+        L.orc_vec_dot_iq3s_q8K.restype = f32
+        L.orc_vec_dot_iq3s_q8K.argtypes = [i32, vp, vp]
+        L.orc_gemv_iq3s_q8K.argtypes = [vp, vp, vp, i32, i32]
+        L.orc_moe_ncmoe.argtypes = [vp, vp, vp, vp, vp, i32]
+        L.orc_ncmoe.argtypes = [vp, vp, vp, i64, i64, i64, vp, vp, i32, vp, vp, i32, i32]
         _LIB = L
     return _LIB
 
@@ -189,6 +195,12 @@ def moe(x, router_w, gate, up, down, exp_type, K, sh=None, sh_type=-1, sh_gate_w
     return out, ids, wts
 
 
+def moe_ncmoe(*args, **kw):
+    """moe() with the routed experts on the ncmoe CPU path (Q8_K activations,
+    IQ3_S experts); router, top-k and shared expert as moe()."""
+    return moe(*args, fn="orc_moe_ncmoe", **kw)
+
+
 def cpu_moe(*args, nthreads=1, **kw):
     """The CPU baseline (cpu_path.c): same arguments and results as moe(),
     to the fp32 tolerance."""
@@ -200,3 +212,38 @@ def cpu_gemv(t, W, xq, ncols, nrows, nthreads=1):
     y = np.zeros(nrows, np.float32)
     lib().cpb_gemv(t, _p(np.ascontiguousarray(W)), _p(np.ascontiguousarray(xq)), _p(y), ncols, nrows, nthreads)
     return y
+
+
+def quantize_q8_K(x):
+    """ggml Q8_K blocks (296 B per 256 values) of a float vector."""
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    assert x.size % 256 == 0
+    out = np.zeros(x.size // 256 * 296, np.uint8)
+    lib().orc_quantize_q8_K(_p(x), x.size, _p(out))
+    return out
+
+
+def vec_dot_iq3s_q8K(w, y, n):
+    return lib().orc_vec_dot_iq3s_q8K(int(n), _p(np.ascontiguousarray(w)), _p(np.ascontiguousarray(y)))
+
+
+def gemv_iq3s_q8K(W, x, nrows, ncols):
+    """y = W x, IQ3_S rows against the Q8_K quantization of f32 x."""
+    W = np.ascontiguousarray(W, np.uint8)
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.zeros(nrows, np.float32)
+    lib().orc_gemv_iq3s_q8K(_p(W), _p(x), _p(y), nrows, ncols)
+    return y
+
+
+def ncmoe(x, gate, up, down, ids, wts, H, F):
+    """The CPU expert loop of one token: sum_k w_k * down_e(silu(gate_e x) * up_e x)
+    with IQ3_S expert tensors [E, rows * row_bytes]."""
+    gate, up, down = (np.ascontiguousarray(a, np.uint8) for a in (gate, up, down))
+    ids = np.ascontiguousarray(ids, np.int32)
+    wts = np.ascontiguousarray(wts, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros(H, np.float32)
+    sg, su, sd = (a[0].size if a.ndim == 2 else a.size // 256 for a in (gate, up, down))
+    lib().orc_ncmoe(_p(gate), _p(up), _p(down), sg, su, sd, _p(ids), _p(wts), ids.size, _p(x), _p(out), H, F)
+    return out

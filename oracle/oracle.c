@@ -644,3 +644,136 @@ void orc_moe(const orc_moe_params *p, const float *x, float *out,
     }
     free(logits); free(dn); free(acc); free(xq);
 }
+
+/* ------------------------------------------------------------ ncmoe path
+ * The reference's CPU expert path (cs/src/qwen35_model/moe_ffn.rs:1507-1591)
+ * over its ggml wrapper (cs/ffi/ggml_iq3s_gemv.c:33-127): activations to
+ * Q8_K once per GEMV, one IQ3_S x Q8_K dot per row.  ggml itself (ik_llama.cpp)
+ * is out of tree; its published semantics are restated here.
+ *
+ * Q8_K block, 296 B (layout cs/ffi/ggml_iq3s_gemv.h:14-16): f32 d, f32 sum,
+ * int8 qs[256], int16 bsums[16].  quantize_row_q8_K: max = the element of
+ * largest |x| (the first one); amax == 0 -> all fields zero; otherwise
+ * iscale = -127 / max, q = min(127, round-half-even(iscale * x)), bsums =
+ * sums of 16 quants, d = 1 / iscale; sum = d * sum(q) (a field the IQ3_S dot
+ * does not read). */
+void orc_quantize_q8_K(const float *x, int64_t k, uint8_t *out) {
+    for (int64_t b = 0; b < k / 256; b++) {
+        const float *v = x + b * 256;
+        uint8_t *o = out + b * 296;
+        float amax = 0.0f, max = 0.0f;
+        for (int j = 0; j < 256; j++) {
+            float ax = fabsf(v[j]);
+            if (ax > amax) { amax = ax; max = v[j]; }
+        }
+        memset(o, 0, 296);
+        if (amax == 0.0f) continue;
+        const float iscale = -127.0f / max;
+        int8_t *q = (int8_t *)(o + 8);
+        int sq = 0;
+        for (int j = 0; j < 256; j++) {
+            int t = (int)rintf(iscale * v[j]);
+            q[j] = (int8_t)(t < 127 ? t : 127);
+            sq += q[j];
+        }
+        for (int g = 0; g < 16; g++) {
+            int s = 0;
+            for (int j = 0; j < 16; j++) s += q[16 * g + j];
+            int16_t s16 = (int16_t)s;
+            memcpy(o + 264 + 2 * g, &s16, 2);
+        }
+        const float d = 1.0f / iscale, sum = d * (float)sq;
+        memcpy(o, &d, 4);
+        memcpy(o + 4, &sum, 4);
+    }
+}
+
+/* IQ3_S super-block(s) x Q8_K: per super-block the exact integer
+ * bsum = sum_ib (1 + 2 s_ib) * sum_e level_e * q_e, then, in super-block
+ * order, acc = fmaf(f32(d_w) * d_y, (float)bsum, acc) (ggml's generic
+ * `sumf += d * bsum` as contracted). */
+float orc_vec_dot_iq3s_q8K(int n, const uint8_t *w, const uint8_t *y) {
+    float acc = 0.0f;
+    for (int b = 0; b < n / 256; b++) {
+        const uint8_t *o = w + (int64_t)b * 110, *yb = y + (int64_t)b * 296;
+        const int8_t *q = (const int8_t *)(yb + 8);
+        float dy;
+        memcpy(&dy, yb, 4);
+        int32_t bsum = 0;
+        for (int ib = 0; ib < 8; ib++) {
+            int32_t s = 0;
+            for (int e = 0; e < 32; e++) s += iq3s_level(o, ib, e) * q[32 * ib + e];
+            bsum += s * iq3s_mult(o, ib);
+        }
+        acc = fmaf(orc_f16_to_f32(rd16(o)) * dy, (float)bsum, acc);
+    }
+    return acc;
+}
+
+void orc_gemv_iq3s_q8K(const uint8_t *W, const float *x, float *y, int nrows, int ncols) {
+    uint8_t *xq = (uint8_t *)malloc((size_t)(ncols / 256) * 296);
+    orc_quantize_q8_K(x, ncols, xq);
+    const int64_t rb = (int64_t)ncols / 256 * 110;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (int r = 0; r < nrows; r++) y[r] = orc_vec_dot_iq3s_q8K(ncols, W + r * rb, xq);
+    free(xq);
+}
+
+/* The expert loop of one token (moe_ffn.rs:1538-1585): for each selected
+ * (expert, weight) in order: gate = W_g x and up = W_u x (IQ3_S x Q8_K),
+ * h = silu(gate) * up in f32 with expf (g / (1 + exp(-g)), as the Rust
+ * code), down = W_d h, combined += weight * down (a product then a sum). */
+void orc_ncmoe(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int64_t sg, int64_t su, int64_t sd,
+               const int32_t *ids, const float *wts, int K, const float *x, float *out, int H, int F) {
+    float *g = (float *)malloc(sizeof(float) * (size_t)F), *u = (float *)malloc(sizeof(float) * (size_t)F);
+    float *dn = (float *)malloc(sizeof(float) * (size_t)H);
+    for (int i = 0; i < H; i++) out[i] = 0.0f;
+    for (int k = 0; k < K; k++) {
+        const int64_t e = ids[k];
+        orc_gemv_iq3s_q8K(gate + e * sg, x, g, F, H);
+        orc_gemv_iq3s_q8K(up + e * su, x, u, F, H);
+        for (int i = 0; i < F; i++) g[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
+        orc_gemv_iq3s_q8K(down + e * sd, g, dn, H, F);
+        for (int i = 0; i < H; i++) out[i] = out[i] + wts[k] * dn[i];
+    }
+    free(g); free(u); free(dn);
+}
+
+/* One MoE layer with the routed experts on the CPU path (moe_ffn.rs:1507-1591)
+ * and everything else as orc_moe: router, top-k, then the shared expert on
+ * the Q8_1 path combined with the CPU experts' sum.  IQ3_S experts only. */
+void orc_moe_ncmoe(const orc_moe_params *p, const float *x, float *out, int32_t *ids, float *wts, int nthreads) {
+    int H = p->H, F = p->F, E = p->E, K = p->K;
+    float *logits = malloc(sizeof(float) * E);
+    float *dn = malloc(sizeof(float) * H);
+    float *acc = malloc(sizeof(float) * H);
+    uint8_t *xq = malloc(pad512(H) / 32 * 36);
+    int32_t id[1024];
+    float w[1024];
+    for (int t = 0; t < p->M; t++) {
+        const float *xt = x + (int64_t)t * H;
+        orc_router(p->router, xt, logits, E, H);
+        if (p->logit_bias) for (int e = 0; e < E; e++) logits[e] = logits[e] + p->logit_bias[e];
+        orc_topk_softmax(logits, E, K, id, w);
+        if (ids) memcpy(ids + (int64_t)t * K, id, sizeof(int32_t) * K);
+        if (wts) memcpy(wts + (int64_t)t * K, w, sizeof(float) * K);
+        orc_ncmoe(p->gate, p->up, p->down, p->stride_gate, p->stride_up, p->stride_down, id, w, K, xt, acc, H, F);
+        float *o = out + (int64_t)t * H;
+        if (p->sh_type >= 0) {
+            orc_quantize_q8_1(xt, H, pad512(H), 1, xq);
+            expert_ffn(p->sh_type, p->sh_gate, p->sh_up, p->sh_down, xq, H, F, p->L, p->G, dn, nthreads);
+            if (p->sh_gate_w) {
+                float gl = dot256(p->sh_gate_w, xt, H);
+                float sc = 1.0f / (1.0f + orc_exp(-gl));
+                for (int i = 0; i < H; i++) o[i] = fmaf(dn[i], sc, acc[i]);
+            } else {
+                for (int i = 0; i < H; i++) o[i] = dn[i] + acc[i];
+            }
+        } else {
+            memcpy(o, acc, sizeof(float) * H);
+        }
+    }
+    free(logits); free(dn); free(acc); free(xq);
+}

@@ -101,6 +101,16 @@ typedef struct {
 void orc_moe(const orc_moe_params *p, const float *x, float *out,
              int32_t *ids, float *wts, int nthreads);
 
+/* ncmoe CPU expert path (moe_ffn.rs:1507-1591, ffi/ggml_iq3s_gemv.c): Q8_K
+ * activations (296-byte blocks), IQ3_S x Q8_K dots, the one-token expert loop. */
+void orc_quantize_q8_K(const float *x, int64_t k, uint8_t *out);
+float orc_vec_dot_iq3s_q8K(int n, const uint8_t *w, const uint8_t *y);
+void orc_gemv_iq3s_q8K(const uint8_t *W, const float *x, float *y, int nrows, int ncols);
+void orc_ncmoe(const uint8_t *gate, const uint8_t *up, const uint8_t *down, int64_t sg, int64_t su, int64_t sd,
+               const int32_t *ids, const float *wts, int K, const float *x, float *out, int H, int F);
+/* orc_moe with the routed experts on the ncmoe CPU path (IQ3_S experts) */
+void orc_moe_ncmoe(const orc_moe_params *p, const float *x, float *out, int32_t *ids, float *wts, int nthreads);
+
 /* CPU baseline (cpu_path.c): the reference's CPU path structure with AVX2
  * vec_dots (Q8_0 / Q4_0 / IQ3_S weights, Q8_1 activations), OpenMP
  * row-parallel with nthreads threads; agrees with the oracle to the fp32
