@@ -140,11 +140,7 @@ def test_moe_edge_cases(dev, et, st, gate_vec, K, E, M):
     run_and_check(layer, torch.randn(M, 1024, generator=g, device=dev))
 
 
-_SKIP_TIES = pytest.mark.skip(reason="held off the GPU: first run was part of a call that faulted the GPU "
-                                     "(cause not identified; see DESIGN.md)")
-
-
-@pytest.mark.parametrize("M", [pytest.param(1, marks=_SKIP_TIES), 2])
+@pytest.mark.parametrize("M", [1, 2])
 def test_moe_zero_input_finite(dev, M):
     """All logits equal: every probability ties, the lowest indices win."""
     layer = build(dev, 9, H=1024, F=256, E=32, K=4)
@@ -153,7 +149,6 @@ def test_moe_zero_input_finite(dev, M):
     assert np.isfinite(og).all() and (ig == np.arange(4)).all()
 
 
-@_SKIP_TIES
 def test_moe_m1_tied_logits(dev):
     """Router rows repeated in pairs: tied probabilities straddle the top-k boundary."""
     layer = build(dev, 21, H=1024, F=256, E=64, K=7)
