@@ -62,7 +62,7 @@ struct PfArgs {
 // j = q (mod 8) (tree levels m = 128 .. 8), then levels 4, 2, 1 run across
 // the 8 lanes.
 __global__ __launch_bounds__(256) void k_pf_router(PfArgs a) {
-    __shared__ float red[32][257];
+    __shared__ float red[32][264];   // row stride = 8 banks: the 8-lane groups read distinct banks
     const int tid = threadIdx.x;
     const int NR = a.E + (a.sh_gate_w ? 1 : 0);
     const int e0 = blockIdx.x * PF_RE, t0 = blockIdx.y * PF_RT;
