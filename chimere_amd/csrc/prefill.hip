@@ -179,7 +179,16 @@ __global__ __launch_bounds__(1024) void k_pf_plan(PfArgs a) {
     for (int e = tid; e < 2 * 1024; e += 1024) cnt[e] = 0;
     for (int e = tid; e < NE; e += 1024) fill[e] = 0;
     __syncthreads();
-    for (int p = tid; p < TK; p += 1024) atomicAdd(&cnt[a.ids[p]], 1);
+    // pairs in batches of 4 per thread: the 4 id loads are issued together
+    // (one memory round trip per batch, not per pair)
+    for (int p0 = tid; p0 < TK; p0 += 4 * 1024) {
+        int e4[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) e4[i] = p0 + i * 1024 < TK ? a.ids[p0 + i * 1024] : -1;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (e4[i] >= 0) atomicAdd(&cnt[e4[i]], 1);
+    }
     if (tid == 0) cnt[a.E] = a.has_shared ? a.T : 0;
     __syncthreads();
     const int c0 = cnt[2 * tid], c1 = cnt[2 * tid + 1];
@@ -200,10 +209,22 @@ __global__ __launch_bounds__(1024) void k_pf_plan(PfArgs a) {
     }
     if (tid == 0) *a.ntiles = tot[1];
     __syncthreads();
-    for (int p = tid; p < TK; p += 1024) {
-        const int e = a.ids[p];
-        a.spairs[cnt[e] + atomicAdd(&fill[e], 1)] = p;
-        if (a.ids_out) { a.ids_out[p] = e; a.w_out[p] = a.wts[p]; }
+    for (int p0 = tid; p0 < TK; p0 += 4 * 1024) {
+        int e4[4];
+        float w4[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const bool in = p0 + i * 1024 < TK;
+            e4[i] = in ? a.ids[p0 + i * 1024] : -1;
+            w4[i] = in && a.ids_out ? a.wts[p0 + i * 1024] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int p = p0 + i * 1024, e = e4[i];
+            if (e < 0) continue;
+            a.spairs[cnt[e] + atomicAdd(&fill[e], 1)] = p;
+            if (a.ids_out) { a.ids_out[p] = e; a.w_out[p] = w4[i]; }
+        }
     }
     if (a.has_shared)
         for (int t = tid; t < a.T; t += 1024) a.spairs[cnt[a.E] + t] = TK + t;
@@ -702,19 +723,45 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_down(PfArgs a) {
 }
 
 // P6: grid (ceil(H/256), T): out = sum_k fmaf(w_k, dn_k, acc) (+ shared expert)
+// one thread per 4 consecutive outputs of a token (H % 4 == 0, which every
+// shape the prefill accepts has: H is a multiple of 256); each output's
+// fmaf chain over k is the one of the decode layer's combine
 __global__ __launch_bounds__(256) void k_pf_combine(PfArgs a) {
-    const int t = blockIdx.y, h = blockIdx.x * 256 + threadIdx.x;
+    const int t = blockIdx.y, h = 4 * (blockIdx.x * 256 + threadIdx.x);
     if (h >= a.H) return;
-    float acc = 0.0f;
-    for (int k = 0; k < a.K; k++)
-        acc = __builtin_fmaf(a.wts[t * a.K + k], a.dn[(int64_t)(t * a.K + k) * a.H + h], acc);
-    float o = acc;
-    if (a.has_shared) {
-        const float shv = a.dn[(int64_t)(a.T * a.K + t) * a.H + h];
-        if (a.sh_gate_w) o = __builtin_fmaf(shv, 1.0f / (1.0f + det_exp(-a.glogit[t])), acc);
-        else o = shv + acc;
+    float4 v[MAX_K + 1];
+#pragma unroll
+    for (int k = 0; k < MAX_K; k++)
+        if (k < a.K) v[k] = *(const float4*)(a.dn + (int64_t)(t * a.K + k) * a.H + h);
+    if (a.has_shared) v[MAX_K] = *(const float4*)(a.dn + (int64_t)(a.T * a.K + t) * a.H + h);
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int k = 0; k < MAX_K; k++) {
+        if (k < a.K) {
+            const float w = a.wts[t * a.K + k];
+            acc.x = __builtin_fmaf(w, v[k].x, acc.x);
+            acc.y = __builtin_fmaf(w, v[k].y, acc.y);
+            acc.z = __builtin_fmaf(w, v[k].z, acc.z);
+            acc.w = __builtin_fmaf(w, v[k].w, acc.w);
+        }
     }
-    a.out[(int64_t)t * a.H + h] = o;
+    float4 o = acc;
+    if (a.has_shared) {
+        const float4 shv = v[MAX_K];
+        if (a.sh_gate_w) {
+            const float sg = 1.0f / (1.0f + det_exp(-a.glogit[t]));
+            o = make_float4(__builtin_fmaf(shv.x, sg, acc.x), __builtin_fmaf(shv.y, sg, acc.y),
+                            __builtin_fmaf(shv.z, sg, acc.z), __builtin_fmaf(shv.w, sg, acc.w));
+        } else {
+            o = make_float4(shv.x + acc.x, shv.y + acc.y, shv.z + acc.z, shv.w + acc.w);
+        }
+    }
+    float* dst = a.out + (int64_t)t * a.H + h;
+    if (((uintptr_t)a.out & 15) == 0) {
+        *(float4*)dst = o;
+    } else {   // a caller's output that is not 16-byte aligned
+        dst[0] = o.x; dst[1] = o.y; dst[2] = o.z; dst[3] = o.w;
+    }
 }
 
 void launch_quantize_q8_1(const float* x, void* out, int64_t ncols, int64_t ncols_padded, int64_t nrows,
@@ -758,7 +805,7 @@ static void launch_pf(const PfArgs& a, const PfPlan& p, hipStream_t s) {
     hipLaunchKernelGGL(k_pf_plan, dim3(1), dim3(1024), 0, s, a);
     hipLaunchKernelGGL((k_pf_gate_up<TE, TS>), dim3(a.F / PF_GU_ROWS, p.max_tiles), dim3(PF_THREADS), 0, s, a);
     hipLaunchKernelGGL((k_pf_down<TE, TS>), dim3(a.H / 128, p.max_tiles), dim3(PF_THREADS), 0, s, a);
-    hipLaunchKernelGGL(k_pf_combine, dim3((a.H + 255) / 256, a.T), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(k_pf_combine, dim3((a.H / 4 + 255) / 256, a.T), dim3(256), 0, s, a);
 }
 
 }  // namespace chimere

@@ -115,6 +115,20 @@ def test_prefill_repeat_and_zero(dev):
     assert np.isfinite(z).all()
 
 
+def test_prefill_unaligned_output(dev):
+    """An output buffer that is not 16-byte aligned (a view one float into an
+    allocation) gets the same bits as an aligned one."""
+    layer = build(dev, 13, H=1024, F=256, E=32, K=4)
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(9, 1024, generator=g, device=dev)
+    want = host(layer.prefill(x))
+    buf = torch.full((9 * 1024 + 1,), float("nan"), device=dev)
+    out = buf[1:].view(9, 1024)
+    layer.prefill(x, out=out)
+    assert (host(out) == want).all()
+    assert np.isnan(host(buf)[0])
+
+
 def kq_layer(dev, seed, et, st, H, F, E, K, gate_vec=True):
     """Experts of type et (device quantizer), a K-quant shared expert of type
     st from the independent packer (valid random blocks)."""
