@@ -340,7 +340,7 @@ def main():
                         nc[f"threads_{nt}"] = {"us_per_token": round(float(np.median(ts)) * 1e6, 1),
                                                "us_cpu_experts": round(float(np.median(te)) * 1e6, 1),
                                                "GBs_cpu_selected": round(sel3 / float(np.median(te)) / 1e9, 2)}
-                    nc["avx2"] = int(CPU.lib().chimere_cpu_has_avx2())
+                    nc["isa"] = ["portable", "avx2", "avx512"][CPU.lib().chimere_cpu_isa()]
                     extra["ncmoe_m1_iq3s_q5k"] = nc
                     del ln.cpu_experts
                 del l5, sh5

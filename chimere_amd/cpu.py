@@ -29,7 +29,7 @@ SIGNATURES = [
     ("ggml_ffi_iq3s_row_bytes", szt, [i32]),
     ("ggml_ffi_q8k_row_bytes", szt, [i32]),
     ("chimere_ncmoe_experts", i32, [vp, vp, vp, szt, szt, szt, vp, vp, i32, vp, vp, i32, i32, i32, i32]),
-    ("chimere_cpu_has_avx2", i32, []),
+    ("chimere_cpu_isa", i32, []),
 ]
 
 _lib = None

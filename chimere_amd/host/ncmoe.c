@@ -164,15 +164,50 @@ __attribute__((target("avx2"))) static int32_t sb_isum_avx2(const uint8_t *w, co
     return _mm_cvtsi128_si32(_mm_add_epi32(s2, _mm_shuffle_epi32(s2, 0xB1)));
 }
 
+/* AVX-512 (F + BW): two sub-blocks (64 weights) per step.  The 16 codebook
+ * entries come from one 16-lane gather (the high index bits set by a lane
+ * mask test), the 64 sign bits negate the activations as a byte mask, and
+ * the two sub-blocks' multipliers sit in the low / high 256 bits of the
+ * multiplier vector. */
+__attribute__((target("avx512f,avx512bw"))) static int32_t sb_isum_avx512(const uint8_t *w, const int8_t *q) {
+    const __m512i lane_bit = _mm512_setr_epi32(1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024, 2048, 4096, 8192,
+                                               16384, 32768);
+    __m512i acc = _mm512_setzero_si512();
+    for (int ib = 0; ib < 8; ib += 2) {
+        const __m512i lo = _mm512_cvtepu8_epi32(_mm_loadu_si128((const __m128i *)(w + 2 + 8 * ib)));
+        const int qh = w[66 + ib] | (w[67 + ib] << 8);
+        const __mmask16 hb = _mm512_test_epi32_mask(_mm512_set1_epi32(qh), lane_bit);
+        const __m512i idx = _mm512_mask_or_epi32(lo, hb, lo, _mm512_set1_epi32(256));
+        const __m512i lev = _mm512_i32gather_epi32(idx, (const void *)k_grid, 4);
+        uint64_t sg;
+        memcpy(&sg, w + 74 + 4 * ib, 8);
+        const __m512i qv = _mm512_loadu_si512((const void *)(q + 32 * ib));
+        const __m512i qs = _mm512_mask_sub_epi8(qv, (__mmask64)sg, _mm512_setzero_si512(), qv);
+        const int sc = w[106 + ib / 2];
+        const __m512i mult = _mm512_mask_set1_epi16(_mm512_set1_epi16((short)(1 + 2 * (sc & 0xF))), (__mmask32)0xFFFF0000u,
+                                                    (short)(1 + 2 * (sc >> 4)));
+        acc = _mm512_add_epi32(acc, _mm512_madd_epi16(_mm512_maddubs_epi16(lev, qs), mult));
+    }
+    return _mm512_reduce_add_epi32(acc);
+}
+
 typedef int32_t (*isum_fn)(const uint8_t *, const int8_t *);
 static isum_fn g_isum;
 
-/* chosen once at load time, before any caller thread exists;
- * CHIMERE_CPU_PORTABLE=1 selects the portable loop (its tests use it) */
+/* chosen once at load time, before any caller thread exists: AVX-512, else
+ * AVX2, else the portable loop (all give the same integers);
+ * CHIMERE_CPU_NO_AVX512=1 / CHIMERE_CPU_PORTABLE=1 step down (for tests) */
 __attribute__((constructor)) static void choose_isum(void) {
     __builtin_cpu_init();
     const char *e = getenv("CHIMERE_CPU_PORTABLE");
-    g_isum = __builtin_cpu_supports("avx2") && !(e && e[0] == '1') ? sb_isum_avx2 : sb_isum_scalar;
+    const int portable = e && e[0] == '1';
+    const char *e2 = getenv("CHIMERE_CPU_NO_AVX512");
+    if (!portable && !(e2 && e2[0] == '1') && __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw"))
+        g_isum = sb_isum_avx512;
+    else if (!portable && __builtin_cpu_supports("avx2"))
+        g_isum = sb_isum_avx2;
+    else
+        g_isum = sb_isum_scalar;
 }
 
 static inline isum_fn pick_isum(void) { return g_isum; }
@@ -308,4 +343,4 @@ int chimere_ncmoe_experts(const void *gate_exps, const void *up_exps, const void
     return CHIMERE_CPU_OK;
 }
 
-int chimere_cpu_has_avx2(void) { return pick_isum() == sb_isum_avx2; }
+int chimere_cpu_isa(void) { return pick_isum() == sb_isum_avx512 ? 2 : pick_isum() == sb_isum_avx2 ? 1 : 0; }

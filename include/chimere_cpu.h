@@ -59,8 +59,8 @@ int chimere_ncmoe_experts(const void* gate_exps, const void* up_exps, const void
                           int top_k, const float* hidden, float* combined, int hidden_size, int expert_ffn,
                           int n_experts, int nthreads);
 
-/* 1 when the AVX2 integer kernel is in use, 0 for the portable one (same results) */
-int chimere_cpu_has_avx2(void);
+/* integer kernel in use: 2 AVX-512, 1 AVX2, 0 portable (all give the same results) */
+int chimere_cpu_isa(void);
 
 #ifdef __cplusplus
 }

@@ -260,35 +260,24 @@ def test_ncmoe_rejects_bad_arguments(bank):
         cpu.iq3s_gemv_cpu(g[0], x, F, 300)
 
 
-def test_portable_loop_equals_avx2():
-    """The portable integer loop (chosen without AVX2) gives the same bits."""
+@pytest.mark.parametrize("env,isa", [({"CHIMERE_CPU_PORTABLE": "1"}, 0), ({"CHIMERE_CPU_NO_AVX512": "1"}, 1)])
+def test_other_integer_kernels_equal_the_oracle(env, isa):
+    """The AVX2 and portable integer loops (chosen where AVX-512 / AVX2 are
+    missing) give the same bits as the oracle."""
+    if isa == 1 and not open("/proc/cpuinfo").read().count(" avx2"):
+        pytest.skip("no AVX2 on this host")
     code = ("import sys, numpy as np; sys.path[:0] = [%r, %r]; import oracle as O; from chimere_amd import cpu;"
             "rng = np.random.default_rng(4); W = O.quantize(O.IQ3_S, rng.normal(0, .03, 40 * 1024).astype(np.float32));"
             "x = rng.normal(0, 1, 1024).astype(np.float32);"
-            "assert cpu.lib().chimere_cpu_has_avx2() == 0;"
+            "assert cpu.lib().chimere_cpu_isa() == %d, cpu.lib().chimere_cpu_isa();"
             "y = cpu.iq3s_gemv_cpu(W, x, 40, 1024); w = O.gemv_iq3s_q8K(W, x, 40, 1024);"
-            "assert (y.view(np.uint32) == w.view(np.uint32)).all(); print('ok')") % (ROOT, os.path.join(ROOT, "tests"))
-    env = dict(os.environ, CHIMERE_CPU_PORTABLE="1")
-    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=120)
+            "assert (y.view(np.uint32) == w.view(np.uint32)).all(); print('ok')") % (ROOT, os.path.join(ROOT, "tests"), isa)
+    r = subprocess.run([sys.executable, "-c", code], env=dict(os.environ, **env), capture_output=True, text=True,
+                       timeout=120)
     assert r.returncode == 0 and "ok" in r.stdout, r.stderr
 
 
-def test_oracle_layer_ncmoe_composition(bank):
-    """oracle.moe_ncmoe = the oracle's router/top-k, then the CPU expert loop,
-    then the shared expert of oracle.moe (its difference to moe without the
-    shared expert equals that of moe_ncmoe to within rounding)."""
-    g, u, d = bank
-    rng = np.random.default_rng(21)
-    router = (rng.normal(0, 0.02, (E, H))).astype(np.float32)
-    sh = (O.quantize(O.Q8_0, rng.normal(0, .02, F * H).astype(np.float32)),
-          O.quantize(O.Q8_0, rng.normal(0, .02, F * H).astype(np.float32)),
-          O.quantize(O.Q8_0, rng.normal(0, .02, H * F).astype(np.float32)))
-    x = rng.normal(0, 1, (2, H)).astype(np.float32)
-    o0, ids, wts = O.moe_ncmoe(x, router, g, u, d, O.IQ3_S, 3)
-    m0, mids, mwts = O.moe(x, router, g, u, d, O.IQ3_S, 3)
-    assert (ids == mids).all() and (wts == mwts).all()
-    for t in range(2):
-        assert (o0[t] == O.ncmoe(x[t], g, u, d, ids[t], wts[t], H, F)).all()
-    o1, _, _ = O.moe_ncmoe(x, router, g, u, d, O.IQ3_S, 3, sh=sh, sh_type=O.Q8_0)
-    m1, _, _ = O.moe(x, router, g, u, d, O.IQ3_S, 3, sh=sh, sh_type=O.Q8_0)
-    assert np.abs((o1 - o0) - (m1 - m0)).max() <= 1e-5 * np.abs(m1 - m0).max()
+def test_isa_in_use():
+    flags = open("/proc/cpuinfo").read()
+    want = 2 if (" avx512f" in flags and " avx512bw" in flags) else 1 if " avx2" in flags else 0
+    assert cpu.lib().chimere_cpu_isa() == want
