@@ -193,31 +193,57 @@ class MoeLayer:
         self._h_w = torch.empty(self.K, dtype=torch.float32, pin_memory=pin)
         self._h_acc = torch.empty(self.H, dtype=torch.float32, pin_memory=pin)
 
+    def _nc_capture(self):
+        """HIP graphs of the device parts of forward_ncmoe: routing (from the
+        static input buffer to ids / weights) and the shared-expert tail (from
+        the static input and routed-sum buffers to the output)."""
+        H, F, K, dev = self.H, self.F, self.K, self.device
+        bufs = self._nc_bufs = G.GgmlGpuBuffers.with_moe(max(H, F), max(H, F), F, H, K, device=dev)
+        self._nc_x = torch.zeros(H, dtype=torch.float32, device=dev)
+        self._nc_accum = torch.zeros(H, dtype=torch.float32, device=dev)
+        s = torch.cuda.Stream(device=dev)
+        s.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(s):                      # first calls outside capture
+            self._route(self._nc_x, bufs)
+            self._shared_tail(self._nc_x, self._nc_accum, bufs)
+        torch.cuda.current_stream(dev).wait_stream(s)
+        torch.cuda.synchronize(dev)
+        self._g_route = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self._g_route):
+            self._nc_ids, self._nc_w = self._route(self._nc_x, bufs)
+        self._g_tail = None                             # no shared expert: the routed sum is the output
+        self._nc_out = self._nc_accum
+        if self.shared_type >= 0:
+            self._g_tail = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self._g_tail):
+                self._nc_out = self._shared_tail(self._nc_x, self._nc_accum, bufs)
+
     def forward_ncmoe(self, x, nthreads=4):
         """One token with the routed experts on the host (moe_ffn.rs:1507-1591):
         router and top-k on the device, then hidden state, ids and weights to
         the host, libchimere_cpu.so's expert loop, the sum back to the device
-        and the shared expert there.  Returns (out [H], ids [K], weights [K]);
-        without a shared expert `out` is a buffer the next call overwrites."""
+        and the shared expert there.  The device parts replay two captured
+        HIP graphs.  Returns (out [H], ids [K], weights [K]): buffers of this
+        layer that the next call overwrites."""
         from . import cpu
         if not hasattr(self, "cpu_experts"):
             raise RuntimeError("attach_cpu_experts() first")
         assert x.numel() == self.H
-        x = x.reshape(self.H)
-        H, F, K, dev = self.H, self.F, self.K, self.device
-        if not hasattr(self, "_nc_bufs"):
-            self._nc_bufs = G.GgmlGpuBuffers.with_moe(max(H, F), max(H, F), F, H, K, device=dev)
-            self._nc_accum = torch.empty(H, dtype=torch.float32, device=dev)
-        bufs = self._nc_bufs
-        ids, w = self._route(x, bufs)
-        self._h_ids.copy_(ids, non_blocking=True)
-        self._h_w.copy_(w, non_blocking=True)
-        self._h_x.copy_(x, non_blocking=True)
-        torch.cuda.current_stream(dev).synchronize()     # the host reads these next
+        H, F = self.H, self.F
+        if not hasattr(self, "_g_route"):
+            self._nc_capture()
+        self._nc_x.copy_(x.reshape(H))
+        self._g_route.replay()
+        self._h_ids.copy_(self._nc_ids, non_blocking=True)
+        self._h_w.copy_(self._nc_w, non_blocking=True)
+        self._h_x.copy_(self._nc_x, non_blocking=True)
+        torch.cuda.current_stream(self.device).synchronize()     # the host reads these next
         g, u, d = self.cpu_experts
         cpu.ncmoe_experts(g, u, d, self._h_ids.numpy(), self._h_w.numpy(), self._h_x.numpy(), H, F,
                           out=self._h_acc.numpy(), nthreads=nthreads)
         # stream-ordered: the next call's synchronize also covers this copy
         # before _h_acc is written again
         self._nc_accum.copy_(self._h_acc, non_blocking=True)
-        return self._shared_tail(x, self._nc_accum, bufs), ids, w
+        if self._g_tail is not None:
+            self._g_tail.replay()
+        return self._nc_out, self._nc_ids, self._nc_w
