@@ -115,6 +115,26 @@ def test_prefill_repeat_and_zero(dev):
     assert np.isfinite(z).all()
 
 
+def test_prefill_more_pairs_than_plan_threads(dev):
+    """T * K above 4096: the plan's count and scatter passes take several
+    batches of pairs.  Sampled tokens bit-exact against the oracle, every
+    routing index against the decode entry point's, and the first tokens
+    equal to a shorter chunk's (each token's output depends only on it)."""
+    layer = build(dev, 31, H=1024, F=256, E=64, K=8)
+    g = torch.Generator(device=dev).manual_seed(17)
+    T = 700                                     # 5600 pairs
+    x = torch.randn(T, 1024, generator=g, device=dev)
+    sample = list(range(0, T, 37)) + [T - 1]
+    og, ig, wg = prefill_check(layer, x, sample=sample)
+    short = host(layer.prefill(x[:130].contiguous()))
+    assert (short == og[:130]).all()
+    ids = torch.zeros(8, layer.K, dtype=torch.int32, device=dev)
+    wts = torch.zeros(8, layer.K, dtype=torch.float32, device=dev)
+    for t0 in (0, 350, 692):
+        layer.forward(x[t0:t0 + 8].contiguous(), ids=ids, wts=wts)
+        assert (host(ids) == ig[t0:t0 + 8]).all()
+
+
 def test_prefill_unaligned_output(dev):
     """An output buffer that is not 16-byte aligned (a view one float into an
     allocation) gets the same bits as an aligned one."""
