@@ -251,6 +251,15 @@ constexpr int pf_row_chunk_bytes() {
 template <int T>
 constexpr int pf_lds_row() { return T == T_IQ3_S ? 128 : pf_row_chunk_bytes<T>(); }
 
+// LDS row strides of the two-stage path, padded so that the 16 rows a wave
+// reads at one block offset spread over the banks: a stride that is a
+// multiple of 128 bytes puts every row on the same banks (IQ3_S: 128 -> 144);
+// the activation rows (PF_CHUNK Q8_1 blocks, 288 bytes) get one more 16-byte
+// piece (304: the A-fragment reads of a half-wave on distinct banks)
+template <int T>
+constexpr int pf_lds_row_al() { return pf_lds_row<T>() % 128 == 0 ? pf_lds_row<T>() + 16 : pf_lds_row<T>(); }
+constexpr int PF_XROW = PF_CHUNK * 36, PF_XROW_AL = PF_XROW + 16;
+
 __constant__ uint32_t c_iq3s_grid_pf[512] = CHIMERE_IQ3S_GRID_INIT;
 
 // 8 weight values of block b of an LDS row as int8, and f32(d); IQ3_S also
@@ -351,11 +360,11 @@ __device__ __forceinline__ long pf_b_frag(const uint8_t* row, int b, int q, uint
 // Per-block metadata of the staged activation blocks (PF_TILE pairs x
 // PF_CHUNK blocks, pair-major, 36 bytes each): xd[b][m] = f32(d),
 // xs8[b][m] = -8 * sum(q) (Q4_0 correction; the MFMA accumulator's start)
-__device__ __forceinline__ void pf_xmeta(const uint8_t* xl, float* xd, int* xs8) {
+__device__ __forceinline__ void pf_xmeta(const uint8_t* xl, float* xd, int* xs8, int xr) {
     const int i = threadIdx.x;
     if (i < PF_TILE * PF_CHUNK) {
         const int m = i / PF_CHUNK, b = i % PF_CHUNK;
-        const uint8_t* blk = xl + i * 36;
+        const uint8_t* blk = xl + m * xr + b * 36;
         int s = 0;
 #pragma unroll
         for (int k = 0; k < 8; k++) s = dot4(*(const int*)(blk + 4 + 4 * k), 0x01010101, s);
@@ -389,7 +398,7 @@ __device__ __forceinline__ void pf_issue(uint8_t* wl, const uint8_t* w, int64_t 
 // PRE: read the per-superblock fields of the rows once per chunk (measured
 // faster on the two-stage gate/up path, slower on the one-stage down path)
 template <int T, int NTN, bool PRE>
-__device__ __forceinline__ void pf_mma_chunk(const uint8_t* xl, const float* xd, const int* xs8,
+__device__ __forceinline__ void pf_mma_chunk(const uint8_t* xl, int xr, const float* xd, const int* xs8,
                                              const uint8_t* wrows, int cbytes, int nb, const uint32_t* grid,
                                              float (&acc)[NTN][4]) {
     const int lane = threadIdx.x & 63, q = lane >> 4, c = lane & 15;
@@ -408,7 +417,7 @@ __device__ __forceinline__ void pf_mma_chunk(const uint8_t* xl, const float* xd,
     for (int b = 0; b <= nb; b++) {
         float4 dx;
         if (b < nb) {
-            const uint8_t* ab = xl + (c * PF_CHUNK + b) * 36 + 4 + 8 * q;
+            const uint8_t* ab = xl + c * xr + b * 36 + 4 + 8 * q;
             const long af = (long)(((uint64_t) * (const uint32_t*)(ab + 4) << 32) | *(const uint32_t*)ab);
             dx = *(const float4*)(xd + b * PF_TILE + 4 * q);
             v4i c0 = {0, 0, 0, 0};
@@ -482,10 +491,11 @@ __device__ __forceinline__ void pf_gemm_k(const PfStage& s0, const PfStage& s1, 
                                           const uint8_t* w1, int64_t rb, int nbk, const uint8_t* xsrc,
                                           const int* xrows, int64_t xstride, int wrow0, const uint32_t* grid,
                                           float (&acc)[NTN][4]) {
-    constexpr int CB = pf_row_chunk_bytes<T>(), CBL = pf_lds_row<T>();
-    static_assert(!AL || CBL % 16 == 0, "chunk rows in 16-byte pieces");
-    constexpr int PCB = CBL / 16, PER = 36 * PF_CHUNK / 16;
-    constexpr int TW = NR * PCB, TWP = (TW + 63) & ~63, TOT = TWP + PF_TILE * PER;
+    constexpr int CB = pf_row_chunk_bytes<T>(), CBL = pf_lds_row<T>(), CBLP = pf_lds_row_al<T>();
+    static_assert(!AL || (CBL % 16 == 0 && CBLP % 16 == 0), "chunk rows in 16-byte pieces");
+    // pieces per row (copied) and per LDS row slot (the rest of a slot is padding)
+    constexpr int PCB = CBL / 16, PCBP = CBLP / 16, PER = PF_XROW / 16, PERP = PF_XROW_AL / 16;
+    constexpr int TW = NR * PCBP, TWP = (TW + 63) & ~63, TOT = TWP + PF_TILE * PERP;
 #pragma unroll
     for (int n = 0; n < NTN; n++)
 #pragma unroll
@@ -499,9 +509,9 @@ __device__ __forceinline__ void pf_gemm_k(const PfStage& s0, const PfStage& s1, 
             pf_issue(s0.w + n0 * CB, w1 + goff, rb, NR - n0, CB, s0.x, xsrc, xrows, xstride, xoff);
             lds_copy_wait();
             __syncthreads();
-            pf_xmeta(s0.x, s0.xd, s0.xs);
+            pf_xmeta(s0.x, s0.xd, s0.xs, PF_XROW);
             __syncthreads();
-            pf_mma_chunk<T, NTN, false>(s0.x, s0.xd, s0.xs, s0.w + wrow0 * CB, CB, PF_CHUNK, grid, acc);
+            pf_mma_chunk<T, NTN, false>(s0.x, PF_XROW, s0.xd, s0.xs, s0.w + wrow0 * CB, CB, PF_CHUNK, grid, acc);
             __syncthreads();
         }
     } else {
@@ -521,17 +531,21 @@ __device__ __forceinline__ void pf_gemm_k(const PfStage& s0, const PfStage& s1, 
             pcol[k] = 0;
             if (c0 < TWP) {
                 if (cc < TW) {
-                    const int row = cc / PCB, col = cc - row * PCB;
-                    psrc[k] = (row < n0 ? w0 + row * rb : w1 + (row - n0) * rb) + col * 16;
-                    pcol[k] = col * 16;
-                    pval[k] = true;
+                    const int row = cc / PCBP, col = cc - row * PCBP;
+                    if (col < PCB) {
+                        psrc[k] = (row < n0 ? w0 + row * rb : w1 + (row - n0) * rb) + col * 16;
+                        pcol[k] = col * 16;
+                        pval[k] = true;
+                    }
                 }
             } else if (c0 < TOT) {
                 const int xc = cc - TWP;
-                if (xc < PF_TILE * PER) {
-                    const int r = xc / PER, col = xc - r * PER;
-                    psrc[k] = xsrc + xrows[r] * xstride + col * 16;
-                    pval[k] = true;
+                if (xc < PF_TILE * PERP) {
+                    const int r = xc / PERP, col = xc - r * PERP;
+                    if (col < PER) {
+                        psrc[k] = xsrc + xrows[r] * xstride + col * 16;
+                        pval[k] = true;
+                    }
                 }
             }
         }
@@ -557,10 +571,11 @@ __device__ __forceinline__ void pf_gemm_k(const PfStage& s0, const PfStage& s1, 
         auto step = [&](int c, const PfStage& cur, const PfStage& nxt) {
             wait_vm<0>();
             lds_barrier();   // chunk c landed (every wave's share)
-            pf_xmeta(cur.x, cur.xd, cur.xs);
+            pf_xmeta(cur.x, cur.xd, cur.xs, PF_XROW_AL);
             if (c + 1 < nc) issue(c + 1, nxt);
             lds_barrier();   // metadata written
-            pf_mma_chunk<T, NTN, true>(cur.x, cur.xd, cur.xs, cur.w + wrow0 * CBL + (c * CB & 15), CBL, PF_CHUNK, grid, acc);
+            pf_mma_chunk<T, NTN, true>(cur.x, PF_XROW_AL, cur.xd, cur.xs, cur.w + wrow0 * CBLP + (c * CB & 15), CBLP,
+                                       PF_CHUNK, grid, acc);
         };
         issue(0, s0);
         for (int c = 0; c < nc; c += 2) {
@@ -590,8 +605,8 @@ __device__ __forceinline__ void pf_gemm(const PfStage& s0, const PfStage& s1, co
 }
 
 template <int T>
-constexpr int pf_wst(int nrows) { return nrows * pf_lds_row<T>() + 16; }
-constexpr int PF_XST = PF_TILE * PF_CHUNK * 36;
+constexpr int pf_wst(int nrows) { return nrows * pf_lds_row_al<T>() + 16; }
+constexpr int PF_XST = PF_TILE * PF_XROW_AL;
 
 // LDS arrays of the two pipeline stages (separate arrays) and their PfStage
 #define PF_STAGE_ARRAYS(WS0, WS1)                                                                     \
