@@ -573,9 +573,23 @@ typedef __attribute__((address_space(1))) void glb_void_t;
 // lds_copy_wait() + __syncthreads().
 template <bool DW = false, int CPOL = 0>
 __device__ __forceinline__ void stage_rows(uint8_t* __restrict__ lds, const uint8_t* __restrict__ g,
-                                           int64_t gstride, int nrows, int seg, int tid, int nthreads) {
+                                           int64_t gstride, int nrows, int seg, int tid, int nthreads,
+                                           int lseg = 0) {
+    // lseg: LDS row stride when it differs from seg (a padded stride, for the
+    // 16-byte piece path only; the caller passes it only with seg % 16 == 0)
+    if (lseg == 0) lseg = seg;
     const uintptr_t al = (uintptr_t)g | (uintptr_t)gstride | (uintptr_t)seg | (uintptr_t)lds;
-    if (gstride == seg && (((uintptr_t)g | (uintptr_t)lds | (uintptr_t)(seg * nrows)) & 15) == 0) {
+    if (lseg != seg) {
+        const int per = seg >> 4, lper = lseg >> 4, tot = lper * nrows;
+        const int lane = tid & 63, wave = tid >> 6, nw = nthreads >> 6;
+        for (int c0 = wave * 64; c0 < tot; c0 += nw * 64) {
+            const int c = c0 + lane;
+            const int r = c / lper, col = c - r * lper;
+            if (c < tot && col < per)   // the rest of an LDS row is padding
+                __builtin_amdgcn_global_load_lds((const glb_void_t*)(g + r * gstride + col * 16),
+                                                 (lds_void_t*)(lds + c0 * 16), 16, 0, CPOL);
+        }
+    } else if (gstride == seg && (((uintptr_t)g | (uintptr_t)lds | (uintptr_t)(seg * nrows)) & 15) == 0) {
         // rows contiguous in memory and the whole run 16-byte aligned (even
         // when a row is not, e.g. 220-byte IQ3_S rows): one linear copy
         const int tot = seg * nrows / 16;

@@ -38,11 +38,17 @@ struct MmvqArgs {
 // CU, and at 64 blocks four are resident per CU already.
 constexpr int MMVQ_BLOCKS = 64;
 
+// LDS row padding of the tile (bytes): with it the 4 rows a wave reads at
+// once start on different banks (from a model of the block reads' bank
+// conflicts: Q4_0 1152 -> 1200 B, Q8_0 2176 -> 2224 B, IQ3_S 880 -> 960 B)
+template <int T>
+constexpr int mmvq_pad() { return T == T_Q4_0 || T == T_Q4_0S || T == T_Q8_0 ? 48 : (T == T_IQ3_S ? 80 : 0); }
+
 template <int T, int NTOK>
 __global__ __launch_bounds__(GEMV_THREADS) void k_mmvq(MmvqArgs a) {
     constexpr int CBLK = MMVQ_BLOCKS;
-    constexpr int CB = chunk_bytes<T>(CBLK);
-    __shared__ __attribute__((aligned(16))) uint8_t tile[TILE_ROWS * CB + 16];
+    constexpr int CB = chunk_bytes<T>(CBLK), PAD = mmvq_pad<T>();
+    __shared__ __attribute__((aligned(16))) uint8_t tile[TILE_ROWS * (CB + PAD) + 16];
     __shared__ XLds xs[NTOK][CBLK];
     __shared__ uint32_t grid[T == T_IQ3_S ? 512 : 1];
 
@@ -57,7 +63,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_mmvq(MmvqArgs a) {
         for (int i = tid; i < 512; i += GEMV_THREADS) grid[i] = c_iq3s_grid_mmvq[i];
 
     float acc[1][NTOK];
-    tile_gemv<T, NTOK, TILE_ROWS, 1, CBLK, CPOL_STREAM>(tile, &xs[0][0], grid,
+    tile_gemv<T, NTOK, TILE_ROWS, 1, CBLK, CPOL_STREAM, PAD>(tile, &xs[0][0], grid,
                                      a.W + e * a.w_slot_stride + (int64_t)r0 * rb, nr,
                                      nullptr, 0, rb, a.ncols, a.x + slot * a.x_slot_stride, a.x_tok_stride,
                                      nullptr, a.ntok, acc);

@@ -59,7 +59,10 @@ __device__ __forceinline__ void xlds_to_blk(const XLds& s, XBlk& x) {
 // and of 8 for IQ3_S); xs holds NT * CBLK decoded blocks (token-major).
 // CPOL: cache policy of the weight copies (2 = non-temporal: weights are
 // streamed once per call).
-template <int T, int NT, int RG, int RPG, int CBLK = ChunkGeom<T>::BLOCKS, int CPOL = 0>
+// PAD: bytes added to the LDS row stride of 16-byte multiple chunk rows, so
+// that the rows a wave reads at once start on different banks (the tile
+// buffer then needs rows * (chunk bytes + PAD))
+template <int T, int NT, int RG, int RPG, int CBLK = ChunkGeom<T>::BLOCKS, int CPOL = 0, int PAD = 0>
 __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds* __restrict__ xs,
                                           const uint32_t* __restrict__ grid,
                                           const uint8_t* base1, int n1, const uint8_t* base2, int n2,
@@ -80,10 +83,16 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds* __re
         const int cb = min(CBLK, nb - b0);
         const int seg = chunk_bytes<T>(cb);
         const int64_t goff = (int64_t)b0 / (QTraits<T>::ELEMS / QK) * QTraits<T>::BYTES;
+        // LDS row stride: seg (== CB except in a ragged last chunk), + PAD for
+        // 16-byte pieces from 16-byte aligned rows
+        const int lseg = PAD && ((seg | goff) & 15) == 0 &&
+                                 (((uintptr_t)base1 | (uintptr_t)rb | (uintptr_t)tile) & 15) == 0 &&
+                                 (n2 == 0 || ((uintptr_t)base2 & 15) == 0)
+                             ? seg + PAD
+                             : seg;
         __syncthreads();   // previous users of tile / xs are done
-        // rows are packed with stride seg (== CB except in a ragged last chunk)
-        if (n1) stage_rows<stage_dw<T>(), CPOL>(tile, base1 + goff, rb, n1, seg, tid, NTH);
-        if (n2) stage_rows<stage_dw<T>(), CPOL>(tile + n1 * seg, base2 + goff, rb, n2, seg, tid, NTH);
+        if (n1) stage_rows<stage_dw<T>(), CPOL>(tile, base1 + goff, rb, n1, seg, tid, NTH, lseg);
+        if (n2) stage_rows<stage_dw<T>(), CPOL>(tile + n1 * lseg, base2 + goff, rb, n2, seg, tid, NTH, lseg);
         for (int i = tid; i < ntok * cb; i += NTH) {
             const int t = i / cb, b = i - t * cb;
             const int tk = toks ? toks[t] : t;
@@ -108,7 +117,7 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds* __re
                     const int row_i = g + RG * r;
                     if (row_i < nr) {
                         WBlk wb;
-                        block_decode<T>(tl + row_i * seg, b, grid, wb);
+                        block_decode<T>(tl + row_i * lseg, b, grid, wb);
                         acc[r][0] = wacc<T>(wb, xb, acc[r][0]);
                     }
                 }
@@ -118,7 +127,7 @@ __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds* __re
             for (int r = 0; r < RPG; r++) {
                 const int row_i = g + RG * r;
                 if (row_i < nr) {
-                    const uint8_t* row = tl + row_i * seg;
+                    const uint8_t* row = tl + row_i * lseg;
                     for (int b = j; b < cb; b += SLOTS) {
                         WBlk wb;   // decoded once, used for every token
                         block_decode<T>(row, b, grid, wb);
