@@ -665,9 +665,10 @@ __device__ __forceinline__ void stage_rows(uint8_t* __restrict__ lds, const uint
 template <int CPOL, class XSrc>
 __device__ __forceinline__ int stage_spans(uint8_t* __restrict__ lds, const uint8_t* g1, int n1, const uint8_t* g2,
                                            int n2, int64_t gstride, int seg, int* rs_out,
-                                           uint8_t* __restrict__ xlds, int nx, XSrc xsrc, int tid, int nthreads) {
+                                           uint8_t* __restrict__ xlds, int nx, XSrc xsrc, int tid, int nthreads,
+                                           int minper = 0) {
     const int pre = (int)((uintptr_t)g1 & 15);
-    const int per = (pre + seg + 15) >> 4;
+    const int per0 = (pre + seg + 15) >> 4, per = per0 > minper ? per0 : minper;   // copied pieces / LDS slots per row
     *rs_out = per * 16;
     const uint8_t* b1 = g1 - pre;
     const uint8_t* b2 = g2 - pre;
@@ -682,7 +683,8 @@ __device__ __forceinline__ int stage_spans(uint8_t* __restrict__ lds, const uint
                 const int cc = second ? c - t1 : c;
                 const int r = cc / per, col = cc - r * per;
                 const uint8_t* src = (second ? b2 : b1) + r * gstride + col * 16;
-                __builtin_amdgcn_global_load_lds((const glb_void_t*)src, (lds_void_t*)(lds + c0 * 16), 16, 0, CPOL);
+                if (col < per0)
+                    __builtin_amdgcn_global_load_lds((const glb_void_t*)src, (lds_void_t*)(lds + c0 * 16), 16, 0, CPOL);
             }
         } else if (c < tot) {
             __builtin_amdgcn_global_load_lds((const glb_void_t*)xsrc(c - twp), (lds_void_t*)(xlds + (c0 - twp) * 16),

@@ -189,8 +189,11 @@ __device__ __forceinline__ void tile_gemv_db(uint8_t* __restrict__ tile, int TB,
         for (int t = 0; t < NT; t++) acc[r][t] = 0.0f;
     // 16-byte aligned spans of 4-byte aligned rows (IQ3_S, Q6_K, MXFP4 chunks)
     // where they fit the buffer: 16-byte copies instead of dword ones
+    // IQ3_S chunks of 16 blocks: 288-byte LDS rows (the spans need 224 or
+    // 240), which spread a wave's 4 rows over the banks (M=8 layer -1 %)
+    constexpr int SPER = T == T_IQ3_S && CBLK == 16 ? 18 : 0;
     const bool spans = stage_dw<T>() && (rb & 15) == 0 && (n2 == 0 || (((uintptr_t)base1 ^ (uintptr_t)base2) & 15) == 0) &&
-                       nr * ((chunk_bytes<T>(CBLK) + 30) / 16 * 16) <= TB;
+                       nr * max((chunk_bytes<T>(CBLK) + 30) / 16 * 16, 16 * SPER) <= TB;
     int pre0 = 0, pre1 = 0, rs0 = 0, rs1 = 0;   // per buffer: data offset and LDS row stride
     auto issue = [&](int c, int buf) {
         const int b0 = c * CBLK, cb = min(CBLK, nb - b0);
@@ -208,7 +211,7 @@ __device__ __forceinline__ void tile_gemv_db(uint8_t* __restrict__ tile, int TB,
         if (spans) {
             int rs;
             const int pre = stage_spans<CPOL>(tb, base1 + goff, n1, base2 + goff, n2, rb, seg, &rs, xb, tot, xsrc,
-                                              tid, NTH);
+                                              tid, NTH, SPER);
             if (buf) { pre1 = pre; rs1 = rs; } else { pre0 = pre; rs0 = rs; }
             return;
         }
