@@ -121,3 +121,24 @@ def test_prefill_two_stage_padded_slots(t, NR, n0):
     span_off = 14 if t == "iq3s" else 0   # (c * CB) % 16: nonzero only for 110-byte chunks
     assert (NR - 1) * CBLP + span_off + chunk_bytes(t, PF_CHUNK) + 4 <= wbuf
     assert (PF_TILE - 1) * PF_XROW_AL + (PF_CHUNK - 1) * 36 + 36 <= xbuf
+
+
+@pytest.mark.parametrize("pre", [0, 2, 4, 6, 8, 10, 12, 14])
+def test_spans_in_288_byte_slots(pre):
+    """stage_spans (common.h) with 18 LDS slots per row, as the double-buffered
+    tile stages 16-block IQ3_S chunks (two 110-byte superblocks, starting
+    `pre` bytes into a 16-byte granule): 64 rows fit the 18,448-byte buffer,
+    every piece of every row once, reads of a row's chunk inside its slot."""
+    seg, nrows, minper, TB = 220, 64, 18, 64 * 16 * 18 + 16
+    per0 = (pre + seg + 15) >> 4
+    per = max(per0, minper)
+    assert nrows * per * 16 <= TB
+    seen = set()
+    for c in range(per * nrows):
+        r, col = divmod(c, per)
+        if col < per0:
+            assert c * 16 == r * per * 16 + col * 16
+            seen.add((r, col))
+    assert len(seen) == nrows * per0
+    # the chunk's last byte (plus a 4-byte unaligned read) stays in the row's slot
+    assert pre + seg + 4 <= per * 16
