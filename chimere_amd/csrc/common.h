@@ -107,6 +107,17 @@ __device__ __forceinline__ uint32_t nib_bits(uint32_t nib) {
 __device__ __forceinline__ uint32_t nib_mask(uint32_t nib) {
     return __builtin_amdgcn_perm(0u, 0u, nib_bits(nib) | 0x0C0C0C0Cu);
 }
+// Sign masks of the two nibbles of byte j of s: bytes 0xFF where bit i (low
+// nibble: m0) / bit 4 + i (high nibble: m1) is set, i = byte index.  One
+// v_perm replicates the byte; each mask is then one AND and one v_perm whose
+// selector byte is 0 (byte 0 of 0xFFFFFF00: 0x00) or 1, 2, 4 (0xFF bytes of
+// the sources), 8 (the sign of byte 1 of 0xFFFFFF00: 0xFF) or 16..128
+// (>= 13: 0xFF).
+__device__ __forceinline__ void byte_sign_masks(uint32_t s, int j, uint32_t& m0, uint32_t& m1) {
+    const uint32_t r = __builtin_amdgcn_perm(s, s, 0x01010101u * (uint32_t)j);
+    m0 = __builtin_amdgcn_perm(0xFFFFFFFFu, 0xFFFFFF00u, r & 0x08040201u);
+    m1 = __builtin_amdgcn_perm(0xFFFFFFFFu, 0xFFFFFF00u, r & 0x80402010u);
+}
 // (hi:lo) >> 8*s, s in 0..3
 __device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t s) {
     return __builtin_amdgcn_alignbyte(hi, lo, s);
@@ -186,10 +197,11 @@ __device__ __forceinline__ void iq3s_levels(uint32_t qs0, uint32_t qs1, uint32_t
         g[2 * p + 1] = *(const uint32_t*)((const uint8_t*)grid + (ab >> 16));
     }
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-        const uint32_t b = nib_bits((sg >> (4 * k)) & 0xFu);
-        const uint32_t m = __builtin_amdgcn_perm(0u, 0u, b | 0x0C0C0C0Cu);
-        v[k] = (g[k] ^ m) + b;
+    for (int j = 0; j < 4; j++) {   // sign byte j: words 2j (low nibble), 2j+1
+        uint32_t m0, m1;
+        byte_sign_masks(sg, j, m0, m1);
+        v[2 * j] = (g[2 * j] ^ m0) + (m0 & 0x01010101u);
+        v[2 * j + 1] = (g[2 * j + 1] ^ m1) + (m1 & 0x01010101u);
     }
 }
 
