@@ -60,8 +60,14 @@ struct MoeArgs {
     int64_t hq_stride;
 };
 
+// Published plan: [nu][uexp][untok][upair], then the items of the
+// several-token gate/up launch: [ng] and ng entries {expert, ntok <= KG_NT,
+// pair0, pair1} -- each unit's tokens in groups of KG_NT, units in order.
+constexpr int KG_NT = 2;
 constexpr int PLAN_UEXP = 1, PLAN_UNTOK = 1 + MAX_TOK * MAX_K, PLAN_UPAIR = 1 + 2 * MAX_TOK * MAX_K;
-constexpr int PLAN_INTS = PLAN_UPAIR + MAX_TOK * MAX_K * MAX_TOK;
+constexpr int PLAN_NG = PLAN_UPAIR + MAX_TOK * MAX_K * MAX_TOK, PLAN_GRP = PLAN_NG + 1;
+constexpr int PLAN_INTS = PLAN_GRP + 4 * MAX_TOK * MAX_K;
+static_assert(KG_NT == 2 && MAX_TOK <= 4 * KG_NT && MAX_TOK * MAX_K <= 128, "plan groups");
 
 // Expert plan: distinct selected experts and, per expert, its (token, k) pairs.
 struct Plan {
@@ -229,6 +235,35 @@ __device__ __forceinline__ void route_plan(const MoeArgs& a, int* first, Plan& p
             P[PLAN_UEXP + i] = pl.uexp[i];
             P[PLAN_UNTOK + i] = pl.untok[i];
             for (int n = 0; n < pl.untok[i]; n++) P[PLAN_UPAIR + i * MAX_TOK + n] = pl.upair[i][n];
+        }
+        // gate/up items: unit i's ceil(untok / KG_NT) groups start at the
+        // number of groups of units < i (per-wave ballot counts; nu <= 128)
+        __shared__ int s_gtot[2];
+        int g = 0, pre = 0;
+        if (tid < 128) {
+            g = tid < nu ? (pl.untok[tid] + KG_NT - 1) / KG_NT : 0;
+            const uint64_t lt = (1ull << (tid & 63)) - 1;
+            int tot = 0;
+#pragma unroll
+            for (int k = 1; k <= MAX_TOK / KG_NT; k++) {
+                const uint64_t m = __ballot(g >= k);
+                pre += __popcll(m & lt);
+                tot += __popcll(m);
+            }
+            if ((tid & 63) == 0) s_gtot[tid >> 6] = tot;
+        }
+        __syncthreads();
+        if (tid < 128) {
+            if (tid >= 64) pre += s_gtot[0];
+            if (tid == 0) P[PLAN_NG] = s_gtot[0] + s_gtot[1];
+            for (int k = 0; k < g; k++) {
+                int* q = P + PLAN_GRP + 4 * (pre + k);
+                const int t0 = KG_NT * k, n = min(KG_NT, pl.untok[tid] - t0);
+                q[0] = pl.uexp[tid];
+                q[1] = n;
+                q[2] = pl.upair[tid][t0];
+                q[3] = n > 1 ? pl.upair[tid][t0 + 1] : 0;
+            }
         }
     }
 
@@ -860,22 +895,31 @@ constexpr int KG_RG = 16;     // KG / KD: 256 threads, 64 rows per tile (4 per r
 constexpr int KG_CHUNK = 32;
 template <int T>
 constexpr int kg_chunk() { return T == T_Q8_0 ? 16 : KG_CHUNK; }
-// KG: K chunks of 16 blocks, double-buffered where two 64-row buffers fit in
-// KG_BUF * 2 bytes (Q4_0, IQ3_S); Q8_0 rows use the same space single-buffered
+// KG: K chunks of 16 blocks, double-buffered where two 64-row buffers of
+// kg_buf bytes fit (Q4_0, Q4_K: 288-byte rows; IQ3_S: 272-byte slots for the
+// 16-byte aligned spans of its 220-byte chunks); Q8_0 / Q5_K / Q6_K rows are
+// single-buffered.  Each item carries at most KG_NT tokens, so the tile, two
+// tokens' activation chunks, the codebook and h fit in 40 KB: four
+// work-groups per CU, and a decode batch's items (M = 8: up to 64 routed
+// groups + 4 shared ones, 16 blocks each) start in one round.
 constexpr int KG_BLK = 16;
 constexpr int KG_BUF = 64 * 16 * 18 + 16;
 template <int T>
-constexpr bool kg_db() { return 64 * chunk_bytes<T>(KG_BLK) + 16 <= KG_BUF; }
+constexpr int kg_buf() { return T == T_IQ3_S ? 64 * 16 * 17 + 16 : KG_BUF; }
+template <int T>
+constexpr bool kg_db() { return 64 * chunk_bytes<T>(KG_BLK) + 16 <= kg_buf<T>(); }
+template <int T>
+constexpr int kg_tile_bytes() { return kg_db<T>() ? 2 * kg_buf<T>() : 64 * chunk_bytes<T>(KG_BLK) + 16; }
 
 template <int T>
 __device__ __forceinline__ void kg_tile(uint8_t* tile, XLds* xs, uint8_t* xraw, const uint32_t* grid, const uint8_t* g,
                                         const uint8_t* u, int64_t rb, const MoeArgs& a, const int* toks, int ntok,
-                                        float (&acc)[4][MAX_TOK]) {
+                                        float (&acc)[4][KG_NT]) {
     if (ntok == 1) {   // most experts of a decode batch serve one token: no token loop
         float a1[4][1];
         if constexpr (kg_db<T>())
-            tile_gemv_db<T, 1, KG_RG, 4, KG_BLK, CPOL_STREAM>(tile, KG_BUF, xraw, grid, g, QK, u, QK, rb, a.H, a.xq, a.xq_stride,
-                                                 toks, 1, a1);
+            tile_gemv_db<T, 1, KG_RG, 4, KG_BLK, CPOL_STREAM>(tile, kg_buf<T>(), xraw, grid, g, QK, u, QK, rb, a.H,
+                                                              a.xq, a.xq_stride, toks, 1, a1);
         else
             tile_gemv<T, 1, KG_RG, 4, KG_BLK, CPOL_STREAM>(tile, xs, grid, g, QK, u, QK, rb, a.H, a.xq, a.xq_stride, toks, 1, a1);
 #pragma unroll
@@ -883,53 +927,59 @@ __device__ __forceinline__ void kg_tile(uint8_t* tile, XLds* xs, uint8_t* xraw, 
         return;
     }
     if constexpr (kg_db<T>())
-        tile_gemv_db<T, MAX_TOK, KG_RG, 4, KG_BLK, CPOL_STREAM>(tile, KG_BUF, xraw, grid, g, QK, u, QK, rb, a.H, a.xq, a.xq_stride,
-                                                   toks, ntok, acc);
+        tile_gemv_db<T, KG_NT, KG_RG, 4, KG_BLK, CPOL_STREAM>(tile, kg_buf<T>(), xraw, grid, g, QK, u, QK, rb, a.H, a.xq,
+                                                              a.xq_stride, toks, ntok, acc);
     else
-        tile_gemv<T, MAX_TOK, KG_RG, 4, KG_BLK, CPOL_STREAM>(tile, xs, grid, g, QK, u, QK, rb, a.H, a.xq, a.xq_stride, toks, ntok,
-                                                acc);
+        tile_gemv<T, KG_NT, KG_RG, 4, KG_BLK, CPOL_STREAM>(tile, xs, grid, g, QK, u, QK, rb, a.H, a.xq, a.xq_stride, toks,
+                                                           ntok, acc);
 }
 
-// KG: grid NB + 8*ceil(M*K/8)*NB.  The first NB work-groups take the shared
-// expert (all M tokens: the heaviest items, dispatched first, block w on XCD
-// w & 7); then item V' = V - NB -> unit V'/NB, block V' % NB.  The items of
-// one unit share no weight bytes, so consecutive items go to consecutive XCDs
-// and the active items (units < nu) spread evenly over the 8 XCDs (the grid
-// runs in about 1.2 rounds of 3 work-groups per CU; an expert's blocks kept on
-// one XCD left two XCDs with 130 items for 96 slots: 1.6 us more per layer).
+// KG: grid NB * (SG + M*K), SG = ceil(M / KG_NT) shared groups (0 without a
+// shared expert).  Work-group V takes group q = V / NB, block w = V % NB:
+// groups q < SG are the shared expert's tokens [KG_NT q, KG_NT q + KG_NT),
+// the rest the plan's gate/up items (groups past the plan's count exit).
+// Consecutive work-groups run on consecutive XCDs, so the items spread evenly
+// over the 8 XCDs, and the groups of one unit (same weight rows, 16 work-groups
+// apart) on one XCD, close in time.
 template <int TE, int TS>
 __global__ __launch_bounds__(GEMV_THREADS) void k_moe_gateup(MoeArgs a) {
-    static_assert(64 * chunk_bytes<T_Q8_0>(KG_BLK) + 16 <= 2 * KG_BUF, "tile");
-    __shared__ __attribute__((aligned(16))) uint8_t tile[2 * KG_BUF];
+    constexpr int TILE = kg_tile_bytes<TE>() > kg_tile_bytes<TS>() ? kg_tile_bytes<TE>() : kg_tile_bytes<TS>();
+    __shared__ __attribute__((aligned(16))) uint8_t tile[TILE];
     // raw Q8_1 blocks (double-buffered path) or decoded blocks (single-buffered path)
-    static_assert(MAX_TOK * KG_BLK * sizeof(XLds) <= 2 * MAX_TOK * KG_BLK * Q8_1_BYTES, "xbuf");
-    __shared__ __attribute__((aligned(16))) uint8_t xraw[2 * MAX_TOK * KG_BLK * Q8_1_BYTES];
+    static_assert(KG_NT * KG_BLK * sizeof(XLds) <= 2 * KG_NT * KG_BLK * Q8_1_BYTES, "xbuf");
+    __shared__ __attribute__((aligned(16))) uint8_t xraw[2 * KG_NT * KG_BLK * Q8_1_BYTES];
     XLds* xs = (XLds*)xraw;
     __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
-    __shared__ float hg[MAX_TOK][QK], hu[MAX_TOK][QK];
-    __shared__ int toks[MAX_TOK], pairs[MAX_TOK];
-    const int NB = a.F / QK;
-    const int MK = a.M * a.K;
-    int u, w;
-    if ((int)blockIdx.x < NB) {
-        u = MK;
-        w = blockIdx.x;
-    } else {
-        const int V = blockIdx.x - NB;
-        u = V / NB;
-        w = V - u * NB;
-        if (u >= MK) return;
-    }
+    __shared__ float hg[KG_NT][QK], hu[KG_NT][QK];
+    __shared__ int toks[KG_NT], pairs[KG_NT];
+    const int NB = a.F / QK, MK = a.M * a.K;
+    const int SG = a.has_shared ? (a.M + KG_NT - 1) / KG_NT : 0;
+    const int q = blockIdx.x / NB, w = blockIdx.x - q * NB;
+    const int tid = threadIdx.x;
     int ntok;
     int64_t e;
-    if (!load_unit(a, u, pairs, toks, ntok, e)) return;
-    const int tid = threadIdx.x;
+    if (q < SG) {
+        e = -1;
+        ntok = min(KG_NT, a.M - KG_NT * q);
+        if (tid < ntok) { toks[tid] = KG_NT * q + tid; pairs[tid] = MK + KG_NT * q + tid; }
+    } else {
+        const int qq = q - SG;
+        if (qq >= a.plan[PLAN_NG]) return;
+        const int* G = a.plan + PLAN_GRP + 4 * qq;
+        e = G[0];
+        ntok = G[1];
+        if (tid < ntok) {
+            const int p = G[2 + tid];
+            pairs[tid] = p;
+            toks[tid] = p / a.K;
+        }
+    }
     if constexpr (TE == T_IQ3_S || TS == T_IQ3_S)
         for (int i = tid; i < 512; i += GEMV_THREADS) grid[i] = c_iq3s_grid_moe[i];
     // toks / pairs (written by the first ntok threads) are read by every wave
     // in the tile's first copy, which precedes the tile's first barrier
     __syncthreads();
-    float acc[4][MAX_TOK];
+    float acc[4][KG_NT];
     const int r0 = w * QK;
     if (e < 0) {
         const int64_t rb = row_bytes(TS, a.H);
@@ -944,7 +994,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_gateup(MoeArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; r++)
 #pragma unroll
-        for (int t = 0; t < MAX_TOK; t++) {
+        for (int t = 0; t < KG_NT; t++) {
             if (t < ntok) {
                 const float v = slot_reduce16(acc[r][t]);
                 if (j == 0) {
@@ -961,9 +1011,9 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_gateup(MoeArgs a) {
         const float xi = det_silu(hg[t][i]) * hu[t][i];
         const float amax = bfly32_max(__builtin_fabsf(xi)), sum = bfly32_sum(xi);
         const float d = amax / 127.0f;
-        const int q = amax == 0.0f ? 0 : (int)__builtin_roundf(xi / d);
+        const int q8 = amax == 0.0f ? 0 : (int)__builtin_roundf(xi / d);
         uint8_t* o = a.hq + (int64_t)pairs[t] * a.hq_stride + w * Q8_1_BYTES;
-        o[4 + i] = (uint8_t)(int8_t)q;
+        o[4 + i] = (uint8_t)(int8_t)q8;
         if (i == 0) *(uint32_t*)o = f2h(d) | (f2h(sum) << 16);
     }
 }
@@ -1277,7 +1327,8 @@ static void launch_layer_multi(const MoeArgs& a, int stage, hipStream_t s) {
         hipLaunchKernelGGL(k_moe_plan, dim3(1), dim3(EX_THREADS), 0, s, a);
     }
     if (stage < 0 || stage == 1)
-        hipLaunchKernelGGL((k_moe_gateup<TE, TS>), dim3(NB + 8 * ((NU - 1 + 7) / 8) * NB), dim3(GEMV_THREADS), 0, s, a);
+        hipLaunchKernelGGL((k_moe_gateup<TE, TS>), dim3(NB * ((a.has_shared ? (a.M + KG_NT - 1) / KG_NT : 0) + NU - 1)),
+                           dim3(GEMV_THREADS), 0, s, a);
     if (stage < 0 || stage == 2) {
         if constexpr (kdc_types<TE, TS>()) {
             if (kdc_fits(a, TE, TS)) {

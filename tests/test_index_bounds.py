@@ -22,7 +22,7 @@ E1_MAX_H = 2048
 ROW_PAD = 512
 BYTES = {"q4_0": 18, "q8_0": 34}
 PLAN_UEXP = 1
-PLAN_INTS = 1 + 2 * 8 * 16 + 8 * 16 * 8
+PLAN_INTS = 1 + 2 * 8 * 16 + 8 * 16 * 8 + 1 + 4 * 8 * 16
 
 
 def row_bytes(t, n):
