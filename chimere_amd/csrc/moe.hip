@@ -1095,11 +1095,14 @@ __global__ __launch_bounds__(256) void k_moe_combine_dn(MoeArgs a) {
 // owning DR output rows.  All selected units' DR down rows (one contiguous
 // run of DR * row_bytes per unit) and every pair's Q8_1(h) row are copied to
 // LDS, so the whole layer's down bytes are in flight at once (one work-group
-// per CU).  Then the tasks -- the shared expert's (row, token) pairs first,
-// then the routed (unit, row) pairs -- are dealt to the 64 groups of 16 lanes:
-// lane j decodes weight block j of the row and, for each of the unit's
-// tokens, forms fmaf(d_w * d_h, sumi, 0) against h block j, summed over the 16
-// lanes by the halving tree (the L=16 order with one block per lane, F = 512).
+// per CU).  The work is in tasks -- a weight row against its tokens -- for
+// the 64 groups of 16 lanes: lane j decodes weight block j of the row and,
+// for each token, forms fmaf(d_w * d_h, sumi, 0) against h block j, summed
+// over the 16 lanes by the halving tree (the L=16 order with one block per
+// lane, F = 512).  The shared expert's (row, token) tasks run first, while
+// the routed runs are in flight; then each wave works on the units whose runs
+// it copied, unit by unit as they land (its own copies, so its in-order copy
+// counter tells it; no barrier), its 4 groups taking rows g, g+4, ...
 // Last, each (token, row) output is the router-weighted sum in k order plus
 // the shared expert, as in k_moe_combine_dn.
 constexpr int KDC_F = 512, KDC_THREADS = 1024, KDC_MAX_UNITS = 64;
@@ -1169,7 +1172,10 @@ __global__ __launch_bounds__(KDC_THREADS) void k_moe_down_comb(MoeArgs a) {
     lds_barrier();
     const int nu = a.plan[0];
     // routed runs: wave w copies units w, w + NW, ... (a unit's source and
-    // destination bases are wave-uniform; lane l copies pieces l, l + 64, ...)
+    // destination bases are wave-uniform; lane l copies pieces l, l + 64, ...):
+    // NPW copy instructions per unit, issued after the wave's h / shared ones
+    constexpr int NPW = (PE + 63) / 64;
+    static_assert(NPW * ((KDC_MAX_UNITS + NW - 1) / NW) <= 15, "copy counter");
     for (int u = wave; u < nu; u += NW) {
         const uint8_t* src = a.down + (int64_t)s_uexp[u] * a.sd + (int64_t)r0 * kdc_rb<TE>();
         uint8_t* dst = wl + RUNS + u * RUNE;
@@ -1177,8 +1183,9 @@ __global__ __launch_bounds__(KDC_THREADS) void k_moe_down_comb(MoeArgs a) {
         for (int c0 = 0; c0 < PE; c0 += 64)
             if (c0 + lane < PE) copy16_lds_untracked(src + (c0 + lane) * 16, dst + c0 * 16);
     }
-    wait_vm<0>();
-    lds_barrier();
+    const int nown = nu > wave ? (nu - wave + NW - 1) / NW : 0;   // units this wave copied
+    wait_vm_n(NPW * nown);   // this wave's h / shared copies have landed
+    lds_barrier();           // ... and every wave's
     const int g = tid >> 4, j = tid & 15;
     // one (weight row, tokens) task: pairs pr[0..ntok) against row r
     auto task = [&](auto tag, const uint8_t* row, int r, int ntok, auto pair_of) {
@@ -1196,18 +1203,19 @@ __global__ __launch_bounds__(KDC_THREADS) void k_moe_down_comb(MoeArgs a) {
             }
         }
     };
-    // tasks: the shared expert's (row, token) pairs first (every token of the
-    // chunk uses it), then the routed (unit, row) pairs
-    const int nsh = a.has_shared ? DR * a.M : 0, ntask = nsh + nu * DR;
-    for (int k = g; k < ntask; k += KDC_THREADS / 16) {
-        if (k < nsh) {
-            const int r = k / a.M, t = k - r * a.M;
-            task(std::integral_constant<int, TS>{}, wl + r * kdc_rb<TS>(), r, 1, [&](int) { return MK + t; });
-        } else {
-            const int u = (k - nsh) / DR, r = (k - nsh) - u * DR;
+    // the shared expert's (row, token) tasks over all groups
+    const int nsh = a.has_shared ? DR * a.M : 0;
+    for (int k = g; k < nsh; k += KDC_THREADS / 16) {
+        const int r = k / a.M, t = k - r * a.M;
+        task(std::integral_constant<int, TS>{}, wl + r * kdc_rb<TS>(), r, 1, [&](int) { return MK + t; });
+    }
+    // this wave's units, each once its runs have landed
+    for (int i = 0; i < nown; i++) {
+        const int u = wave + NW * i;
+        wait_vm_n(NPW * (nown - 1 - i));
+        for (int r = g & 3; r < DR; r += 4)
             task(std::integral_constant<int, TE>{}, wl + RUNS + u * RUNE + r * kdc_rb<TE>(), r, (int)s_untok[u],
                  [&](int t) { return (int)s_upair[u][t]; });
-        }
     }
     __syncthreads();
     if (tid < a.M * DR) {
