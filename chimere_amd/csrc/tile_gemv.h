@@ -240,40 +240,23 @@ __device__ __forceinline__ void tile_gemv_db(uint8_t* __restrict__ tile, int TB,
         const uint8_t* tb = tile + buf * TB + (buf ? pre1 : pre0);
         const int seg = buf ? rs1 : rs0;   // LDS row stride of this chunk
         const uint8_t* xb = xraw + buf * XB;
-        if constexpr (NT == 1) {
-            // one token: the activation block is read once for all RPG rows
-            // (each row still accumulates its blocks in ascending order)
-            for (int b = j; b < cb; b += SLOTS) {
-                XBlk x;
-                raw_xblk<T>(xb + b * Q8_1_BYTES, x);
+        // the chunk's activation blocks of the (at most NT) tokens are read
+        // once for all RPG rows; each (row, token) still accumulates its
+        // blocks in ascending order
+        for (int b = j; b < cb; b += SLOTS) {
+            XBlk x[NT];
 #pragma unroll
-                for (int r = 0; r < RPG; r++) {
-                    const int row_i = g + RG * r;
-                    if (row_i < nr) {
-                        WBlk wb;
-                        block_decode<T>(tb + row_i * seg, b, grid, wb);
-                        acc[r][0] = wacc<T>(wb, x, acc[r][0]);
-                    }
-                }
-            }
-        } else {
+            for (int t = 0; t < NT; t++)
+                if (t < ntok) raw_xblk<T>(xb + (t * cb + b) * Q8_1_BYTES, x[t]);
 #pragma unroll
             for (int r = 0; r < RPG; r++) {
                 const int row_i = g + RG * r;
                 if (row_i < nr) {
-                    const uint8_t* row = tb + row_i * seg;
-                    for (int b = j; b < cb; b += SLOTS) {
-                        WBlk wb;
-                        block_decode<T>(row, b, grid, wb);
+                    WBlk wb;
+                    block_decode<T>(tb + __mul24(row_i, seg), b, grid, wb);
 #pragma unroll
-                        for (int t = 0; t < NT; t++) {
-                            if (t < ntok) {
-                                XBlk x;
-                                raw_xblk<T>(xb + (t * cb + b) * Q8_1_BYTES, x);
-                                acc[r][t] = wacc<T>(wb, x, acc[r][t]);
-                            }
-                        }
-                    }
+                    for (int t = 0; t < NT; t++)
+                        if (t < ntok) acc[r][t] = wacc<T>(wb, x[t], acc[r][t]);
                 }
             }
         }
