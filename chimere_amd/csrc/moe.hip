@@ -78,12 +78,16 @@ struct Plan {
     int utok[MAX_TOK * MAX_K][MAX_TOK];
 };
 
-// K1: grid E (router rows) + has_gate (shared-expert gate row) + M (x quantizers).
-template <int NT>
+// K1: grid (E + has_gate) * TS work-groups (router rows, then the
+// shared-expert gate row; TS work-groups per row, each for NT of the tokens)
+// + the x quantizers.
+template <int NT, int TS = 1>
 __global__ __launch_bounds__(256) void k_moe_route(MoeArgs a) {
     __shared__ float red[NT * 256];
-    const int row = blockIdx.x;
     const int ng = a.sh_gate_w ? 1 : 0;
+    const int nrw = (a.E + ng) * TS;
+    const int bid = blockIdx.x;
+    const int row = bid < nrw ? bid / TS : a.E + ng + (bid - nrw);
     if (row >= a.E + ng) {
         // Q8_1(x): 8 blocks per work-group (one per half-wave), so that this
         // part of the grid finishes with the router rows
@@ -100,13 +104,16 @@ __global__ __launch_bounds__(256) void k_moe_route(MoeArgs a) {
             });
         return;
     }
+    const int t0 = (bid - row * TS) * NT;
+    if (t0 >= a.M) return;
+    const int nt = min(NT, a.M - t0);
     float v[NT];
     const float* A = row < a.E ? a.router + (int64_t)row * a.H : a.sh_gate_w;
-    f32_row_dot<NT>(A, a.x, a.H, a.M, red, v);
+    f32_row_dot<NT>(A, a.x + (int64_t)t0 * a.H, a.H, nt, red, v);
     if (threadIdx.x == 0) {
-        for (int t = 0; t < a.M; t++) {
-            if (row < a.E) a.logits[t * a.E + row] = a.bias ? v[t] + a.bias[row] : v[t];
-            else a.glogit[t] = v[t];
+        for (int t = 0; t < nt; t++) {
+            if (row < a.E) a.logits[(t0 + t) * a.E + row] = a.bias ? v[t] + a.bias[row] : v[t];
+            else a.glogit[t0 + t] = v[t];
         }
     }
 }
@@ -188,7 +195,7 @@ __device__ __forceinline__ void route_plan(const MoeArgs& a, int* first, Plan& p
         // t*K+k) selecting an expert numbers it by its rank among first pairs;
         // the order of pairs inside an expert does not affect any result.
         __shared__ int s_fcnt[2], s_cnt[MAX_TOK * MAX_K];
-        for (int e = tid; e < a.E; e += EX_THREADS) first[e] = 0x7fffffff;
+        for (int e = tid; e < a.E; e += (int)blockDim.x) first[e] = 0x7fffffff;
         if (tid < MAX_TOK * MAX_K) s_cnt[tid] = 0;
         __syncthreads();
         if (tid < MK) atomicMin(&first[s_ids[tid]], tid);
@@ -225,13 +232,13 @@ __device__ __forceinline__ void route_plan(const MoeArgs& a, int* first, Plan& p
     }
     if (publish) {
         const int nu = pl.nu;
-        for (int i = tid; i < MK; i += EX_THREADS) {
+        for (int i = tid; i < MK; i += (int)blockDim.x) {
             a.wts[i] = s_w[i];
             if (a.ids_out) { a.ids_out[i] = s_ids[i]; a.w_out[i] = s_w[i]; }
         }
         int* P = a.plan;
         if (tid == 0) P[0] = nu;
-        for (int i = tid; i < nu; i += EX_THREADS) {
+        for (int i = tid; i < nu; i += (int)blockDim.x) {
             P[PLAN_UEXP + i] = pl.uexp[i];
             P[PLAN_UNTOK + i] = pl.untok[i];
             for (int n = 0; n < pl.untok[i]; n++) P[PLAN_UPAIR + i * MAX_TOK + n] = pl.upair[i][n];
@@ -860,7 +867,10 @@ __global__ __launch_bounds__((E1_MAX_K + 1) * 64) void k_moe_dc1(MoeArgs a) {
 // tile of H) with every h block of the expert's tokens (each output row
 // reduced in the L=16 order in place), KC router-weighted combine.
 
-__global__ __launch_bounds__(EX_THREADS) void k_moe_plan(MoeArgs a) {
+// one wave per token (M <= 8): 512 threads
+constexpr int PLAN_THREADS = MAX_TOK * 64;
+static_assert(PLAN_THREADS >= MAX_TOK * MAX_K, "one thread per pair");
+__global__ __launch_bounds__(PLAN_THREADS) void k_moe_plan(MoeArgs a) {
     __shared__ int first[MAX_E];
     __shared__ Plan pl;
     __shared__ int s_ids[MAX_TOK * MAX_K];
@@ -1273,9 +1283,11 @@ static WsPlan plan_ws(int H, int F, int E, int K, int M) {
 
 // K1 grid: router rows (+ the shared-expert gate row) and 8 Q8_1 blocks of x
 // per work-group
-static int route_grid(const MoeArgs& a) {
-    return a.E + (a.sh_gate_w ? 1 : 0) + a.M * ((a.H / QK + 7) / 8);
+constexpr int ROUTE_TS = 4;   // several-token router: work-groups per row
+static int route_grid(const MoeArgs& a, int ts = 1) {
+    return (a.E + (a.sh_gate_w ? 1 : 0)) * ts + a.M * ((a.H / QK + 7) / 8);
 }
+
 
 // K2 grid: all items, capped at one work-group per CU (a multiple of 8)
 static int expert_grid(int items) {
@@ -1331,8 +1343,12 @@ template <int TE, int TS>
 static void launch_layer_multi(const MoeArgs& a, int stage, hipStream_t s) {
     const int NB = a.F / QK, NU = a.M * a.K + 1;
     if (stage < 0 || stage == 0) {
-        hipLaunchKernelGGL((k_moe_route<MAX_TOK>), dim3(route_grid(a)), dim3(256), 0, s, a);
-        hipLaunchKernelGGL(k_moe_plan, dim3(1), dim3(EX_THREADS), 0, s, a);
+        // four work-groups per router row, two tokens each (M = 8: layer
+        // 49.8 -> 49.2 us uniform, 40.9 -> 39.4 us Zipf against one
+        // work-group per row; one token each or two rows per work-group
+        // measured slower)
+        hipLaunchKernelGGL((k_moe_route<MAX_TOK / ROUTE_TS, ROUTE_TS>), dim3(route_grid(a, ROUTE_TS)), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(k_moe_plan, dim3(1), dim3(PLAN_THREADS), 0, s, a);
     }
     if (stage < 0 || stage == 1)
         hipLaunchKernelGGL((k_moe_gateup<TE, TS>), dim3(NB * ((a.has_shared ? (a.M + KG_NT - 1) / KG_NT : 0) + NU - 1)),
