@@ -65,7 +65,21 @@ __global__ __launch_bounds__(256) void k_pf_router(PfArgs a) {
     __shared__ float red[32][264];   // row stride = 8 banks: the 8-lane groups read distinct banks
     const int tid = threadIdx.x;
     const int NR = a.E + (a.sh_gate_w ? 1 : 0);
-    const int e0 = blockIdx.x * PF_RE, t0 = blockIdx.y * PF_RT;
+    // 1-D grid of ET x TT tiles.  Work-groups are dealt to the 8 XCDs
+    // round-robin; when TT is a multiple of 8, XCD x takes the token tiles
+    // [x TT/8, (x+1) TT/8) against every router row, so each XCD's L2 holds
+    // the router once and only its own tokens' rows
+    const int ET = (NR + PF_RE - 1) / PF_RE, TT = (a.T + PF_RT - 1) / PF_RT;
+    int et, tt;
+    if ((TT & 7) == 0) {
+        const int x = blockIdx.x & 7, k = blockIdx.x >> 3;
+        tt = x * (TT >> 3) + k / ET;
+        et = k - (k / ET) * ET;
+    } else {
+        tt = blockIdx.x / ET;
+        et = blockIdx.x - tt * ET;
+    }
+    const int e0 = et * PF_RE, t0 = tt * PF_RT;
     const float* rows[PF_RE];
 #pragma unroll
     for (int e = 0; e < PF_RE; e++) {
@@ -813,7 +827,8 @@ static PfPlan plan_pf(int H, int F, int E, int K, int T) {
 
 template <int TE, int TS>
 static void launch_pf(const PfArgs& a, const PfPlan& p, hipStream_t s) {
-    hipLaunchKernelGGL(k_pf_router, dim3((a.E + (a.sh_gate_w ? 1 : 0) + PF_RE - 1) / PF_RE, (a.T + PF_RT - 1) / PF_RT),
+    hipLaunchKernelGGL(k_pf_router,
+                       dim3(((a.E + (a.sh_gate_w ? 1 : 0) + PF_RE - 1) / PF_RE) * ((a.T + PF_RT - 1) / PF_RT)),
                        dim3(256), 0, s, a);
     launch_quantize_q8_1(a.x, a.xq, a.H, p.xq_stride / Q8_1_BYTES * QK, a.T, s);
     hipLaunchKernelGGL(k_pf_topk, dim3(a.T), dim3(64), 0, s, a);
