@@ -12,6 +12,7 @@
 // the halving tree xor 8,4,2,1 (slot_reduce16).  sumi is the exact int32
 // block dot.  Q4_K / Q5_K blocks add a second fmaf for their min term (wacc).
 #pragma once
+#include <type_traits>
 #include "common.h"
 
 namespace chimere {
@@ -243,23 +244,32 @@ __device__ __forceinline__ void tile_gemv_db(uint8_t* __restrict__ tile, int TB,
         // the chunk's activation blocks of the (at most NT) tokens are read
         // once for all RPG rows; each (row, token) still accumulates its
         // blocks in ascending order
-        for (int b = j; b < cb; b += SLOTS) {
-            XBlk x[NT];
+        // a full tile (every row group holds RPG rows, NT tokens) runs
+        // without the per-row and per-token guards, so the rows' block
+        // decodes are straight-line code the compiler can interleave (one
+        // row's LDS reads under another's arithmetic)
+        auto blocks = [&](auto full) {
+            for (int b = j; b < cb; b += SLOTS) {
+                XBlk x[NT];
 #pragma unroll
-            for (int t = 0; t < NT; t++)
-                if (t < ntok) raw_xblk<T>(xb + (t * cb + b) * Q8_1_BYTES, x[t]);
+                for (int t = 0; t < NT; t++)
+                    if (decltype(full)::value || t < ntok) raw_xblk<T>(xb + (t * cb + b) * Q8_1_BYTES, x[t]);
 #pragma unroll
-            for (int r = 0; r < RPG; r++) {
-                const int row_i = g + RG * r;
-                if (row_i < nr) {
-                    WBlk wb;
-                    block_decode<T>(tb + __mul24(row_i, seg), b, grid, wb);
+                for (int r = 0; r < RPG; r++) {
+                    const int row_i = g + RG * r;
+                    if (decltype(full)::value || row_i < nr) {
+                        WBlk wb;
+                        block_decode<T>(tb + __mul24(row_i, seg), b, grid, wb);
 #pragma unroll
-                    for (int t = 0; t < NT; t++)
-                        if (t < ntok) acc[r][t] = wacc<T>(wb, x[t], acc[r][t]);
+                        for (int t = 0; t < NT; t++)
+                            if (decltype(full)::value || t < ntok) acc[r][t] = wacc<T>(wb, x[t], acc[r][t]);
+                    }
                 }
             }
-        }
+        };
+        // full: every row group holds RPG rows and the item has NT tokens
+        if (nr == RG * RPG && ntok == NT) blocks(std::true_type{});
+        else blocks(std::false_type{});
     }
 }
 
