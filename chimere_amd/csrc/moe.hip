@@ -1223,9 +1223,15 @@ __global__ __launch_bounds__(KDC_THREADS) void k_moe_down_comb(MoeArgs a) {
     for (int i = 0; i < nown; i++) {
         const int u = wave + NW * i;
         wait_vm_n(NPW * (nown - 1 - i));
-        for (int r = g & 3; r < DR; r += 4)
+        // the group's rows (DR / 4 of them, or one) unrolled: independent
+        // decodes the compiler can interleave
+#pragma unroll
+        for (int ri = 0; ri < (DR + 3) / 4; ri++) {
+            const int r = (g & 3) + 4 * ri;
+            if (DR % 4 != 0 && r >= DR) break;   // DR = 2: groups 2 and 3 have no row
             task(std::integral_constant<int, TE>{}, wl + RUNS + u * RUNE + r * kdc_rb<TE>(), r, (int)s_untok[u],
                  [&](int t) { return (int)s_upair[u][t]; });
+        }
     }
     __syncthreads();
     if (tid < a.M * DR) {
