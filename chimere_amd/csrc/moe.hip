@@ -814,11 +814,12 @@ __device__ __forceinline__ float dc1_row_lds(uint8_t* rows, const uint8_t* d0, i
 
 // k_moe_dc1 runs only where expert1_fits holds (top_k <= E1_MAX_K)
 constexpr int E1_MAX_K = 8;
-static_assert((E1_MAX_K + 1) * 64 <= 1024, "dc1 work-group size");
+static_assert((E1_MAX_K + 2) * 64 <= 1024, "dc1 work-group size");
 
 template <int TE, int TS>
-__global__ __launch_bounds__((E1_MAX_K + 1) * 64) void k_moe_dc1(MoeArgs a) {
+__global__ __launch_bounds__((E1_MAX_K + 2) * 64) void k_moe_dc1(MoeArgs a) {
     __shared__ float dn[DC1_ROWS][E1_MAX_K + 1];
+    __shared__ float s_wk[E1_MAX_K + 1];   // routing weights, then the shared-expert gate logit
     __shared__ __attribute__((aligned(16))) uint8_t srows[is_kquant<TS>() ? DC1_ROWS * 2 * 256 : 1];   // F <= 512
     __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
     const int tid = threadIdx.x, j = tid & 15, rr = (tid >> 4) & (DC1_ROWS - 1), p = tid >> 6;
@@ -827,12 +828,19 @@ __global__ __launch_bounds__((E1_MAX_K + 1) * 64) void k_moe_dc1(MoeArgs a) {
     const int NB = a.F / QK, K = a.K;
     const bool act = j < NB && r < a.H;
     const uint8_t* hb = a.hq + (int64_t)p * a.hq_stride + j * Q8_1_BYTES;
-    float v;
+    float v = 0.0f;
     if constexpr (TE == T_IQ3_S || TS == T_IQ3_S) {
         for (int i = tid; i < 512; i += blockDim.x) grid[i] = c_iq3s_grid_moe[i];
         __syncthreads();
     }
-    if (p < K) {
+    if (p == K + a.has_shared) {
+        // the last wave only reads the routing weights and the gate logit
+        // (results of the previous launch) into LDS, so that no pair's
+        // down-row loads queue behind them and the combine finds them there
+        const int lane = tid & 63;
+        if (lane < K) s_wk[lane] = a.wts[lane];
+        else if (lane == K && a.has_shared && a.sh_gate_w) s_wk[K] = a.glogit[0];
+    } else if (p < K) {
         const int e = a.plan[PLAN_UEXP + p];
         v = dc1_row<TE>(a.down + (int64_t)e * a.sd + (int64_t)r * row_bytes(TE, a.F), j, hb, grid, act);
     } else if constexpr (is_kquant<TS>()) {
@@ -841,17 +849,17 @@ __global__ __launch_bounds__((E1_MAX_K + 1) * 64) void k_moe_dc1(MoeArgs a) {
     } else {
         v = dc1_row<TS>(a.sh_down + (int64_t)r * row_bytes(TS, a.F), j, hb, grid, act);
     }
-    if (j == 0) dn[rr][p] = v;
+    if (j == 0 && p < K + a.has_shared) dn[rr][p] = v;
     __syncthreads();
     if (tid < DC1_ROWS) {
         const int rg = tile_i * DC1_ROWS + tid;
         if (rg < a.H) {
             float acc = 0.0f;
-            for (int k = 0; k < K; k++) acc = __builtin_fmaf(a.wts[k], dn[tid][k], acc);
+            for (int k = 0; k < K; k++) acc = __builtin_fmaf(s_wk[k], dn[tid][k], acc);
             float o = acc;
             if (a.has_shared) {
                 const float sh = dn[tid][K];
-                if (a.sh_gate_w) o = __builtin_fmaf(sh, 1.0f / (1.0f + det_exp(-a.glogit[0])), acc);
+                if (a.sh_gate_w) o = __builtin_fmaf(sh, 1.0f / (1.0f + det_exp(-s_wk[K])), acc);
                 else o = sh + acc;
             }
             a.out[rg] = o;
@@ -1331,8 +1339,8 @@ static void launch_layer_nt(const MoeArgs& a, int stage, hipStream_t s) {
             if (stage < 0 || stage == 1)
                 hipLaunchKernelGGL((k_moe_expert1<TE, TS>), dim3(expert_grid(256)), dim3(EX_THREADS), 0, s, a);
             if (stage < 0 || stage == 2)
-                hipLaunchKernelGGL((k_moe_dc1<TE, TS>), dim3(a.H / DC1_ROWS), dim3((a.K + a.has_shared) * 64), 0, s,
-                                   a);
+                hipLaunchKernelGGL((k_moe_dc1<TE, TS>), dim3(a.H / DC1_ROWS), dim3((a.K + a.has_shared + 1) * 64), 0,
+                                   s, a);
             return;
         }
     }

@@ -148,17 +148,26 @@ def emulate(H, F, E, K, te, ts, has_shared, ids, grid=256):
         # Q8_1(h) block w of `pair`: half-wave 0
         o = pair * hq_stride + w * Q8_1
         ck.rng("expert1: hq write", o, o + Q8_1, P * hq_stride)
-    # ---- K3 k_moe_dc1: grid H / 4, (K + has_shared) * 64 threads
+    # ---- K3 k_moe_dc1: grid H / 4, (K + has_shared + 1) * 64 threads (the
+    # last wave loads the routing weights and the gate logit into LDS)
     G3 = H // DC1_ROWS
     assert G3 % 8 == 0
-    nthr = (K + int(has_shared)) * 64
+    npair = K + int(has_shared)
+    nthr = (npair + 1) * 64
+    assert nthr <= 1024
     t3 = np.arange(nthr)
     j, rr, p = t3 & 15, (t3 >> 4) & (DC1_ROWS - 1), t3 >> 6
+    lane = t3 & 63
+    ld = (p == npair) & (lane < K)
+    ck.rng("dc1: wts read", lane[ld] * 4, lane[ld] * 4 + 4, K * 4)
+    ck.rng("dc1: s_wk write", lane[ld] * 4, lane[ld] * 4 + 4, 9 * 4)
+    if has_shared:
+        ck.rng("dc1: s_wk gate logit", np.array([K * 4]), np.array([K * 4 + 4]), 9 * 4)
     for b in range(G3):
         tile_i = (b & 7) * (G3 >> 3) + (b >> 3)
         assert tile_i < G3
         r = tile_i * DC1_ROWS + rr
-        act = (j < NB) & (r < H)
+        act = (j < NB) & (r < H) & (p < npair)
         hb = p * hq_stride + j * Q8_1
         ck.rng("dc1: hq read", hb[act], hb[act] + Q8_1, P * hq_stride)
         rt = act & (p < K)
@@ -168,7 +177,8 @@ def emulate(H, F, E, K, te, ts, has_shared, ids, grid=256):
         sh = act & (p == K)
         off = r[sh] * rbF_s + j[sh] * BYTES[ts]
         ck.rng("dc1: shared down row", off, off + BYTES[ts], shd_sz)
-        ck.rng("dc1: dn LDS", (rr * 9 + p) * 4, (rr * 9 + p) * 4 + 4, DC1_ROWS * 9 * 4)
+        wr = (j == 0) & (p < npair)
+        ck.rng("dc1: dn LDS", (rr[wr] * 9 + p[wr]) * 4, (rr[wr] * 9 + p[wr]) * 4 + 4, DC1_ROWS * 9 * 4)
         ck.rng("dc1: out", (tile_i * DC1_ROWS + np.arange(DC1_ROWS)) * 4,
                (tile_i * DC1_ROWS + np.arange(DC1_ROWS)) * 4 + 4, H * 4)
     return ck.n
