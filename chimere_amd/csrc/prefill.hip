@@ -87,34 +87,44 @@ __global__ __launch_bounds__(256) void k_pf_router(PfArgs a) {
         rows[e] = r < a.E ? a.router + (int64_t)r * a.H : a.sh_gate_w;
     }
     float acc[PF_RT][PF_RE];
-#pragma unroll
-    for (int t = 0; t < PF_RT; t++)
-#pragma unroll
-        for (int e = 0; e < PF_RE; e++) acc[t][e] = 0.0f;
-    // the loads of column step h + 256 are issued before step h's products
+    // the loads of column step h + 256 are issued before step h's products;
+    // the loop runs two column steps per trip on two register sets (no
+    // copies between the sets), and every load is a uniform row base plus a
+    // 32-bit lane offset (no 64-bit address arithmetic per load)
     const float* xr[PF_RT];
 #pragma unroll
     for (int t = 0; t < PF_RT; t++) xr[t] = a.x + (int64_t)min(t0 + t, a.T - 1) * a.H;
-    float rv[PF_RE], xv[PF_RT];
+    auto ld = [](const float* base, int h) {
+        return *(const float*)((const char*)base + (uint32_t)h * 4u);
+    };
+    float r0[PF_RE], x0[PF_RT], r1[PF_RE], x1[PF_RT];
+    auto load = [&](float (&r)[PF_RE], float (&x)[PF_RT], int h) {
 #pragma unroll
-    for (int e = 0; e < PF_RE; e++) rv[e] = rows[e][tid];
+        for (int e = 0; e < PF_RE; e++) r[e] = ld(rows[e], h);
 #pragma unroll
-    for (int t = 0; t < PF_RT; t++) xv[t] = xr[t][tid];
-    for (int h = tid; h < a.H; h += 256) {
-        float rn[PF_RE], xn[PF_RT];
-        const int hn = h + 256 < a.H ? h + 256 : h;
-#pragma unroll
-        for (int e = 0; e < PF_RE; e++) rn[e] = rows[e][hn];
-#pragma unroll
-        for (int t = 0; t < PF_RT; t++) xn[t] = xr[t][hn];
+        for (int t = 0; t < PF_RT; t++) x[t] = ld(xr[t], h);
+    };
+    auto step = [&](const float (&r)[PF_RE], const float (&x)[PF_RT]) {
 #pragma unroll
         for (int t = 0; t < PF_RT; t++)
 #pragma unroll
-            for (int e = 0; e < PF_RE; e++) acc[t][e] = __builtin_fmaf(rv[e], xv[t], acc[t][e]);
+            for (int e = 0; e < PF_RE; e++) acc[t][e] = __builtin_fmaf(r[e], x[t], acc[t][e]);
+    };
+    // column step tid (acc = fmaf(r, x, 0), the first fma of the chain)
+    load(r0, x0, tid);
+    load(r1, x1, tid + 256 < a.H ? tid + 256 : tid);
 #pragma unroll
-        for (int e = 0; e < PF_RE; e++) rv[e] = rn[e];
+    for (int t = 0; t < PF_RT; t++)
 #pragma unroll
-        for (int t = 0; t < PF_RT; t++) xv[t] = xn[t];
+        for (int e = 0; e < PF_RE; e++) acc[t][e] = __builtin_fmaf(r0[e], x0[t], 0.0f);
+    // h: the step whose operands are in set 1 (H is a multiple of 256, so
+    // every bound below is uniform)
+    for (int h = tid + 256; h < a.H; h += 512) {
+        load(r0, x0, h + 256 < a.H ? h + 256 : h);
+        step(r1, x1);
+        if (h + 256 >= a.H) break;
+        load(r1, x1, h + 512 < a.H ? h + 512 : h);
+        step(r0, x0);
     }
     const int o = tid >> 3, q = tid & 7;
 #pragma unroll
