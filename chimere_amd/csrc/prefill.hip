@@ -203,15 +203,27 @@ __global__ __launch_bounds__(1024) void k_pf_plan(PfArgs a) {
     for (int e = tid; e < 2 * 1024; e += 1024) cnt[e] = 0;
     for (int e = tid; e < NE; e += 1024) fill[e] = 0;
     __syncthreads();
-    // pairs in batches of 4 per thread: the 4 id loads are issued together
-    // (one memory round trip per batch, not per pair)
+    // pairs in batches of 4 per thread: the 4 id loads (and weight loads)
+    // are issued together (one memory round trip per batch, not per pair);
+    // the first batch's ids and weights stay in registers for the scatter
+    int k4[4];
+    float kw[4];
     for (int p0 = tid; p0 < TK; p0 += 4 * 1024) {
         int e4[4];
+        float w4[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) e4[i] = p0 + i * 1024 < TK ? a.ids[p0 + i * 1024] : -1;
+        for (int i = 0; i < 4; i++) {
+            const bool in = p0 + i * 1024 < TK;
+            e4[i] = in ? a.ids[p0 + i * 1024] : -1;
+            w4[i] = in && a.ids_out ? a.wts[p0 + i * 1024] : 0.0f;
+        }
 #pragma unroll
         for (int i = 0; i < 4; i++)
             if (e4[i] >= 0) atomicAdd(&cnt[e4[i]], 1);
+        if (p0 == tid) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) { k4[i] = e4[i]; kw[i] = w4[i]; }
+        }
     }
     if (tid == 0) cnt[a.E] = a.has_shared ? a.T : 0;
     __syncthreads();
@@ -236,11 +248,16 @@ __global__ __launch_bounds__(1024) void k_pf_plan(PfArgs a) {
     for (int p0 = tid; p0 < TK; p0 += 4 * 1024) {
         int e4[4];
         float w4[4];
+        if (p0 == tid) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const bool in = p0 + i * 1024 < TK;
-            e4[i] = in ? a.ids[p0 + i * 1024] : -1;
-            w4[i] = in && a.ids_out ? a.wts[p0 + i * 1024] : 0.0f;
+            for (int i = 0; i < 4; i++) { e4[i] = k4[i]; w4[i] = kw[i]; }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const bool in = p0 + i * 1024 < TK;
+                e4[i] = in ? a.ids[p0 + i * 1024] : -1;
+                w4[i] = in && a.ids_out ? a.wts[p0 + i * 1024] : 0.0f;
+            }
         }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
