@@ -90,20 +90,17 @@ __device__ __forceinline__ void f32_row_dot(const float* __restrict__ a, const f
 // wave's LDS accesses complete in issue order, so no barrier is needed).
 // Composite c = key << 32 | ~index orders entries as the k rounds of arg-max
 // do (larger p first, lower index on equal p); all composites differ.
-//  1. candidates: the entries with key >= a threshold, the largest of four
+//  1. candidates: the entries with key >= a threshold, the largest of eight
 //     fractions of the top probability for which at least K entries pass
-//     (the four counts are kept in two packed lane values and summed over
-//     the wave by butterflies); every entry above a candidate is a candidate,
-//     so a candidate's round is the number of candidates above it;
-//  2. the n candidates (K <= n <= 64) are compacted into sc[64..64+n) at
-//     offsets from a prefix sum of the lanes' candidate counts (the rest of
-//     sc[64..128) is zero, below every composite), and lane l < n counts the
+//     (each count is four ballots and their population counts, scalar work
+//     with no cross-lane chain); every entry above a candidate is a
+//     candidate, so a candidate's round is the number of candidates above it;
+//  2. the n candidates (K <= n <= 64) are compacted into sc[64..64+n) in
+//     index order (slot-major offsets from the ballots' population counts
+//     and each lane's count of set bits below it), and lane l < n counts the
 //     candidates above candidate l;
 //  3. the candidate of round r is written to sc[r]; lane k < K takes round
 //     k and every lane sums rounds 0..K-1 in order (the renormalisation sum).
-// The single-lane steps of the k rounds of arg-max (maximum, ballot, scalar
-// round trips) are what make those slow on one wave; this path has none in
-// its chain except the three butterfly / scan reductions.
 // Returns false (nothing written) when no threshold leaves between K and 64
 // candidates (e.g. many exactly equal probabilities): the caller then runs
 // the k rounds of arg-max.  Otherwise lane k < K gets round k's index and
@@ -112,40 +109,30 @@ __device__ __forceinline__ bool topk4_select(const uint32_t (&key)[4], uint32_t 
                                              int& my_idx, float& my_w) {
     const int lane = threadIdx.x & 63;
     const float pmax = __builtin_bit_cast(float, kmax - 1u);
-    uint32_t kt[4];
-    kt[0] = __builtin_bit_cast(uint32_t, pmax * 0.6f) + 1u;
-    kt[1] = __builtin_bit_cast(uint32_t, pmax * 0.4f) + 1u;
-    kt[2] = __builtin_bit_cast(uint32_t, pmax * 0.25f) + 1u;
-    kt[3] = __builtin_bit_cast(uint32_t, pmax * 0.1f) + 1u;
-    // per-lane counts of the four thresholds, two 16-bit fields per int
-    int pa = 0, pb = 0;
+    constexpr float FR[8] = {0.7f, 0.5f, 0.35f, 0.25f, 0.17f, 0.12f, 0.08f, 0.05f};
+    uint32_t thr = 0;
+    int n = 0;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        pa += (key[i] >= kt[0] ? 1 : 0) + (key[i] >= kt[1] ? 1 << 16 : 0);
-        pb += (key[i] >= kt[2] ? 1 : 0) + (key[i] >= kt[3] ? 1 << 16 : 0);
+    for (int t = 0; t < 8; t++) {
+        const uint32_t kt = __builtin_bit_cast(uint32_t, pmax * FR[t]) + 1u;
+        int c = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) c += __builtin_popcountll(__ballot(key[i] >= kt));
+        if (c >= K) { thr = kt; n = c; break; }
     }
-    int ta = pa, tb = pb;
-    ta += xlane<1>(ta); tb += xlane<1>(tb);
-    ta += xlane<2>(ta); tb += xlane<2>(tb);
-    ta += xlane<4>(ta); tb += xlane<4>(tb);
-    ta += xlane<8>(ta); tb += xlane<8>(tb);
-    ta += xlane<16>(ta); tb += xlane<16>(tb);
-    ta += xlane<32>(ta); tb += xlane<32>(tb);
-    const int c0 = ta & 0xFFFF, c1 = ta >> 16, c2 = tb & 0xFFFF, c3 = tb >> 16;
-    const int t = c0 >= K ? 0 : (c1 >= K ? 1 : (c2 >= K ? 2 : 3));
-    const int n = t == 0 ? c0 : (t == 1 ? c1 : (t == 2 ? c2 : c3));
     if (n < K || n > 64) return false;
-    const uint32_t thr = kt[t];
-    const int mine_n = ((t < 2 ? pa : pb) >> (t & 1 ? 16 : 0)) & 0xFFFF;
-    int off = wave_incl_scan(mine_n) - mine_n;
-    sc[64 + lane] = 0;
+    int base = 0;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
+        const uint64_t m = __ballot(key[i] >= thr);
         if (key[i] >= thr) {
-            sc[64 + off] = ((uint64_t)key[i] << 32) | (uint32_t)~(uint32_t)(lane + 64 * i);
-            off++;
+            const int pos = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+            sc[64 + pos] = ((uint64_t)key[i] << 32) | (uint32_t)~(uint32_t)(lane + 64 * i);
         }
+        base += __builtin_popcountll(m);
     }
+    if (lane >= n) sc[64 + lane] = 0;   // below every composite
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
