@@ -3,6 +3,8 @@
 // layer sequences of chimere-server/src/qwen35_model/moe_ffn.rs).
 #include "ggml_gpu.hpp"
 
+#include <new>
+
 #include "chimere_cpu.h"
 
 namespace chimere {
@@ -278,6 +280,7 @@ void MoeLayer::forward_ncmoe(const float* x, float* out, int* ids, float* w, int
     const int rc = chimere_ncmoe_experts(cg_, cu_, cd_, (size_t)c_.gate_stride, (size_t)c_.up_stride,
                                          (size_t)c_.down_stride, h_ids_.data(), h_w_.data(), K, h_x_.data(),
                                          h_acc_.data(), H, F, c_.n_experts, nthreads);
+    if (rc == CHIMERE_CPU_ENOMEM) throw std::bad_alloc();   // a host allocation failed, not a bad argument
     if (rc != CHIMERE_CPU_OK) throw Error(CHIMERE_ERR_ARG, "chimere_ncmoe_experts rejected its arguments");
     hip_check(hipMemcpyAsync(accum_.get(), h_acc_.data(), sizeof(float) * H, hipMemcpyHostToDevice, s),
               "hipMemcpyAsync");

@@ -166,6 +166,8 @@ public:
     // One token with the routed experts on the host (IQ3_S experts): host
     // copies [E * expert_bytes] of gate / up / down, nthreads host threads.
     void attach_cpu_experts(const uint8_t* gate, const uint8_t* up, const uint8_t* down);
+    // Throws Error(CHIMERE_ERR_ARG) for rejected arguments, std::bad_alloc
+    // when the host expert loop cannot allocate.
     void forward_ncmoe(const float* x, float* out, int* ids, float* w, int nthreads, hipStream_t s);
 
 private:

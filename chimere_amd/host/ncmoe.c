@@ -115,7 +115,9 @@ static int32_t sb_isum_scalar(const uint8_t *w, const int8_t *q) {
             for (int j = 0; j < 4; j++) {
                 const int lv = (int)((gv >> (8 * j)) & 0xFFu);
                 const int v = q[32 * ib + 4 * p + j];
-                s += (sb >> j) & 1 ? -lv * v : lv * v;
+                /* the sign flips the int8 activation, wrapping as the SIMD
+                 * paths' byte negation does (-(-128) stays -128) */
+                s += lv * ((sb >> j) & 1 ? (int)(int8_t)(uint8_t)(-v) : v);
             }
         }
         tot += s * (1 + 2 * ((w[106 + ib / 2] >> (4 * (ib & 1))) & 0xF));

@@ -34,6 +34,10 @@ extern "C" {
 void ggml_ffi_quantize_q8_K(const float* x, void* y, int64_t k);
 
 /* *s = IQ3_S row (n weights) . Q8_K vector (n values)  (ggml_iq3s_gemv.h:30) */
+/* The Q8_K quants are expected in [-127, 127] (the library's quantizer
+ * never emits -128).  A caller-supplied -128 under a negative IQ3_S sign is
+ * negated by byte wrap-around (it stays -128) on every instruction-set path,
+ * as ggml's AVX2 sign instruction does. */
 void ggml_ffi_vec_dot_iq3s_q8K(int n, float* s, const void* vx, const void* vy);
 
 /* y[nrows] = W[nrows, ncols] (IQ3_S) x[ncols] (f32, quantized to Q8_K

@@ -206,9 +206,10 @@ typedef struct chimere_moe_layer {
 
 /* Workspace bytes for chimere_moe_ffn_decode at up to max_ntok tokens. */
 size_t chimere_moe_workspace_size(const chimere_moe_layer *layer, int max_ntok);
-/* Clears a workspace once after allocation (a fill kernel, graph-safe).  The
- * MoE kernels leave their counters at zero on exit, so a workspace is reused
- * across calls without clearing; calls sharing one workspace must not overlap. */
+/* Clears a workspace (a fill kernel, graph-safe).  Optional: the decode
+ * kernels keep no counters or flags in the workspace, and every field a call
+ * reads was written earlier in the same call, so a workspace is reused across
+ * calls without clearing.  Calls sharing one workspace must not overlap. */
 void chimere_moe_workspace_init(void *workspace, size_t bytes, hipStream_t stream);
 /* x [ntok, H] f32 -> out [ntok, H] f32.  ids_out [ntok, K] / w_out [ntok, K]
  * receive the routing when non-NULL. */

@@ -281,3 +281,23 @@ def test_isa_in_use():
     flags = open("/proc/cpuinfo").read()
     want = 2 if (" avx512f" in flags and " avx512bw" in flags) else 1 if " avx2" in flags else 0
     assert cpu.lib().chimere_cpu_isa() == want
+
+
+def test_q8k_minus_128_same_on_every_isa():
+    """A caller-supplied Q8_K block holding -128 (which the library's
+    quantizer never emits): the portable, AVX2 and AVX-512 integer loops give
+    the same bits (negation under a sign bit wraps in every one of them)."""
+    code = ("import sys, numpy as np; sys.path[:0] = [%r]; from chimere_amd import cpu;"
+            "rng = np.random.default_rng(11); w = rng.integers(0, 256, 2 * 110, dtype=np.uint8);"
+            "w[0:2] = np.frombuffer(np.float16(0.01).tobytes(), np.uint8); w[110:112] = w[0:2];"
+            "y = np.zeros(2 * 296, np.uint8); q = rng.integers(-128, 128, 512).astype(np.int8);"
+            "q[::7] = -128; y[8:264] = q[:256].view(np.uint8); y[296 + 8:296 + 264] = q[256:].view(np.uint8);"
+            "y[0:4] = np.frombuffer(np.float32(0.02).tobytes(), np.uint8); y[296:300] = y[0:4];"
+            "print(repr(np.float32(cpu.vec_dot_iq3s_q8K(512, w, y)).view(np.uint32)))") % ROOT
+    out = set()
+    for env in ({"CHIMERE_CPU_PORTABLE": "1"}, {"CHIMERE_CPU_NO_AVX512": "1"}, {}):
+        r = subprocess.run([sys.executable, "-c", code], env=dict(os.environ, **env), capture_output=True, text=True,
+                           timeout=120)
+        assert r.returncode == 0, r.stderr
+        out.add(r.stdout.strip())
+    assert len(out) == 1, out
