@@ -796,17 +796,21 @@ template <int T>
 __device__ __forceinline__ float dc1_row_lds(uint8_t* rows, const uint8_t* d0, int64_t rbF, int rr, int j,
                                              const uint8_t* hblk, bool act) {
     const int lane = threadIdx.x & 63;
-    const int n16 = (int)(DC1_ROWS * rbF / 2);
-    for (int i = lane; i < n16; i += 64) {
-        const int r = i / (int)(rbF / 2), c = i - r * (int)(rbF / 2);
-        ((uint16_t*)rows)[i] = *(const uint16_t*)(d0 + r * rbF + 2 * c);
+    XBlk xb;
+    if (act) load_xblk(hblk, xb);
+    // the DC1_ROWS rows are contiguous: 16-byte pieces where the weights are
+    // 16-byte aligned (Q4_K / Q5_K rows at F = 512: 288 / 352 bytes), else
+    // 2-byte pieces (the boundary only promises 2-byte aligned weights)
+    const int nb = (int)(DC1_ROWS * rbF);
+    if ((((uintptr_t)d0 | (uintptr_t)nb) & 15) == 0) {
+        for (int i = lane; i < nb / 16; i += 64) ((uint4*)rows)[i] = ((const uint4*)d0)[i];
+    } else {
+        for (int i = lane; i < nb / 2; i += 64) ((uint16_t*)rows)[i] = ((const uint16_t*)d0)[i];
     }
     float v = 0.0f;
     if (act) {
         WBlk w;
         block_decode<T>(rows + rr * rbF, j, nullptr, w);
-        XBlk xb;
-        load_xblk(hblk, xb);
         v = wacc<T>(w, xb, 0.0f);
     }
     return slot_reduce16(v);
