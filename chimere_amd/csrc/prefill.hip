@@ -23,7 +23,9 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr int PF_CHUNK = 8;      // 32-element blocks per K chunk staged in LDS
 constexpr int PF_TILE = 16;      // (token, k) pairs per tile: the M dimension of v_mfma_i32_16x16x32_i8
 constexpr int PF_THREADS = 256;  // 4 waves
-constexpr int PF_RT = 16, PF_RE = 8;   // router tile: tokens x rows per work-group
+// router tile: tokens x rows per work-group (8 x 8: 100 VGPRs, four
+// work-groups per CU; 16 x 8 at 170 VGPRs ran the 512-token chunk ~5 us slower)
+constexpr int PF_RT = 8, PF_RE = 8;
 
 struct PfArgs {
     int H, F, E, K, T, has_shared;
@@ -52,12 +54,12 @@ struct PfArgs {
     int max_tiles;
 };
 
-// P1: grid (ceil((E + has_gate) / 8), ceil(T / 16)), 256 threads: logits of 16
-// tokens x 8 router rows.  Every output keeps the reference's order
+// P1: grid (ceil((E + has_gate) / PF_RE), ceil(T / PF_RT)), 256 threads: logits
+// of PF_RT tokens x PF_RE router rows.  Every output keeps the reference's order
 // (elementwise.rs:186-221 launched with 256 threads): thread j accumulates
 // columns j, j+256, ... with fma, then the 256 partials are summed by the
 // halving tree (pairs j, j+m for m = 128, ..., 1).  Thread j owns partial j
-// of all 128 outputs of the tile; the tree runs in LDS for 32 outputs at a
+// of all PF_RT * PF_RE outputs of the tile; the tree runs in LDS for 32 outputs at a
 // time: 8 threads per output, thread q first reduces the 32 partials
 // j = q (mod 8) (tree levels m = 128 .. 8), then levels 4, 2, 1 run across
 // the 8 lanes.
