@@ -289,10 +289,11 @@ constexpr int pf_row_chunk_bytes() {
 }
 
 // LDS row stride of a staged chunk on the two-stage path: the chunk bytes,
-// or for IQ3_S the 16-byte aligned span that holds the superblock (it starts
-// at (110 c) % 16 inside the span: at most 14 + 110 bytes)
+// or for IQ3_S / Q6_K the 16-byte aligned span that holds the superblock (it
+// starts at (110 c) % 16 / (210 c) % 16 inside the span: at most 14 + 110 /
+// 14 + 210 bytes)
 template <int T>
-constexpr int pf_lds_row() { return T == T_IQ3_S ? 128 : pf_row_chunk_bytes<T>(); }
+constexpr int pf_lds_row() { return T == T_IQ3_S ? 128 : T == T_Q6_K ? 224 : pf_row_chunk_bytes<T>(); }
 
 // LDS row strides of the two-stage path, padded so that the 16 rows a wave
 // reads at one block offset spread over the banks: a stride that is a
@@ -360,6 +361,28 @@ __device__ __forceinline__ long pf_b_frag(const uint8_t* row, int b, int q, uint
             lo |= ((qh[0] >> b) & 0x01010101u) << 4;
             hi |= ((qh[1] >> b) & 0x01010101u) << 4;
         }
+    } else if constexpr (T == T_Q6_K) {
+        // block b = 4 gi + jj of the superblock [ql 128][qh 64][scales 16 x i8][f16 d]
+        // (gguf_loader.rs:839-917): element l of the block is nibble jj / 2 of
+        // ql[64 gi + 32 (jj & 1) + l] with bits 2 jj, 2 jj + 1 of qh[32 gi + l]
+        // as bits 4, 5, minus 32; lane group q holds elements 8q .. 8q+7.  The
+        // block's two 16-element halves have their own int8 scales: *mult holds
+        // both (low byte: elements 0..15, high byte: 16..31)
+        const int gi = b >> 2, jj = b & 3;
+        const int lo_off = 64 * gi + 32 * (jj & 1) + 8 * q, hi_off = 128 + 32 * gi + 8 * q;
+        const int nsh = 4 * (jj >> 1), hsh = 2 * jj;
+        uint32_t v[2];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint32_t u = ((lds_u32(row, lo_off + 4 * i) >> nsh) & 0x0F0F0F0Fu) |
+                               (((lds_u32(row, hi_off + 4 * i) >> hsh) & 0x03030303u) << 4);
+            const uint32_t t = u ^ 0x20202020u, sgn = t & 0x20202020u;   // u - 32 per byte, 6-bit
+            v[i] = t | (sgn << 1) | (sgn << 2);                             // sign-extended
+        }
+        lo = v[0];
+        hi = v[1];
+        *dw = lds_u16(row, 208);
+        *mult = (int)lds_u16(row, 192 + 8 * gi + 2 * jj);
     } else if constexpr (T == T_IQ3_S) {
         // sub-block b of the superblock [f16 d][qs 64][qh 8][signs 32][scales 4];
         // lane group q holds elements 8q .. 8q+7: grid entries qs[8b+2q] and
@@ -448,6 +471,7 @@ __device__ __forceinline__ void pf_mma_chunk(const uint8_t* xl, int xr, const fl
     // two blocks in flight: block b's matrix products are issued before block
     // b-1's results are rescaled, so the MFMA latency overlaps VALU work
     v4i r[NTN], rp[NTN];
+    v4i r2[NTN], rp2[NTN];     // Q6_K: the products of the block's second 16-element half
     float dw[NTN], dwp[NTN];
     int mu[NTN], mup[NTN];   // IQ3_S / K-quant sub-block factors
     PfMin mn[NTN], mnp[NTN];   // K-quant min terms
@@ -471,7 +495,14 @@ __device__ __forceinline__ void pf_mma_chunk(const uint8_t* xl, int xr, const fl
                 const long bf =
                     pf_b_frag<T, PRE>(wrows + (16 * n + c) * cbytes, b, q, &dwb, &mu[n], grid, sb[n], &mn[n]);
                 dw[n] = h2f(dwb);
-                r[n] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bf, c0, 0, 0, 0);
+                if constexpr (T == T_Q6_K) {
+                    // the two halves (lane groups 0, 1 and 2, 3) in separate
+                    // products, each scaled by its own factor below
+                    r[n] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, q < 2 ? bf : 0l, c0, 0, 0, 0);
+                    r2[n] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, q < 2 ? 0l : bf, c0, 0, 0, 0);
+                } else {
+                    r[n] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bf, c0, 0, 0, 0);
+                }
             }
         }
         if (b > 0) {
@@ -480,6 +511,15 @@ __device__ __forceinline__ void pf_mma_chunk(const uint8_t* xl, int xr, const fl
                 for (int n = 0; n < NTN; n++)
 #pragma unroll
                     for (int i = 0; i < 4; i++) rp[n][i] = __mul24(rp[n][i], mup[n]);   // |.| < 2^21
+            }
+            if constexpr (T == T_Q6_K) {
+                // the exact block dot lo * sc0 + hi * sc1 (|.| <= 2 * 16*32*127*128 < 2^24)
+#pragma unroll
+                for (int n = 0; n < NTN; n++) {
+                    const int s0 = (int)(int8_t)(mup[n] & 0xFF), s1 = (int)(int8_t)((mup[n] >> 8) & 0xFF);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) rp[n][i] = __mul24(rp[n][i], s0) + __mul24(rp2[n][i], s1);
+                }
             }
 #pragma unroll
             for (int n = 0; n < NTN; n++) {
@@ -497,7 +537,7 @@ __device__ __forceinline__ void pf_mma_chunk(const uint8_t* xl, int xr, const fl
             }
         }
 #pragma unroll
-        for (int n = 0; n < NTN; n++) { rp[n] = r[n]; dwp[n] = dw[n]; mup[n] = mu[n]; mnp[n] = mn[n]; }
+        for (int n = 0; n < NTN; n++) { rp[n] = r[n]; rp2[n] = r2[n]; dwp[n] = dw[n]; mup[n] = mu[n]; mnp[n] = mn[n]; }
         dxp = dx;
         if constexpr (pf_kq<T>()) {
             // sum q_x = -(xs8 / 8) of the block just issued (xs8 = -8 * sum q_x)
@@ -664,7 +704,7 @@ constexpr int PF_XST = PF_TILE * PF_XROW_AL;
 // experts' chunk rows (two stages of 128 Q8_0 chunk rows leave one work-group
 // per CU)
 template <int TE, int TS>
-constexpr bool pf_sh_one() { return (TS == T_Q8_0 || pf_kq<TS>()) && TE != TS; }
+constexpr bool pf_sh_one() { return (TS == T_Q8_0 || pf_kq<TS>() || TS == T_Q6_K) && TE != TS; }
 template <int TE, int TS>
 constexpr int pf_ws0(int nrows) { return pf_wst<TE>(nrows) > pf_wst<TS>(nrows) ? pf_wst<TE>(nrows) : pf_wst<TS>(nrows); }
 template <int TE, int TS>
@@ -761,9 +801,9 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_down(PfArgs a) {
         constexpr int T = decltype(tag)::value;
         const int64_t rb = row_bytes(T, a.F);
         const uint8_t* d = sh ? a.sh_down : a.down + (int64_t)e * a.sd;
-        // IQ3_S down rows (F / 256 superblocks of 110 bytes) are 16-byte aligned
-        // only when F is a multiple of 2048: one stage
-        constexpr bool two = T != T_IQ3_S && !(T == TS && pf_sh_one<TE, TS>());
+        // IQ3_S / Q6_K down rows (F / 256 superblocks of 110 / 210 bytes) are
+        // 16-byte aligned only when F is a multiple of 2048: one stage
+        constexpr bool two = T != T_IQ3_S && T != T_Q6_K && !(T == TS && pf_sh_one<TE, TS>());
         pf_gemm<T, 2, 128, two>(s0, s1, d + r0 * rb, 128, d, rb, a.F / QK, a.hq, prs, a.hq_stride, wave * 32, grid,
                                 acc);
     };
@@ -890,9 +930,10 @@ void chimere_moe_prefill(const chimere_moe_layer* L, const float* x, float* out,
     const bool has_sh = L->shared_type >= 0;
     auto pf_type = [](int t) { return t == T_Q4_0 || t == T_Q8_0 || t == T_IQ3_S; };
     CHIMERE_REQUIRE(pf_type(L->expert_type) &&
-                        (!has_sh || pf_type(L->shared_type) || L->shared_type == T_Q4_K || L->shared_type == T_Q5_K),
+                        (!has_sh || pf_type(L->shared_type) || L->shared_type == T_Q4_K || L->shared_type == T_Q5_K ||
+                         L->shared_type == T_Q6_K),
                     CHIMERE_ERR_ARG,
-                    "moe_prefill: Q4_0 / Q8_0 / IQ3_S experts, shared expert also Q4_K / Q5_K (expert %d, shared %d)",
+                    "moe_prefill: Q4_0 / Q8_0 / IQ3_S experts, shared expert also Q4_K / Q5_K / Q6_K (expert %d, shared %d)",
                     L->expert_type, L->shared_type);
     CHIMERE_REQUIRE(!has_sh || (L->sh_gate && L->sh_up && L->sh_down), CHIMERE_ERR_ARG,
                     "moe_prefill: shared expert incomplete");
@@ -930,6 +971,7 @@ void chimere_moe_prefill(const chimere_moe_layer* L, const float* x, float* out,
         else if (ts == T_Q8_0) launch_pf<TE, T_Q8_0>(a, p, stream);
         else if (ts == T_Q4_K) launch_pf<TE, T_Q4_K>(a, p, stream);
         else if (ts == T_Q5_K) launch_pf<TE, T_Q5_K>(a, p, stream);
+        else if (ts == T_Q6_K) launch_pf<TE, T_Q6_K>(a, p, stream);
         else launch_pf<TE, T_IQ3_S>(a, p, stream);
     };
     if (te == T_Q4_0) with_ts(std::integral_constant<int, T_Q4_0>{});

@@ -93,7 +93,8 @@ class MoeLayer:
 
     def prefill(self, x, out=None, ids=None, wts=None):
         """x [T, H] f32, any T >= 1 -> out [T, H] through chimere_moe_prefill
-        (int8 matrix-core grouped GEMMs; Q4_0 / Q8_0 / IQ3_S weights).  The prefill
+        (int8 matrix-core grouped GEMMs; Q4_0 / Q8_0 / IQ3_S experts, the shared expert
+        also Q4_K / Q5_K / Q6_K).  The prefill
         workspace is allocated on first use and grown when T exceeds it."""
         T = x.shape[0]
         if out is None:

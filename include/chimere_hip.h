@@ -244,7 +244,7 @@ void chimere_moe_ffn_decode_stage(const chimere_moe_layer *layer, const float *x
  * matrix-core GEMMs.  Same routing and arithmetic per token as
  * chimere_moe_ffn_decode except the fp32 accumulation order of the quantized
  * projections, which is ascending block order (one accumulator per row).
- * Q4_0 / Q8_0 / IQ3_S experts; the shared expert also Q4_K / Q5_K (the
+ * Q4_0 / Q8_0 / IQ3_S experts; the shared expert also Q4_K / Q5_K / Q6_K (the
  * reference model's Q5_K, compute_graph.rs:997-999).  ids_out / w_out (both or
  * neither) receive [ntok][top_k].  No allocation; workspace from
  * chimere_moe_prefill_workspace_size(layer, >= ntok), 256-byte aligned, needs

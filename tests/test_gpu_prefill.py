@@ -173,6 +173,9 @@ def kq_layer(dev, seed, et, st, H, F, E, K, gate_vec=True):
     (O.Q4_0, O.Q5_K, 1024, 256, 32, 4, 37),
     (O.Q8_0, O.Q4_K, 1024, 256, 16, 8, 20),
     (O.IQ3_S, O.Q5_K, 1024, 256, 64, 8, 9),
+    (O.Q4_0, O.Q6_K, 1024, 256, 32, 4, 37),
+    (O.Q8_0, O.Q6_K, 1024, 512, 16, 8, 20),
+    (O.IQ3_S, O.Q6_K, 2048, 256, 64, 8, 9),
 ])
 def test_prefill_kquant_shared_small(dev, et, st, H, F, E, K, T):
     """K-quant shared expert on the MFMA path (scale on the int32 result, the
@@ -181,6 +184,18 @@ def test_prefill_kquant_shared_small(dev, et, st, H, F, E, K, T):
     layer = kq_layer(dev, 800 + et + st + T, et, st, H, F, E, K)
     g = torch.Generator(device=dev).manual_seed(T)
     prefill_check(layer, torch.randn(T, H, generator=g, device=dev))
+
+
+def test_prefill_q6k_shared_full_shape(dev):
+    """A Q6_K shared expert (two int8 scales per 32-element block: the two
+    16-element halves in separate products, combined exactly before the
+    block's one rescale) at the model shape: 1680-byte gate/up rows on the
+    two-stage path, 420-byte down rows on the one-stage path, every token
+    bit-exact against the oracle's L=1 order."""
+    print("prefill IQ3_S + Q6_K shared, full shape, 40 tokens", flush=True)
+    layer = kq_layer(dev, 890, O.IQ3_S, O.Q6_K, 2048, 512, 256, 8)
+    g = torch.Generator(device=dev).manual_seed(89)
+    prefill_check(layer, torch.randn(40, 2048, generator=g, device=dev))
 
 
 def test_prefill_model_layer_types_full_shape(dev):
