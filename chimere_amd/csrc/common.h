@@ -28,6 +28,34 @@ constexpr int TILE_ROWS = 16;      // rows per GEMV work-group tile (one per 16-
 constexpr int GEMV_THREADS = TILE_ROWS * SLOTS;   // 256 = 4 waves of 64
 constexpr int CHUNK_BLOCKS = 64;   // 32-element blocks of one row held in LDS at a time
 
+// IQ3_S codebook with the block's sign bits folded in: entry 16 * i + n is
+// codebook entry i with byte k negated where bit k of the 4-bit nibble n is
+// set, so one lookup gives four signed int8 levels (8192 words, 32 KiB of
+// LDS, against 512 words and per-word sign masks).  Generated at compile
+// time from the codebook.
+struct Iq3sSignedGrid {
+    uint32_t w[8192];
+    constexpr Iq3sSignedGrid() : w() {
+        constexpr uint32_t base[512] = CHIMERE_IQ3S_GRID_INIT;
+        for (int i = 0; i < 512; i++)
+            for (int n = 0; n < 16; n++) {
+                uint32_t v = 0;
+                for (int k = 0; k < 4; k++) {
+                    const uint32_t b = (base[i] >> (8 * k)) & 0xFFu;
+                    v |= (((n >> k) & 1) ? ((0x100u - b) & 0xFFu) : b) << (8 * k);
+                }
+                w[16 * i + n] = v;
+            }
+    }
+};
+static __device__ const Iq3sSignedGrid c_iq3s_sgrid{};
+// Fills a work-group's LDS copy of the sign-folded codebook (8192 words, 16-byte
+// aligned); the caller synchronises before use.
+__device__ __forceinline__ void iq3s_sgrid_fill(uint32_t* lds, int tid, int nth) {
+    const uint4* src = (const uint4*)c_iq3s_sgrid.w;
+    for (int i = tid; i < 2048; i += nth) ((uint4*)lds)[i] = src[i];
+}
+
 __host__ __device__ inline int64_t pad_to(int64_t n, int64_t a) { return (n + a - 1) / a * a; }
 
 template <int T> struct QTraits;
@@ -183,9 +211,25 @@ __device__ __forceinline__ int dot_q4_0_core(uint32_t dbits, const uint32_t (&qs
 // 16-bit indices, and one shift turns both into byte offsets of the table.
 // Negation per byte: (g ^ m) + (m & 1) with m = 0xFF bytes, no carry across
 // bytes since every level is >= 1.
+// SG: grid is the sign-folded codebook (Iq3sSignedGrid in LDS)
+template <bool SG = false>
 __device__ __forceinline__ void iq3s_levels(uint32_t qs0, uint32_t qs1, uint32_t qh, uint32_t sg,
                                             const uint32_t* grid, uint32_t (&v)[8]) {
     const uint32_t h0 = nib_bits(qh & 0xFu), h1 = nib_bits((qh >> 4) & 0xFu);
+    if constexpr (SG) {
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const uint32_t pr = __builtin_amdgcn_perm(p < 2 ? h0 : h1, p < 2 ? qs0 : qs1,
+                                                      (p & 1) ? 0x07030602u : 0x05010400u);
+            // sign byte p: low nibble for word 2p, high nibble for word 2p+1,
+            // placed as 4 * nibble in each 16-bit half beside 64 * index
+            const uint32_t t = __mul24((sg >> (8 * p)) & 0xFFu, 0x4004u) & 0x003C003Cu;
+            const uint32_t ab = (pr << 6) | t;
+            v[2 * p] = *(const uint32_t*)((const uint8_t*)grid + (ab & 0xFFFFu));
+            v[2 * p + 1] = *(const uint32_t*)((const uint8_t*)grid + (ab >> 16));
+        }
+        return;
+    }
     uint32_t g[8];
 #pragma unroll
     for (int p = 0; p < 4; p++) {
@@ -314,12 +358,13 @@ __device__ __forceinline__ void wdec_q4_0_core(uint32_t dbits, const uint32_t (&
     }
 }
 
+template <bool SG = false>
 __device__ __forceinline__ void wdec_iq3_s_core(uint32_t dbits, uint32_t qs0, uint32_t qs1, uint32_t qh, uint32_t sg,
                                                 uint32_t nib, const uint32_t* grid, WBlk& w) {
     w.dw = h2f(dbits);
     w.mult = 1 + 2 * (int)nib;
     uint32_t v[8];
-    iq3s_levels(qs0, qs1, qh, sg, grid, v);
+    iq3s_levels<SG>(qs0, qs1, qh, sg, grid, v);
 #pragma unroll
     for (int k = 0; k < 8; k++) w.v[k] = (int)v[k];
 }
@@ -428,8 +473,10 @@ __device__ __forceinline__ void wdec_mxfp4(const uint8_t* row, int off, WBlk& w)
     w.mmin = 0;
 }
 
-// Block b of a row chunk in LDS (layout as block_dot below), decoded.
-template <int T>
+// Block b of a row chunk in LDS (layout as block_dot below), decoded.  SG:
+// IQ3_S lookups in the sign-folded codebook (Iq3sSignedGrid) instead of the
+// 512-word one.
+template <int T, bool SG = false>
 __device__ __forceinline__ void block_decode(const uint8_t* row, int b, const uint32_t* grid, WBlk& w) {
     if constexpr (T == T_Q8_0) {
         const int off = b * 34;
@@ -454,7 +501,7 @@ __device__ __forceinline__ void block_decode(const uint8_t* row, int b, const ui
     } else {
         const int off = (b >> 3) * 110, ib = b & 7;
         const uint32_t sc = row[off + 106 + (ib >> 1)];
-        wdec_iq3_s_core(lds_u16(row, off), lds_u32(row, off + 2 + 8 * ib), lds_u32(row, off + 6 + 8 * ib),
+        wdec_iq3_s_core<SG>(lds_u16(row, off), lds_u32(row, off + 2 + 8 * ib), lds_u32(row, off + 6 + 8 * ib),
                         row[off + 66 + ib], lds_u32(row, off + 74 + 4 * ib), (sc >> (4 * (ib & 1))) & 0xFu, grid, w);
     }
 }

@@ -483,6 +483,14 @@ __device__ __forceinline__ int e1_issue(uint8_t* buf, const uint8_t* gate, const
     return pre;
 }
 
+// k_moe_expert1's items decode IQ3_S with the sign-folded codebook: 36 of
+// the ~70 VALU instructions of a block's decode (the per-word sign masks) go
+// for ~8 more of index arithmetic; the 32 KiB fill overlaps the logits /
+// top-k phase, and the kernel's one work-group per CU has the LDS.  One-token
+// IQ3_S layer 16.86 -> 16.76 us (Q5_K shared), 16.75 -> 16.61 us (Q8_0); in
+// the several-token and prefill kernels, whose LDS it crowds and whose fill
+// it cannot hide, the same table was slower.
+constexpr bool E1_SG = true;
 // Dots of chunk c for this thread's row (row group g) and lane j: blocks
 // j, j+16, ... of the chunk, in ascending order (the L=16 order).
 template <int T>
@@ -496,7 +504,7 @@ __device__ __forceinline__ float e1_dots(const uint8_t* buf, int pre, const XLds
     for (int b = j; b < CBLK; b += SLOTS) {
         if (b < cb) {
             WBlk wb;
-            block_decode<T>(row, b, grid, wb);
+            block_decode<T, E1_SG>(row, b, grid, wb);
             XBlk xb;
             xlds_to_blk(xs[c * CBLK + b], xb);
             acc = wacc<T>(wb, xb, acc);
@@ -601,7 +609,7 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert1(MoeArgs a) {
     // + 16: lds_u32 of a row's last block reads up to 4 bytes past the row
     __shared__ __attribute__((aligned(16))) uint8_t bufA[2 * QK * CB + 16];
     __shared__ __attribute__((aligned(16))) uint8_t bufB[2 * QK * CB + 16];
-    __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
+    __shared__ __attribute__((aligned(16))) uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? (E1_SG ? 8192 : 512) : 1];
     __shared__ XLds xs[E1_MAX_H / QK];
     __shared__ float hg[1][QK], hu[1][QK];
     __shared__ int s_ids[MAX_K];
@@ -617,8 +625,13 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert1(MoeArgs a) {
     const int ns = a.has_shared ? (NB > x ? (NB - 1 - x) / 8 + 1 : 0) : 0;
     const int nx = nr * NB + ns;
     const bool routed = lb < nr * NB, shared = !routed && lb < nx;
-    if constexpr (TE == T_IQ3_S || TS == T_IQ3_S)   // visible after the first barrier below
-        for (int i = tid; i < 512; i += EX_THREADS) grid[i] = c_iq3s_grid_moe[i];
+    if constexpr (TE == T_IQ3_S || TS == T_IQ3_S) {   // visible after the first barrier below
+        if constexpr (E1_SG) {
+            if (routed || shared) iq3s_sgrid_fill(grid, tid, EX_THREADS);
+        } else {
+            for (int i = tid; i < 512; i += EX_THREADS) grid[i] = c_iq3s_grid_moe[i];
+        }
+    }
     if (!shared) {
         // wave 0: softmax / top-k; the other waves decode Q8_1(x) meanwhile
         if (wave == 0) {

@@ -15,8 +15,8 @@ read may touch) must stay inside the buffer."""
 import pytest
 
 QK = 32
-BYTES = {"q4_0": 18, "q8_0": 34, "iq3s": 110}
-ELEMS = {"q4_0": 32, "q8_0": 32, "iq3s": 256}
+BYTES = {"q4_0": 18, "q8_0": 34, "iq3s": 110, "q6k": 210}
+ELEMS = {"q4_0": 32, "q8_0": 32, "iq3s": 256, "q6k": 256}
 
 
 def chunk_bytes(t, blocks):
@@ -73,7 +73,7 @@ PF_XROW, PF_XROW_AL = PF_CHUNK * 36, PF_CHUNK * 36 + 16
 
 
 def pf_lds_row(t):
-    return 128 if t == "iq3s" else chunk_bytes(t, PF_CHUNK)
+    return {"iq3s": 128, "q6k": 224}.get(t, chunk_bytes(t, PF_CHUNK))
 
 
 def pf_lds_row_al(t):
@@ -82,7 +82,7 @@ def pf_lds_row_al(t):
 
 
 @pytest.mark.parametrize("t,NR,n0", [("q4_0", 128, 64), ("q8_0", 128, 64), ("iq3s", 128, 64), ("iq3s", 128, 128),
-                                     ("q4_0", 128, 128)])
+                                     ("q4_0", 128, 128), ("q6k", 128, 64), ("q6k", 128, 128)])
 def test_prefill_two_stage_padded_slots(t, NR, n0):
     CBL, CBLP = pf_lds_row(t), pf_lds_row_al(t)
     PCB, PCBP, PER, PERP = CBL // 16, CBLP // 16, PF_XROW // 16, PF_XROW_AL // 16
@@ -116,9 +116,10 @@ def test_prefill_two_stage_padded_slots(t, NR, n0):
                         assert (r, col) not in xseen
                         xseen.add((r, col))
     assert len(wseen) == NR * PCB and len(xseen) == PF_TILE * PER
-    # readers: the last row's chunk (at most 14 bytes into its span for IQ3_S)
-    # plus a 4-byte unaligned read; the activation metadata / fragments
-    span_off = 14 if t == "iq3s" else 0   # (c * CB) % 16: nonzero only for 110-byte chunks
+    # readers: the last row's chunk (at most 14 bytes into its span for IQ3_S
+    # and Q6_K) plus a 4-byte unaligned read; the activation metadata / fragments
+    span_off = max(c * chunk_bytes(t, PF_CHUNK) % 16 for c in range(16))   # 110- / 210-byte chunks: 14
+    assert span_off + chunk_bytes(t, PF_CHUNK) <= CBL   # the chunk fits its span
     assert (NR - 1) * CBLP + span_off + chunk_bytes(t, PF_CHUNK) + 4 <= wbuf
     assert (PF_TILE - 1) * PF_XROW_AL + (PF_CHUNK - 1) * 36 + 36 <= xbuf
 
@@ -142,3 +143,57 @@ def test_spans_in_288_byte_slots(pre):
     assert len(seen) == nrows * per0
     # the chunk's last byte (plus a 4-byte unaligned read) stays in the row's slot
     assert pre + seg + 4 <= per * 16
+
+
+def test_iq3s_sign_folded_codebook_lookup():
+    """The one-token expert kernel's IQ3_S lookups in the sign-folded codebook
+    (chimere_amd/csrc/common.h: Iq3sSignedGrid, iq3s_levels<true>): entry
+    16 i + n is entry i with byte k negated where bit k of n is set, and the
+    byte offsets (pr << 6) | ((s * 0x4004) & 0x3C003C) of a perm-packed index
+    pair give entries 16 idx + nibble in both 16-bit halves.  Checked against
+    the codebook with the signs applied per byte (the decode every other kernel
+    and the oracle use), for every entry and sign nibble, and on random blocks."""
+    import numpy as np
+    import npref
+    G = npref.GRID.astype(np.int64)
+    tab = np.zeros(8192, np.int64)
+    for n in range(16):
+        v = np.zeros(512, np.int64)
+        for k in range(4):
+            b = (G >> (8 * k)) & 255
+            v |= (np.where((n >> k) & 1, (256 - b) & 255, b)) << (8 * k)
+        tab[np.arange(512) * 16 + n] = v
+    for n in range(16):   # every entry, every sign nibble: signed levels
+        for k in range(4):
+            lv = (G >> (8 * k)) & 255
+            got = ((tab[np.arange(512) * 16 + n] >> (8 * k)) & 255).astype(np.int8).astype(np.int64)
+            assert (got == np.where((n >> k) & 1, -lv, lv)).all()
+
+    def perm(src0, src1, sel):   # v_perm_b32 with selectors 0..7 (bytes of src1, then src0)
+        b = [(src1 >> (8 * i)) & 255 for i in range(4)] + [(src0 >> (8 * i)) & 255 for i in range(4)]
+        return sum(b[(sel >> (8 * i)) & 255] << (8 * i) for i in range(4))
+
+    def nib_bits(n):
+        return (n * 0x00204081) & 0x01010101
+
+    rng = np.random.default_rng(5)
+    for _ in range(2000):
+        qs = [int(x) for x in rng.integers(0, 256, 8)]
+        qh, sg = int(rng.integers(0, 256)), int(rng.integers(0, 1 << 32))
+        qs0 = qs[0] | qs[1] << 8 | qs[2] << 16 | qs[3] << 24
+        qs1 = qs[4] | qs[5] << 8 | qs[6] << 16 | qs[7] << 24
+        h0, h1 = nib_bits(qh & 15), nib_bits((qh >> 4) & 15)
+        for p in range(4):
+            pr = perm(h0 if p < 2 else h1, qs0 if p < 2 else qs1, 0x07030602 if p & 1 else 0x05010400)
+            t = (((sg >> (8 * p)) & 255) * 0x4004) & 0x003C003C
+            ab = ((pr << 6) | t) & 0xFFFFFFFF
+            for half, word in ((ab & 0xFFFF, 2 * p), (ab >> 16, 2 * p + 1)):
+                assert half % 4 == 0 and half < 32768
+                idx = qs[word] | ((qh >> word) & 1) << 8          # entry of word `word`
+                nib = (sg >> (4 * word)) & 15                     # its sign nibble
+                assert half // 4 == 16 * idx + nib
+                want = 0
+                for k in range(4):
+                    lv = (int(G[idx]) >> (8 * k)) & 255
+                    want |= (((256 - lv) & 255) if (nib >> k) & 1 else lv) << (8 * k)
+                assert int(tab[half // 4]) == want
