@@ -330,6 +330,22 @@ def main():
                     t1m, _ = graph_time(fns, flush=flush)
                     u1 = t1m / 96 * 1e6
                     extra[tag] = {"us_per_layer": round(u1, 2), "GBs_selected": round(sel3 / (u1 * 1e-6) / 1e9, 1)}
+                # the reference's f32-activation IQ3_S expert path (fused_moe_iq3s) on the same
+                # routed experts: K experts per call, a new expert set per step, cache flushed
+                from chimere_amd.moe import fused_moe_iq3s
+                gf = torch.Generator(device=dev).manual_seed(11)
+                fm_ids = [torch.randperm(E, generator=gf, device=dev)[:K].to(torch.int32) for _ in range(96)]
+                fm_w = torch.rand(K, generator=gf, device=dev) * 0.2
+                fm_out = torch.zeros(H, device=dev)
+                fm_ws = torch.empty(K * F * 4, dtype=torch.uint8, device=dev)
+                fm_t = [lb.tensors[1:4] for lb in l8base]
+                fns = [(lambda i=i: fused_moe_iq3s(x1[i % 64, 0], *fm_t[i % len(fm_t)], fm_ids[i], fm_w, fm_out, H, F,
+                                                   fm_t[0][0].shape[1], fm_t[0][1].shape[1], fm_t[0][2].shape[1], K,
+                                                   workspace=fm_ws)) for i in range(96)]
+                tfm, _ = graph_time(fns, flush=flush)
+                ufm = tfm / 96 * 1e6
+                extra["fused_moe_iq3s_f32_top8"] = {"us": round(ufm, 2), "GBs_selected": round(sel3 / (ufm * 1e-6) / 1e9, 1),
+                                                    "note": "routed experts only (no router, no shared expert), f32 activations"}
                 if not args.no_ncmoe:
                     # the same layer with its routed experts on the host (the
                     # reference's ncmoe path): device router + top-k, host expert

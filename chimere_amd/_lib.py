@@ -56,6 +56,8 @@ SIGNATURES = [
     ("chimere_moe_ffn_decode_noalloc", None, [vp, vp, vp, i32, vp, vp, vp]),
     ("chimere_moe_prefill_workspace_size", szt, [vp, i32]),
     ("chimere_moe_prefill", None, [vp, vp, vp, i32, vp, vp, vp, szt, vp]),
+    ("chimere_fused_moe_iq3s_workspace_size", szt, [i32, i32, i32]),
+    ("chimere_fused_moe_iq3s", None, [vp, vp, vp, vp, vp, vp, vp, i32, i32, i64, i64, i64, i32, vp, szt, vp]),
     ("chimere_quantize_weights", None, [i32, vp, vp, i64, vp]),
     ("chimere_dbg_block_dots", None, [i32, vp, vp, vp, i32, i32, vp]),
     ("chimere_hip_get_last_error", i32, []),

@@ -10,6 +10,9 @@ for a chunk of tokens.
 (``chimere_amd.cpu``, the reference's "ncmoe" path) and the rest on the
 device.
 
+``fused_moe_iq3s`` is the expert FFN on unquantized activations (the
+reference's fallback GPU path, ``chimere-server/src/kernels/fused_moe.rs``).
+
 ``forward_moe_v3`` replays the reference's own launch sequence
 (``chimere-server/src/qwen35_model/moe_ffn.rs:1094-1384`` V3 batched path and
 ``:1597-1761`` shared expert) through the ``ggml_gpu`` mirror; it computes the
@@ -248,3 +251,23 @@ class MoeLayer:
         if self._g_tail is not None:
             self._g_tail.replay()
         return self._nc_out, self._nc_ids, self._nc_w
+
+
+def fused_moe_iq3s(hidden, gate_exps, up_exps, down_exps, expert_ids, expert_weights, output, hidden_size,
+                   expert_ffn, expert_bytes_gate, expert_bytes_up, expert_bytes_down, top_k, workspace=None):
+    """output [hidden_size] f32 += sum_k expert_weights[k] * FFN_{expert_ids[k]}(hidden): IQ3_S experts on
+    the f32 hidden state through ``chimere_fused_moe_iq3s`` (the arguments of the reference's
+    ``fused_moe_iq3s_gpu_resident``, chimere-server/src/kernels/fused_moe.rs:417-468; ids and weights are
+    device tensors).  As there, output accumulates: zero it for the bare FFN.  The workspace (h of
+    every expert) is allocated here unless one is passed."""
+    need = lib().chimere_fused_moe_iq3s_workspace_size(hidden_size, expert_ffn, top_k)
+    if workspace is None:
+        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=output.device)
+    lib().chimere_fused_moe_iq3s(C.c_void_p(hidden.data_ptr()), C.c_void_p(gate_exps.data_ptr()),
+                                 C.c_void_p(up_exps.data_ptr()), C.c_void_p(down_exps.data_ptr()),
+                                 C.c_void_p(expert_ids.data_ptr()), C.c_void_p(expert_weights.data_ptr()),
+                                 C.c_void_p(output.data_ptr()), hidden_size, expert_ffn, expert_bytes_gate,
+                                 expert_bytes_up, expert_bytes_down, top_k, C.c_void_p(workspace.data_ptr()),
+                                 workspace.numel(), G._stream())
+    check()
+    return output

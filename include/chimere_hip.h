@@ -254,6 +254,29 @@ void chimere_moe_prefill(const chimere_moe_layer *layer, const float *x, float *
                          int *ids_out, float *w_out, void *workspace, size_t workspace_bytes,
                          hipStream_t stream);
 
+/* Expert FFN on unquantized activations, IQ3_S experts: replaces the
+ * reference's fused_moe_iq3s (cs/src/kernels/fused_moe.rs:345-468, kernel
+ * :261-311 = cs/kernels/chimere_kernels.cu:1093-1143), its GPU path when the
+ * ggml Q8_1 kernels are not selected (cs/src/qwen35_model/moe_ffn.rs:1476-1500).
+ * For k < top_k, e = expert_ids[k] (device array; each id must index an expert
+ * of the stacked tensors): g = G_e x, u = U_e x with f32 x = hidden,
+ * h = silu(g) * u, y_k = D_e h, and output[r] += sum_k expert_weights[k] * y_k[r]
+ * (output accumulates, as the reference's atomicAdd does: zero it first for
+ * the bare FFN).  gate_exps / up_exps hold [E][expert_ffn rows][hidden_size]
+ * IQ3_S, down_exps [E][hidden_size rows][expert_ffn], expert_bytes_* apart.
+ * Unlike the reference (atomicAdd in block order), the sum over k is in
+ * ascending k and every dot has a fixed order, so results repeat bit for bit.
+ * hidden_size a multiple of 256 up to 4096, expert_ffn a multiple of 256 up to
+ * 512, top_k 1..16; weights 4-byte aligned, hidden 16-byte aligned.  The
+ * workspace (h of every expert) is chimere_fused_moe_iq3s_workspace_size
+ * bytes, 16-byte aligned; no allocation. */
+size_t chimere_fused_moe_iq3s_workspace_size(int hidden_size, int expert_ffn, int top_k);
+void chimere_fused_moe_iq3s(const float *hidden, const void *gate_exps, const void *up_exps,
+                            const void *down_exps, const int *expert_ids, const float *expert_weights,
+                            float *output, int hidden_size, int expert_ffn, int64_t expert_bytes_gate,
+                            int64_t expert_bytes_up, int64_t expert_bytes_down, int top_k,
+                            void *workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* ----------------------------------------------- weight quantizers (GPU) */
 /* Not part of the reference's ABI (its weights come pre-quantized from GGUF);
  * used to build synthetic weights on the device.  n multiple of 32 (IQ3_S:

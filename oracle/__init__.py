@@ -50,6 +50,7 @@ def lib():
         L.orc_moe.argtypes = [vp, vp, vp, vp, vp, i32]
         L.cpb_gemv.argtypes = [i32, vp, vp, vp, i32, i32, i32]
         L.cpb_moe.argtypes = [vp, vp, vp, vp, vp, i32]
+        L.orc_fused_moe_iq3s.argtypes = [vp, vp, vp, vp, vp, vp, vp, i32, i32, i64, i64, i64, i32]
         L.orc_quantize_q8_K.argtypes = [vp, i64, vp]
         L.orc_vec_dot_iq3s_q8K.restype = f32
         L.orc_vec_dot_iq3s_q8K.argtypes = [i32, vp, vp]
@@ -137,6 +138,16 @@ def gemv_q8_0_f64(W, x, ncols, nrows):
     y = np.zeros(nrows, np.float32)
     lib().orc_gemv_q8_0_f64(_p(np.ascontiguousarray(W)), _p(np.ascontiguousarray(x, np.float32)), _p(y), ncols, nrows)
     return y
+
+
+def fused_moe_iq3s(x, gate, up, down, ids, wts, out, H, F, bg, bu, bd):
+    """out (f32 [H], updated in place) += the f32-activation IQ3_S expert FFN of the
+    experts ids with weights wts (the library's fixed order)."""
+    ids = np.ascontiguousarray(ids, np.int32)
+    lib().orc_fused_moe_iq3s(_p(np.ascontiguousarray(x, np.float32)), _p(np.ascontiguousarray(gate)),
+                             _p(np.ascontiguousarray(up)), _p(np.ascontiguousarray(down)), _p(ids),
+                             _p(np.ascontiguousarray(wts, np.float32)), _p(out), H, F, bg, bu, bd, ids.size)
+    return out
 
 
 def router(Wr, x):

@@ -103,6 +103,11 @@ void orc_moe(const orc_moe_params *p, const float *x, float *out,
 
 /* ncmoe CPU expert path (moe_ffn.rs:1507-1591, ffi/ggml_iq3s_gemv.c): Q8_K
  * activations (296-byte blocks), IQ3_S x Q8_K dots, the one-token expert loop. */
+/* fused MoE on f32 activations, IQ3_S experts (the library's fixed order):
+ * out[r] += sum_k wts[k] * (D_{ids[k]} (silu(G x) * (U x)))[r] */
+void orc_fused_moe_iq3s(const float *x, const uint8_t *gate, const uint8_t *up, const uint8_t *down,
+                        const int32_t *ids, const float *wts, float *out, int H, int F,
+                        int64_t bg, int64_t bu, int64_t bd, int K);
 void orc_quantize_q8_K(const float *x, int64_t k, uint8_t *out);
 float orc_vec_dot_iq3s_q8K(int n, const uint8_t *w, const uint8_t *y);
 void orc_gemv_iq3s_q8K(const uint8_t *W, const float *x, float *y, int nrows, int ncols);
