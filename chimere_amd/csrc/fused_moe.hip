@@ -11,18 +11,21 @@
 // The reference runs one block per expert and adds w_k * y_k into output with
 // atomicAdd (an order that varies between runs).  Here two launches, and a
 // fixed fp32 order:
-//   * a row's dot: lane j of its 16-lane group takes the 32-element blocks
-//     j, j+16, ... in ascending order; a block's sum is s = fmaf(level_e, x_e, s)
-//     over its 32 elements (signed int8 levels, exact as f32), then
-//     acc = fmaf(f32(d) * (1 + 2 * scale), s, acc); the 16 lanes are summed by
-//     the halving tree xor 8, 4, 2, 1;
+//   * a row's dot over L lanes (gate / up rows: L = 64, one wave per row; down
+//     rows: L = 16): lane j takes the 32-element blocks j, j+L, ... in
+//     ascending order; a block's sum is s = fmaf(level_e, x_e, s) over its 32
+//     elements (signed int8 levels, exact as f32), then
+//     acc = fmaf(f32(d) * (1 + 2 * scale), s, acc); the L lanes are summed by
+//     the halving tree (lanes j, j + m for m = L/2, ..., 1);
 //   * h = det_silu(g) * u;
 //   * output[r] = output[r] + a, a = fmaf(w_k, y_k[r], a) over k ascending from 0.
-// Launch 1 (gate/up): grid (F/32, K), 1024 threads: gate rows [32w, 32w+32) and
-// the same up rows of expert ids[k] (64 rows, one per 16-lane group), the
-// activation row in LDS, weight rows staged in 64-block chunks; h to the
-// workspace.  Launch 2 (down + combine): grid H/8, 128 threads: 8 down rows
-// for every expert (all K experts' row runs staged at once), then the combine.
+// Launch 1 (gate/up): grid (F/2, K), 256 threads: gate rows 2w, 2w+1 and the
+// same up rows of expert ids[k] (one wave each; h needs only a row's own gate
+// and up values), the activation row in LDS, weight rows staged in 64-block
+// chunks (one block per lane per chunk); h to the workspace.  Launch 2 (down + combine):
+// grid ceil(H/R), 256 threads, R = 16 / K rows: 16-lane group g takes down row
+// r0 + g / K of expert g % K; the R rows' K results are then combined in k
+// order by one thread per row.
 #include "api_internal.h"
 #include "common.h"
 
@@ -30,13 +33,14 @@ namespace chimere {
 
 __constant__ uint32_t c_iq3s_grid_fm[512] = CHIMERE_IQ3S_GRID_INIT;
 
-constexpr int FM_RG = 64;                   // gate/up rows per work-group (32 gate + 32 up)
-constexpr int FM_THREADS = FM_RG * SLOTS;   // 1024
+// gate rows per work-group (and as many up rows): 2 (2048 work-groups of 4
+// waves for F = 512, top-8) measured 10.3 us against 12.3 us with 8
+constexpr int FM_GR = 2;
+constexpr int FM_THREADS = 2 * FM_GR * 64;   // a wave per gate / up row
 constexpr int FM_CBLK = 64;                 // 32-element blocks per staged chunk (8 superblocks)
 constexpr int FM_CB = FM_CBLK / 8 * 110;    // 880 bytes of a row per chunk
 constexpr int FM_MAX_H = 4096;              // activation row in LDS (16 KiB)
-constexpr int FM_DR = 8;                    // down rows per work-group
-constexpr int FM_MAX_F = 512;               // down rows staged whole: F / 256 superblocks
+constexpr int FM_MAX_F = 512;               // a down row staged whole: F / 256 superblocks
 constexpr int FM_MAX_K = 16;
 
 struct FmArgs {
@@ -61,76 +65,107 @@ __device__ __forceinline__ float blk_dot_f32(const WBlk& w, const float* __restr
 }
 
 __global__ __launch_bounds__(FM_THREADS) void k_fm_gate_up(FmArgs a) {
-    __shared__ float xs[FM_MAX_H];
-    __shared__ __attribute__((aligned(16))) uint8_t tile[FM_RG * FM_CB + 16];
+    __shared__ __attribute__((aligned(16))) float xs[FM_MAX_H];
+    __shared__ __attribute__((aligned(16))) uint8_t tile[2 * FM_GR * FM_CB + 16];
     __shared__ uint32_t grid[512];
-    __shared__ float hg[QK], hu[QK];
-    const int tid = threadIdx.x, g = tid >> 4, j = tid & 15;
+    __shared__ float hg[FM_GR], hu[FM_GR];
+    const int tid = threadIdx.x, g = tid >> 6, j = tid & 63;
     const int w = blockIdx.x, k = blockIdx.y;
     const int64_t e = a.ids[k];
     const int nb = a.H / QK;
     const int64_t rb = (int64_t)a.H / 256 * 110;
-    for (int i = tid; i < a.H; i += FM_THREADS) xs[i] = a.x[i];
-    for (int i = tid; i < 512; i += FM_THREADS) grid[i] = c_iq3s_grid_fm[i];
-    const uint8_t* g0 = a.gate + e * a.bg + (int64_t)w * QK * rb;
-    const uint8_t* u0 = a.up + e * a.bu + (int64_t)w * QK * rb;
+    const uint8_t* g0 = a.gate + e * a.bg + (int64_t)w * FM_GR * rb;
+    const uint8_t* u0 = a.up + e * a.bu + (int64_t)w * FM_GR * rb;
     float acc = 0.0f;
     for (int b0 = 0; b0 < nb; b0 += FM_CBLK) {
         const int cb = min(FM_CBLK, nb - b0), seg = cb / 8 * 110;
         const int64_t goff = (int64_t)b0 / 8 * 110;
-        __syncthreads();   // the previous chunk is consumed (and xs / grid written)
-        stage_rows<true, CPOL_STREAM>(tile, g0 + goff, rb, QK, seg, tid, FM_THREADS);
-        stage_rows<true, CPOL_STREAM>(tile + QK * seg, u0 + goff, rb, QK, seg, tid, FM_THREADS);
+        if (b0) __syncthreads();   // the previous chunk is consumed
+        stage_rows<true, CPOL_STREAM>(tile, g0 + goff, rb, FM_GR, seg, tid, FM_THREADS);
+        stage_rows<true, CPOL_STREAM>(tile + FM_GR * seg, u0 + goff, rb, FM_GR, seg, tid, FM_THREADS);
+        if (b0 == 0) {   // the activation row and the codebook, while the first chunk's rows are in flight
+            for (int i = tid; i < a.H / 4; i += FM_THREADS) ((float4*)xs)[i] = ((const float4*)a.x)[i];
+            for (int i = tid; i < 512; i += FM_THREADS) grid[i] = c_iq3s_grid_fm[i];
+        }
         lds_copy_wait();
         __syncthreads();
         const uint8_t* row = tile + g * seg;
-        for (int b = j; b < cb; b += SLOTS) {
+        if (j < cb) {   // chunks of 64 blocks: block j
             WBlk wb;
-            block_decode<T_IQ3_S>(row, b, grid, wb);
-            const float s = blk_dot_f32(wb, xs + QK * (b0 + b));
+            block_decode<T_IQ3_S>(row, j, grid, wb);
+            const float s = blk_dot_f32(wb, xs + QK * (b0 + j));
             acc = __builtin_fmaf(wb.dw * (float)wb.mult, s, acc);
         }
     }
-    const float v = slot_reduce16(acc);
+    // the 64 lanes by the halving tree (lane 0 holds it)
+    float v = acc + xlane<32>(acc);
+    v = v + xlane<16>(v);
+    v = slot_reduce16(v);
     if (j == 0) {
-        if (g < QK) hg[g] = v;
-        else hu[g - QK] = v;
+        if (g < FM_GR) hg[g] = v;
+        else hu[g - FM_GR] = v;
     }
     __syncthreads();
-    if (tid < QK) a.h[(int64_t)k * a.F + w * QK + tid] = det_silu(hg[tid]) * hu[tid];
+    if (tid < FM_GR) a.h[(int64_t)k * a.F + w * FM_GR + tid] = det_silu(hg[tid]) * hu[tid];
 }
 
-__global__ __launch_bounds__(FM_DR * SLOTS) void k_fm_down(FmArgs a) {
-    constexpr int RUN = FM_DR * (FM_MAX_F / 256 * 110);   // bytes of one expert's FM_DR rows at most
-    __shared__ __attribute__((aligned(16))) uint8_t wl[FM_MAX_K * RUN + 16];
+__global__ __launch_bounds__(256) void k_fm_down(FmArgs a) {
+    constexpr int ROWB = FM_MAX_F / 256 * 110;   // bytes of a down row at most
+    __shared__ __attribute__((aligned(16))) uint8_t wl[16 * ROWB + 16];
     __shared__ uint32_t grid[512];
+    __shared__ float ys[16];
+    __shared__ int s_ids[FM_MAX_K];
+    __shared__ float s_w[FM_MAX_K];
     const int tid = threadIdx.x, g = tid >> 4, j = tid & 15;
-    const int r0 = blockIdx.x * FM_DR;
+    const int K = a.K, R = 16 / K, r0 = blockIdx.x * R;
     const int nb = a.F / QK;
-    const int64_t rb = (int64_t)a.F / 256 * 110;
-    const int run = FM_DR * (int)rb;
-    for (int i = tid; i < 512; i += FM_DR * SLOTS) grid[i] = c_iq3s_grid_fm[i];
-    for (int k = 0; k < a.K; k++)
-        stage_rows<true, CPOL_STREAM>(wl + k * run, a.down + (int64_t)a.ids[k] * a.bd + r0 * rb, rb, FM_DR,
-                                      (int)rb, tid, FM_DR * SLOTS);
-    lds_copy_wait();
-    __syncthreads();
-    float o = 0.0f;
-    for (int k = 0; k < a.K; k++) {
-        const uint8_t* row = wl + k * run + g * rb;
-        const float* hk = a.h + (int64_t)k * a.F;
-        float acc = 0.0f;
-        for (int b = j; b < nb; b += SLOTS) {
-            WBlk wb;
-            block_decode<T_IQ3_S>(row, b, grid, wb);
-            float hb[QK];
+    const int rb = a.F / 256 * 110;
+    if (tid < K) {
+        s_ids[tid] = a.ids[tid];
+        s_w[tid] = a.wts[tid];
+    }
+    for (int i = tid; i < 512; i += 256) grid[i] = c_iq3s_grid_fm[i];
+    // group g: down row r0 + g / K of expert g % K
+    const bool act = g < R * K && r0 + g / K < a.H;
+    const int k = g % K;
+    // prefetched while the ids load: this lane's h block (F <= 512: block j
+    // only) and the output values of the combining threads
+    float hb[QK];
+    if (act && j < nb) {
+        const float* hk = a.h + (int64_t)k * a.F + QK * j;
 #pragma unroll
-            for (int i = 0; i < QK / 4; i++) *(float4*)(hb + 4 * i) = *(const float4*)(hk + QK * b + 4 * i);
+        for (int i = 0; i < QK / 4; i++) *(float4*)(hb + 4 * i) = *(const float4*)(hk + 4 * i);
+    }
+    const bool comb = tid < R && r0 + tid < a.H;
+    const float out0 = comb ? a.out[r0 + tid] : 0.0f;
+    __syncthreads();   // s_ids, s_w, grid
+    if (act) {
+        // the group stages its own row (lanes of one wave: visible to the
+        // group once its LDS writes are done)
+        uint8_t* row = wl + g * ROWB;
+        const uint8_t* src = a.down + (int64_t)s_ids[k] * a.bd + (int64_t)(r0 + g / K) * rb;
+        if ((rb & 3) == 0) {
+            for (int c = j; c < rb / 4; c += SLOTS) ((uint32_t*)row)[c] = ((const uint32_t*)src)[c];
+        } else {
+            for (int c = j; c < rb / 2; c += SLOTS) ((uint16_t*)row)[c] = ((const uint16_t*)src)[c];
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's LDS writes are done
+        __builtin_amdgcn_wave_barrier();
+        float acc = 0.0f;
+        if (j < nb) {   // F <= 512: one block per lane
+            WBlk wb;
+            block_decode<T_IQ3_S>(row, j, grid, wb);
             acc = __builtin_fmaf(wb.dw * (float)wb.mult, blk_dot_f32(wb, hb), acc);
         }
-        o = __builtin_fmaf(a.wts[k], slot_reduce16(acc), o);
+        const float v = slot_reduce16(acc);
+        if (j == 0) ys[g] = v;
     }
-    if (j == 0) a.out[r0 + g] = a.out[r0 + g] + o;
+    __syncthreads();
+    if (comb) {
+        float o = 0.0f;
+        for (int kk = 0; kk < K; kk++) o = __builtin_fmaf(s_w[kk], ys[tid * K + kk], o);
+        a.out[r0 + tid] = out0 + o;
+    }
 }
 
 }  // namespace chimere
@@ -176,8 +211,9 @@ void chimere_fused_moe_iq3s(const float* hidden, const void* gate_exps, const vo
     a.ids = expert_ids; a.wts = expert_weights; a.out = output; a.h = (float*)workspace;
     a.H = H; a.F = F; a.K = K;
     a.bg = expert_bytes_gate; a.bu = expert_bytes_up; a.bd = expert_bytes_down;
-    hipLaunchKernelGGL(k_fm_gate_up, dim3(F / QK, K), dim3(FM_THREADS), 0, stream, a);
-    hipLaunchKernelGGL(k_fm_down, dim3(H / FM_DR), dim3(FM_DR * SLOTS), 0, stream, a);
+    const int R = 16 / K;
+    hipLaunchKernelGGL(k_fm_gate_up, dim3(F / FM_GR, K), dim3(FM_THREADS), 0, stream, a);
+    hipLaunchKernelGGL(k_fm_down, dim3((H + R - 1) / R), dim3(256), 0, stream, a);
     check_launch("fused_moe_iq3s");
 }
 

@@ -652,23 +652,23 @@ void orc_moe(const orc_moe_params *p, const float *x, float *out,
  * output += w_k * y_k.  The reference sums each row sequentially in one
  * thread (fma of d * (1 + 2 sc) * level * sign with x) and adds the experts'
  * terms by atomicAdd, in no fixed order; restated here in the HIP kernels'
- * fixed order (chimere_amd/csrc/fused_moe.hip): lane j = b % 16 of a row
- * takes its 32-element blocks in ascending order, a block's s = fmaf(level_e,
- * x_e, s) over e = 0..31, acc_j = fmaf(f32(d) * (1 + 2 sc), s, acc_j), lanes
- * by the halving tree; output[r] = output[r] + a, a = fmaf(w_k, y_k[r], a)
- * for k ascending. */
-static float iq3s_row_f32(const uint8_t *row, const float *x, int nb) {
-    float acc[16];
-    for (int j = 0; j < 16; j++) acc[j] = 0.0f;
+ * fixed order (chimere_amd/csrc/fused_moe.hip): lane j = b % L of a row
+ * (gate / up rows L = 64, down rows L = 16) takes its 32-element blocks in
+ * ascending order, a block's s = fmaf(level_e, x_e, s) over e = 0..31,
+ * acc_j = fmaf(f32(d) * (1 + 2 sc), s, acc_j), lanes by the halving tree;
+ * output[r] = output[r] + a, a = fmaf(w_k, y_k[r], a) for k ascending. */
+static float iq3s_row_f32(const uint8_t *row, const float *x, int nb, int L) {
+    float acc[64];
+    for (int j = 0; j < L; j++) acc[j] = 0.0f;
     for (int b = 0; b < nb; b++) {
         const uint8_t *blk = row + (int64_t)(b >> 3) * 110;
         const int ib = b & 7;
         float s = 0.0f;
         for (int e = 0; e < 32; e++) s = fmaf((float)iq3s_level(blk, ib, e), x[32 * b + e], s);
         const float scale = orc_f16_to_f32(rd16(blk)) * (float)iq3s_mult(blk, ib);
-        acc[b % 16] = fmaf(scale, s, acc[b % 16]);
+        acc[b % L] = fmaf(scale, s, acc[b % L]);
     }
-    for (int m = 8; m >= 1; m >>= 1)
+    for (int m = L / 2; m >= 1; m >>= 1)
         for (int i = 0; i < m; i++) acc[i] = acc[i] + acc[i + m];
     return acc[0];
 }
@@ -680,14 +680,14 @@ void orc_fused_moe_iq3s(const float *x, const uint8_t *gate, const uint8_t *up, 
     float *h = malloc(sizeof(float) * (size_t)K * F);
     for (int k = 0; k < K; k++)
         for (int f = 0; f < F; f++) {
-            const float g = iq3s_row_f32(gate + ids[k] * bg + f * rbH, x, H / 32);
-            const float u = iq3s_row_f32(up + ids[k] * bu + f * rbH, x, H / 32);
+            const float g = iq3s_row_f32(gate + ids[k] * bg + f * rbH, x, H / 32, 64);
+            const float u = iq3s_row_f32(up + ids[k] * bu + f * rbH, x, H / 32, 64);
             h[(int64_t)k * F + f] = orc_silu(g) * u;
         }
     for (int r = 0; r < H; r++) {
         float a = 0.0f;
         for (int k = 0; k < K; k++)
-            a = fmaf(wts[k], iq3s_row_f32(down + ids[k] * bd + r * rbF, h + (int64_t)k * F, F / 32), a);
+            a = fmaf(wts[k], iq3s_row_f32(down + ids[k] * bd + r * rbF, h + (int64_t)k * F, F / 32, 16), a);
         out[r] = out[r] + a;
     }
     free(h);
