@@ -46,7 +46,7 @@ def parse():
     ap.add_argument("--no-ncmoe", action="store_true", help="skip the host expert path (ncmoe) figures")
     ap.add_argument("--cpu-seconds", type=float, default=6.0, help="CPU baseline budget (about a tenth per figure)")
     ap.add_argument("--pmc", action="store_true", help="light mode for rocprofv3 --pmc runs")
-    ap.add_argument("--pmc-workload", choices=["m1", "m8", "prefill", "prefill_iq3s", "head"], default="m1",
+    ap.add_argument("--pmc-workload", choices=["m1", "m8", "prefill", "prefill_iq3s", "head", "q5k"], default="m1",
                     help="workload of the --pmc light mode")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="run one device copy of this many MiB at the end (calibrates PMC byte counters)")
@@ -147,6 +147,17 @@ def main():
             y = torch.empty(V, device=dev)
             for i in range(args.steps):
                 G.ggml_gpu_gemv_q4_0_q8(head, xq, y, V, H)
+        elif wl == "q5k":
+            # the Q5_K GEMV (the reference model's shared-expert type) at 16384 x 4096,
+            # random valid blocks as in the timed leg
+            Rk, Ck = 16384, 4096
+            g = torch.Generator(device=dev).manual_seed(2)
+            wk = torch.randint(0, 256, (Rk * (Ck // 256 * 176),), dtype=torch.uint8, device=dev, generator=g)
+            xk = torch.empty(G.q8_1_row_bytes(Ck), dtype=torch.uint8, device=dev)
+            G.ggml_gpu_quantize_q8_1(torch.randn(Ck, generator=g, device=dev), xk, Ck)
+            yk = torch.empty(Rk, device=dev)
+            for i in range(args.steps):
+                G.ggml_gpu_gemv_q5k_q8(wk, xk, yk, Rk, Ck)
         else:
             L = make_layer(100, *((IQ3_S, Q8_0) if wl in ("m8", "prefill_iq3s") else (Q4_0, Q4_0)))
             M = {"m1": 1, "m8": 8, "prefill": 512, "prefill_iq3s": 512}[wl]
