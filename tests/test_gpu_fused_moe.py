@@ -90,3 +90,15 @@ def test_fused_moe_iq3s_graph_replays(dev):
         want = oracle_of(gate, up, down, x, ids, wts, torch.zeros(H, device=dev), H, F)
         assert (got.view(np.uint32) == want.view(np.uint32)).all(), r
         torch.randn(1024, device=dev).sum()   # eager work between replays
+
+
+def test_fused_moe_iq3s_repeated_ids(dev):
+    """Expert ids are taken as given (the reference does no dedup either):
+    a repeated expert contributes once per occurrence, in k order."""
+    H, F, E, K = 1024, 512, 8, 5
+    gate, up, down, x, _, wts, out0 = case(dev, 31, H, F, E, K)
+    ids = torch.tensor([3, 3, 7, 3, 0], dtype=torch.int32, device=dev)
+    out = out0.clone()
+    fused_moe_iq3s(x, gate, up, down, ids, wts, out, H, F, gate.shape[1], up.shape[1], down.shape[1], K)
+    want = oracle_of(gate, up, down, x, ids, wts, out0, H, F)
+    assert (host(out).view(np.uint32) == want.view(np.uint32)).all()
