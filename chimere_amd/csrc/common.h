@@ -373,16 +373,14 @@ __device__ __forceinline__ void wdec_iq3_s_core(uint32_t dbits, uint32_t qs0, ui
 // (as three little-endian words s0, s1, s2) of a Q4_K / Q5_K superblock
 // (gguf_loader.rs:1150-1163): j < 4: sc = b[j] & 63, m = b[j+4] & 63;
 // j >= 4: sc = (b[j+4] & 15) | (b[j-4] >> 6) << 4, m = (b[j+4] >> 4) | (b[j] >> 6) << 4.
+// Branch-free: j varies across the lanes of a wave (a lane's sub-block), so
+// both forms are formed from the same shifted words and one is selected.
 __device__ __forceinline__ void kq_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j, int& sc, int& m) {
-    if (j < 4) {
-        sc = (int)((s0 >> (8 * j)) & 63u);
-        m = (int)((s1 >> (8 * j)) & 63u);
-    } else {
-        const int k = 8 * (j - 4);
-        const uint32_t hi = (s2 >> k) & 0xFFu;
-        sc = (int)((hi & 15u) | (((s0 >> k) & 0xC0u) >> 2));
-        m = (int)((hi >> 4) | (((s1 >> k) & 0xC0u) >> 2));
-    }
+    const int k = 8 * (j & 3);
+    const uint32_t a0 = s0 >> k, a1 = s1 >> k, a2 = s2 >> k;
+    const uint32_t sc_hi = (a2 & 15u) | ((a0 & 0xC0u) >> 2), m_hi = ((a2 >> 4) & 15u) | ((a1 & 0xC0u) >> 2);
+    sc = (int)(j < 4 ? a0 & 63u : sc_hi);
+    m = (int)(j < 4 ? a1 & 63u : m_hi);
 }
 
 // Q4_K superblock (144 B: f16 d, f16 dmin, scales[12], qs[128]) sub-block ib
@@ -411,9 +409,12 @@ __device__ __forceinline__ void wdec_q5_k(const uint8_t* sb, int ib, WBlk& w) {
     const int sh = 4 * (ib & 1);
     const uint32_t* qh = u + 4;
     const uint32_t* qs = u + 12 + 8 * (ib >> 1);
+    // bit ib of each qh byte to bit 4 of the byte: a rotate right by ib - 4
+    // (mod 32) moves bit 8k + ib to bit 8k + 4 without crossing the word
+    const uint32_t rot = (uint32_t)(ib - 4) & 31u;
 #pragma unroll
     for (int i = 0; i < 8; i++)
-        w.v[i] = (int)(((qs[i] >> sh) & 0x0F0F0F0Fu) | (((qh[i] >> ib) & 0x01010101u) << 4));
+        w.v[i] = (int)(((qs[i] >> sh) & 0x0F0F0F0Fu) | (__builtin_amdgcn_alignbit(qh[i], qh[i], rot) & 0x10101010u));
     w.mult2 = 0;
 }
 
