@@ -303,12 +303,17 @@ struct WBlk {
 template <int T>
 __device__ __forceinline__ int wdot(const WBlk& w, const XBlk& x) {
     if constexpr (T == T_Q6_K) {
-        int lo = 0, hi = 0;
+        // w.v holds the unsigned 6-bit quants u (0..63, valid non-negative
+        // int8): sum (u - 32) q_x = sum u q_x - 32 sum q_x per 16-element half
+        int lo = 0, hi = 0, slo = 0;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             lo = dot4(w.v[i], x.q[i], lo);
             hi = dot4(w.v[4 + i], x.q[4 + i], hi);
+            slo = dot4(x.q[i], 0x01010101, slo);
         }
+        lo -= 32 * slo;
+        hi -= 32 * (x.sumq - slo);
         return __mul24(lo, w.mult) + __mul24(hi, w.mult2);   // |.| <= 2 * 16*32*127*128 < 2^24
     }
     int s = 0;
@@ -339,7 +344,7 @@ __device__ __forceinline__ float wacc(const WBlk& w, const XBlk& x, float acc) {
 
 // Q8_1 blocks need the sum of their quants for these weight types
 template <int T>
-constexpr bool needs_sumq() { return T == T_Q4_0 || T == T_Q4_K || T == T_Q5_K; }
+constexpr bool needs_sumq() { return T == T_Q4_0 || T == T_Q4_K || T == T_Q5_K || T == T_Q6_K; }
 
 __device__ __forceinline__ void wdec_q8_0_core(uint32_t dbits, const uint32_t (&q)[8], WBlk& w) {
     w.dw = h2f(dbits);
@@ -422,18 +427,24 @@ __device__ __forceinline__ void wdec_q5_k(const uint8_t* sb, int ib, WBlk& w) {
 // ib = 4*gi + jj (gguf_loader.rs:839-917): element l (0..31) =
 // (nibble (jj >> 1) of ql[64*gi + 32*(jj & 1) + l]) | ((qh[32*gi + l] >> 2*jj) & 3) << 4,
 // minus 32; scale scales[8*gi + 2*jj + l/16].  `row` is a 4-byte aligned
-// buffer, off the superblock's byte offset in it (even).
+// buffer, off the superblock's byte offset in it (even).  w.v holds the
+// unsigned 6-bit values; wdot<T_Q6_K> applies the minus 32.
 __device__ __forceinline__ void wdec_q6_k(const uint8_t* row, int off, int ib, WBlk& w) {
     const int gi = ib >> 2, jj = ib & 3;
     const int lo_off = off + 64 * gi + 32 * (jj & 1), hi_off = off + 128 + 32 * gi;
-    const int nsh = 4 * (jj >> 1), hsh = 2 * jj;
+    // both runs share off's 2-byte phase a: read aligned words; one funnel
+    // shift per word both realigns it and selects the nibble (lo) or the
+    // 2-bit field (hi): bits 8a + shift .. of the word pair.  The quants stay
+    // unsigned (0..63); wdot subtracts 32 per element through the block's sums
+    const uint32_t a8 = 8u * (uint32_t)(off & 3);
+    const uint32_t ls = a8 + 4u * (uint32_t)(jj >> 1), hs = a8 + 2u * (uint32_t)jj;
+    const uint32_t* lw = (const uint32_t*)(row + (lo_off & ~3));
+    const uint32_t* hw = (const uint32_t*)(row + (hi_off & ~3));
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        const uint32_t u = ((lds_u32(row, lo_off + 4 * i) >> nsh) & 0x0F0F0F0Fu) |
-                           (((lds_u32(row, hi_off + 4 * i) >> hsh) & 0x03030303u) << 4);
-        // u - 32 per byte: t = u ^ 0x20 is the 6-bit two's complement, then sign-extend bit 5
-        const uint32_t t = u ^ 0x20202020u, sgn = t & 0x20202020u;
-        w.v[i] = (int)(t | (sgn << 1) | (sgn << 2));
+        const uint32_t lo = __builtin_amdgcn_alignbit(lw[i + 1], lw[i], ls) & 0x0F0F0F0Fu;
+        const uint32_t hx = __builtin_amdgcn_alignbit(hw[i + 1], hw[i], hs);
+        w.v[i] = (int)(lo | ((hx << 4) & 0x30303030u));
     }
     const uint32_t scw = lds_u16(row, off + 192 + 8 * gi + 2 * jj);
     w.mult = (int)(int8_t)(scw & 0xFFu);
