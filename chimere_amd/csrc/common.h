@@ -642,6 +642,44 @@ typedef __attribute__((address_space(1))) void glb_void_t;
 // in flight together; otherwise all pieces are loaded to registers before any
 // is stored.  The caller completes the copy with
 // lds_copy_wait() + __syncthreads().
+// stage_rows for a compile-time geometry: rows [0, n1) from g1 and [n1,
+// nrows) from g2 (global row stride gstride), SEG-byte segments in UNIT-byte
+// pieces (16: global_load_lds_dwordx4, 4: _dword; every piece UNIT-aligned),
+// LDS row stride LSEG >= SEG (the padding is skipped), at most NRMAX rows, NTH
+// threads.  Piece -> (row, column) by constant divisors and the loop fully
+// unrolled, so a wave issues its copies back to back.
+template <int SEG, int LSEG, int UNIT, int NRMAX, int NTH, int CPOL>
+__device__ __forceinline__ void stage_rows_fixed(uint8_t* __restrict__ lds, const uint8_t* g1, int n1,
+                                                 const uint8_t* g2, int64_t gstride, int nrows, int tid) {
+    constexpr int PER = SEG / UNIT, LPER = LSEG / UNIT, NW = NTH / 64;
+    constexpr int IT = (LPER * NRMAX + NTH - 1) / NTH;
+    static_assert((UNIT == 16 || UNIT == 4) && SEG % UNIT == 0 && LSEG % UNIT == 0 && NTH % 64 == 0, "geometry");
+    // lane through an empty asm: the piece addresses are formed here, next
+    // to their copies, instead of being hoisted (registers) out of a caller's
+    // chunk loop
+    int lane = tid & 63;
+    asm volatile("" : "+v"(lane));
+    const int wave = tid >> 6;
+    const unsigned tot = (unsigned)(LPER * nrows);
+    // rows past n1 are g2's (32-bit offsets within a row run: gstride * rows < 2^31)
+    const uintptr_t b2 = (uintptr_t)g2 - (uintptr_t)((int64_t)n1 * gstride);
+    const unsigned gs = (unsigned)gstride;
+#pragma unroll
+    for (int k = 0; k < IT; k++) {
+        const int c0 = (k * NW + wave) * 64;
+        const unsigned c = (unsigned)(c0 + lane);
+        const unsigned r = c / LPER, col = c - r * LPER;
+        if (c < tot && (LPER == PER || col < PER)) {
+            const uintptr_t base = (int)r < n1 ? (uintptr_t)g1 : b2;
+            const uint8_t* src = (const uint8_t*)(base + (r * gs + col * UNIT));
+            if constexpr (UNIT == 16)
+                __builtin_amdgcn_global_load_lds((const glb_void_t*)src, (lds_void_t*)(lds + c0 * 16), 16, 0, CPOL);
+            else
+                __builtin_amdgcn_global_load_lds((const glb_void_t*)src, (lds_void_t*)(lds + c0 * 4), 4, 0, CPOL);
+        }
+    }
+}
+
 template <bool DW = false, int CPOL = 0>
 __device__ __forceinline__ void stage_rows(uint8_t* __restrict__ lds, const uint8_t* __restrict__ g,
                                            int64_t gstride, int nrows, int seg, int tid, int nthreads,

@@ -63,7 +63,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_mmvq(MmvqArgs a) {
         for (int i = tid; i < 512; i += GEMV_THREADS) grid[i] = c_iq3s_grid_mmvq[i];
 
     float acc[1][NTOK];
-    tile_gemv<T, NTOK, TILE_ROWS, 1, CBLK, CPOL_STREAM, PAD>(tile, &xs[0][0], grid,
+    tile_gemv<T, NTOK, TILE_ROWS, 1, CBLK, CPOL_STREAM, PAD, true>(tile, &xs[0][0], grid,
                                      a.W + e * a.w_slot_stride + (int64_t)r0 * rb, nr,
                                      nullptr, 0, rb, a.ncols, a.x + slot * a.x_slot_stride, a.x_tok_stride,
                                      nullptr, a.ntok, acc);

@@ -50,6 +50,112 @@ __device__ __forceinline__ void xlds_to_blk(const XLds& s, XBlk& x) {
     x.sumq = s.sumq;
 }
 
+// The dots of one staged chunk: rows [0, nr) of the tile (LDS row stride
+// lseg) against the chunk's cb decoded activation blocks per token.  KC > 0:
+// a full chunk of a compile-time row stride KC and CBLK blocks (the block loop
+// kept rolled: unrolled it holds more registers and measured slower);
+// CHECK: some of the tile's rows are absent (nr < RG*RPG).
+template <int T, int NT, int RG, int RPG, int CBLK, int KC, bool CHECK>
+__device__ __forceinline__ void tile_compute(const uint8_t* __restrict__ tl, int lseg_rt, int cb_rt,
+                                             const XLds* __restrict__ xs, const uint32_t* __restrict__ grid,
+                                             int nr, int ntok, float (&acc)[RPG][NT]) {
+    const int tid = threadIdx.x;
+    const int g = tid >> 4, j = tid & 15;
+    const int lseg = KC ? KC : lseg_rt, cb = KC ? CBLK : cb_rt;
+    if constexpr (NT == 1) {
+        // one token: the activation block is read once for all RPG rows
+#pragma unroll 1
+        for (int b = j; b < cb; b += SLOTS) {
+            XBlk xb;
+            xlds_to_blk(xs[b], xb);
+#pragma unroll
+            for (int r = 0; r < RPG; r++) {
+                const int row_i = g + RG * r;
+                if (!CHECK || row_i < nr) {
+                    WBlk wb;
+                    block_decode<T>(tl + row_i * lseg, b, grid, wb);
+                    acc[r][0] = wacc<T>(wb, xb, acc[r][0]);
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < RPG; r++) {
+            const int row_i = g + RG * r;
+            if (!CHECK || row_i < nr) {
+                const uint8_t* row = tl + row_i * lseg;
+#pragma unroll 1
+                for (int b = j; b < cb; b += SLOTS) {
+                    WBlk wb;   // decoded once, used for every token
+                    block_decode<T>(row, b, grid, wb);
+#pragma unroll
+                    for (int t = 0; t < NT; t++) {
+                        if (t < ntok) {
+                            XBlk xb;
+                            xlds_to_blk(xs[t * CBLK + b], xb);
+                            acc[r][t] = wacc<T>(wb, xb, acc[r][t]);
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+// One K chunk of tile_gemv (below): blocks [b0, b0 + cb) of the tile's rows.
+// FAST: a full chunk (cb == CBLK) with 16-byte aligned pieces, staged by
+// stage_rows_fixed (the copies issued back to back) and computed with a
+// compile-time row stride and block count; otherwise the general path.
+template <int T, int NT, int RG, int RPG, int CBLK, int CPOL, int PAD, bool FAST>
+__device__ __forceinline__ void tile_chunk(uint8_t* __restrict__ tile, XLds* __restrict__ xs,
+                                           const uint32_t* __restrict__ grid, const uint8_t* base1, int n1,
+                                           const uint8_t* base2, int n2, int64_t rb, int b0, int cb,
+                                           const uint8_t* __restrict__ X, int64_t x_tok_stride, const int* toks,
+                                           int ntok, float (&acc)[RPG][NT]) {
+    constexpr int NTH = RG * SLOTS;
+    constexpr int CB = chunk_bytes<T>(CBLK);
+    const int tid = threadIdx.x;
+    const int nr = n1 + n2;
+    const int seg = chunk_bytes<T>(cb);
+    const int64_t goff = (int64_t)b0 / (QTraits<T>::ELEMS / QK) * QTraits<T>::BYTES;
+    // LDS row stride: seg (== CB except in a ragged last chunk), + PAD for
+    // 16-byte pieces from 16-byte aligned rows (always so on the FAST path)
+    const int lseg = PAD && (FAST || (((seg | goff) & 15) == 0 &&
+                                      (((uintptr_t)base1 | (uintptr_t)rb | (uintptr_t)tile) & 15) == 0 &&
+                                      (n2 == 0 || ((uintptr_t)base2 & 15) == 0)))
+                         ? seg + PAD
+                         : seg;
+    __syncthreads();   // previous users of tile / xs are done
+    if constexpr (FAST) {
+        static_assert(CB % 16 == 0, "16-byte pieces");
+        stage_rows_fixed<CB, CB + PAD, 16, RG * RPG, NTH, CPOL>(tile, base1 + goff, n1, base2 + goff, rb, nr, tid);
+    } else {
+        if (n1) stage_rows<stage_dw<T>(), CPOL>(tile, base1 + goff, rb, n1, seg, tid, NTH, lseg);
+        if (n2) stage_rows<stage_dw<T>(), CPOL>(tile + n1 * lseg, base2 + goff, rb, n2, seg, tid, NTH, lseg);
+    }
+    for (int i = tid; i < ntok * cb; i += NTH) {
+        const int t = i / cb, b = i - t * cb;
+        const int tk = toks ? toks[t] : t;
+        XBlk xb;
+        load_xblk(X + tk * x_tok_stride + (int64_t)(b0 + b) * Q8_1_BYTES, xb);
+        XLds& o = xs[t * CBLK + b];
+#pragma unroll
+        for (int k = 0; k < 8; k++) o.q[k] = xb.q[k];
+        o.d = xb.d;
+        o.sumq = T == T_Q4_0S ? (int)xb.sbits : xb.sumq;   // the s-form needs s, not the quant sum
+    }
+    lds_copy_wait();
+    __syncthreads();
+    if constexpr (FAST) {
+        if (nr == RG * RPG)
+            tile_compute<T, NT, RG, RPG, CBLK, CB + PAD, false>(tile, 0, 0, xs, grid, nr, ntok, acc);
+        else
+            tile_compute<T, NT, RG, RPG, CBLK, CB + PAD, true>(tile, 0, 0, xs, grid, nr, ntok, acc);
+    } else {
+        tile_compute<T, NT, RG, RPG, CBLK, 0, true>(tile, lseg, cb, xs, grid, nr, ntok, acc);
+    }
+}
+
 // Accumulates per-lane partial dots for the rows of a tile against up to NT
 // tokens.  Tile rows [0, n1) come from base1, rows [n1, n1+n2) from base2
 // (global row stride rb for both); n1 + n2 <= RG*RPG.  Token i's Q8_1 row is
@@ -63,87 +169,35 @@ __device__ __forceinline__ void xlds_to_blk(const XLds& s, XBlk& x) {
 // PAD: bytes added to the LDS row stride of 16-byte multiple chunk rows, so
 // that the rows a wave reads at once start on different banks (the tile
 // buffer then needs rows * (chunk bytes + PAD))
-template <int T, int NT, int RG, int RPG, int CBLK = ChunkGeom<T>::BLOCKS, int CPOL = 0, int PAD = 0>
+// FIX: full 16-byte aligned chunks on tile_chunk's FAST path (measured
+// faster for the standalone GEMV, slower -- more registers -- in the MoE
+// kernels' tiles)
+template <int T, int NT, int RG, int RPG, int CBLK = ChunkGeom<T>::BLOCKS, int CPOL = 0, int PAD = 0,
+          bool FIX = false>
 __device__ __forceinline__ void tile_gemv(uint8_t* __restrict__ tile, XLds* __restrict__ xs,
                                           const uint32_t* __restrict__ grid,
                                           const uint8_t* base1, int n1, const uint8_t* base2, int n2,
                                           int64_t rb, int ncols, const uint8_t* __restrict__ X,
                                           int64_t x_tok_stride, const int* toks, int ntok,
                                           float (&acc)[RPG][NT]) {
-    constexpr int NTH = RG * SLOTS;
     static_assert(CBLK % SLOTS == 0 && (QTraits<T>::ELEMS != 256 || CBLK % 8 == 0) && CBLK <= MAX_CHUNK_BLOCKS, "chunk");
-    const int tid = threadIdx.x;
-    const int g = tid >> 4, j = tid & 15;
-    const int nr = n1 + n2;
     const int nb = ncols / QK;
 #pragma unroll
     for (int r = 0; r < RPG; r++)
 #pragma unroll
         for (int t = 0; t < NT; t++) acc[r][t] = 0.0f;
+    constexpr bool FIXOK = FIX && chunk_bytes<T>(CBLK) % 16 == 0;
+    const bool al16 = (((uintptr_t)base1 | (uintptr_t)rb | (uintptr_t)tile) & 15) == 0 &&
+                      (n2 == 0 || ((uintptr_t)base2 & 15) == 0);
     for (int b0 = 0; b0 < nb; b0 += CBLK) {
-        const int cb = min(CBLK, nb - b0);
-        const int seg = chunk_bytes<T>(cb);
-        const int64_t goff = (int64_t)b0 / (QTraits<T>::ELEMS / QK) * QTraits<T>::BYTES;
-        // LDS row stride: seg (== CB except in a ragged last chunk), + PAD for
-        // 16-byte pieces from 16-byte aligned rows
-        const int lseg = PAD && ((seg | goff) & 15) == 0 &&
-                                 (((uintptr_t)base1 | (uintptr_t)rb | (uintptr_t)tile) & 15) == 0 &&
-                                 (n2 == 0 || ((uintptr_t)base2 & 15) == 0)
-                             ? seg + PAD
-                             : seg;
-        __syncthreads();   // previous users of tile / xs are done
-        if (n1) stage_rows<stage_dw<T>(), CPOL>(tile, base1 + goff, rb, n1, seg, tid, NTH, lseg);
-        if (n2) stage_rows<stage_dw<T>(), CPOL>(tile + n1 * lseg, base2 + goff, rb, n2, seg, tid, NTH, lseg);
-        for (int i = tid; i < ntok * cb; i += NTH) {
-            const int t = i / cb, b = i - t * cb;
-            const int tk = toks ? toks[t] : t;
-            XBlk xb;
-            load_xblk(X + tk * x_tok_stride + (int64_t)(b0 + b) * Q8_1_BYTES, xb);
-            XLds& o = xs[t * CBLK + b];
-#pragma unroll
-            for (int k = 0; k < 8; k++) o.q[k] = xb.q[k];
-            o.d = xb.d;
-            o.sumq = T == T_Q4_0S ? (int)xb.sbits : xb.sumq;   // the s-form needs s, not the quant sum
-        }
-        lds_copy_wait();
-        __syncthreads();
-        const uint8_t* tl = tile;
-        if constexpr (NT == 1) {
-            // one token: the activation block is read once for all RPG rows
-            for (int b = j; b < cb; b += SLOTS) {
-                XBlk xb;
-                xlds_to_blk(xs[b], xb);
-#pragma unroll
-                for (int r = 0; r < RPG; r++) {
-                    const int row_i = g + RG * r;
-                    if (row_i < nr) {
-                        WBlk wb;
-                        block_decode<T>(tl + row_i * lseg, b, grid, wb);
-                        acc[r][0] = wacc<T>(wb, xb, acc[r][0]);
-                    }
-                }
-            }
-        } else {
-#pragma unroll
-            for (int r = 0; r < RPG; r++) {
-                const int row_i = g + RG * r;
-                if (row_i < nr) {
-                    const uint8_t* row = tl + row_i * lseg;
-                    for (int b = j; b < cb; b += SLOTS) {
-                        WBlk wb;   // decoded once, used for every token
-                        block_decode<T>(row, b, grid, wb);
-#pragma unroll
-                        for (int t = 0; t < NT; t++) {
-                            if (t < ntok) {
-                                XBlk xb;
-                                xlds_to_blk(xs[t * CBLK + b], xb);
-                                acc[r][t] = wacc<T>(wb, xb, acc[r][t]);
-                            }
-                        }
-                    }
-                }
-            }
-        }
+        // chunk offsets are multiples of the (16-byte multiple) chunk bytes
+        if (FIXOK && al16 && nb - b0 >= CBLK)
+            tile_chunk<T, NT, RG, RPG, CBLK, CPOL, PAD, FIXOK>(tile, xs, grid, base1, n1, base2, n2, rb, b0, CBLK, X,
+                                                               x_tok_stride, toks, ntok, acc);
+        else
+            tile_chunk<T, NT, RG, RPG, CBLK, CPOL, PAD, false>(tile, xs, grid, base1, n1, base2, n2, rb, b0,
+                                                               min(CBLK, nb - b0), X, x_tok_stride, toks, ntok,
+                                                               acc);
     }
 }
 
