@@ -88,11 +88,13 @@ def test_gemv_bit_exact(dev, t, nrows, ncols):
 
 
 @pytest.mark.parametrize("t", [O.Q8_0, O.Q4_0, O.IQ3_S])
-def test_gemv_batched_by_expert_ids(dev, t):
+@pytest.mark.parametrize("H", [1024, 2048])
+def test_gemv_batched_by_expert_ids(dev, t, H):
     """ggml_gpu_cuda.cu:243-279 semantics: slot k uses expert ids[k] and input
-    k*input_stride (0 = shared)."""
+    k*input_stride (0 = shared).  H=2048: whole 64-block chunks (the GEMV's
+    compile-time chunk path); H=1024: a partial chunk."""
     rng = np.random.default_rng(70 + t)
-    E, F, H, K = 12, 64, 1024, 5
+    E, F, K = 12, 64, 5
     w = O.quantize(t, rng.normal(0, 0.02, (E * F, H)).astype(np.float32)).reshape(E, -1)
     xs = rng.standard_normal((K, H)).astype(np.float32)
     xq = O.quantize_q8_1(xs)                        # [K, row bytes]
