@@ -534,11 +534,17 @@ __device__ __forceinline__ void pf_mma_chunk(const uint8_t* xl, int xr, const fl
                     acc[n][2] = __builtin_fmaf(-(mnp[n].dm * dxp.z), (float)__mul24(mnp[n].m, sqp.z), acc[n][2]);
                     acc[n][3] = __builtin_fmaf(-(mnp[n].dm * dxp.w), (float)__mul24(mnp[n].m, sqp.w), acc[n][3]);
                 }
+                // the block's rescale stays in its iteration: without this the
+                // fmas of the unrolled blocks sink below all of their matrix
+                // products, which then hold 36 more registers
+                asm volatile("" : "+v"(acc[n][0]), "+v"(acc[n][1]), "+v"(acc[n][2]), "+v"(acc[n][3]));
             }
         }
 #pragma unroll
         for (int n = 0; n < NTN; n++) { rp[n] = r[n]; rp2[n] = r2[n]; dwp[n] = dw[n]; mup[n] = mu[n]; mnp[n] = mn[n]; }
         dxp = dx;
+        // nor do the scheduler's clusters of matrix products span blocks
+        __builtin_amdgcn_sched_barrier(0);
         if constexpr (pf_kq<T>()) {
             // sum q_x = -(xs8 / 8) of the block just issued (xs8 = -8 * sum q_x)
             if (b < nb) {
