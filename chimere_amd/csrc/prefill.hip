@@ -716,18 +716,22 @@ constexpr int pf_ws0(int nrows) { return pf_wst<TE>(nrows) > pf_wst<TS>(nrows) ?
 template <int TE, int TS>
 constexpr int pf_ws1(int nrows) { return pf_sh_one<TE, TS>() ? pf_wst<TE>(nrows) : pf_ws0<TE, TS>(nrows); }
 
-// Rows per gate_up work-group: PF_GU_NTN 16-row tiles per wave, half the
-// waves on gate rows and half on the same up rows
-constexpr int PF_GU_NTN = 2;   // 64-row work-groups (one tile per wave) measured slower
-constexpr int PF_GU_ROWS = 32 * PF_GU_NTN;   // gate (and up) rows per work-group
+// Rows per gate_up work-group: pf_gu_ntn 16-row tiles per wave, half the
+// waves on gate rows and half on the same up rows.  IQ3_S experts: one tile
+// per wave (64-row work-groups, 30-40 KB of LDS: four work-groups per CU;
+// 512-token chunk 365 -> 354 us); the others two (measured alike or better).
+template <int TE>
+constexpr int pf_gu_ntn() { return TE == T_IQ3_S ? 1 : 2; }
+template <int TE>
+constexpr int pf_gu_rows() { return 32 * pf_gu_ntn<TE>(); }   // gate (and up) rows per work-group
 
-// P4: grid (F/PF_GU_ROWS, max_tiles).  Waves 0, 1: gate and up rows f0 +
+// P4: grid (F/pf_gu_rows, max_tiles).  Waves 0, 1: gate and up rows f0 +
 // [0, 16*NTN); waves 2, 3: the same for the next 16*NTN rows (NTN 16-row
 // tiles per wave); then h = silu(gate) * up and Q8_1 of its 32-row blocks per
 // pair.
 template <int TE, int TS>
 __global__ __launch_bounds__(PF_THREADS) void k_pf_gate_up(PfArgs a) {
-    constexpr int NTN = PF_GU_NTN, R = PF_GU_ROWS;
+    constexpr int NTN = pf_gu_ntn<TE>(), R = pf_gu_rows<TE>();
     constexpr int WS = pf_ws0<TE, TS>(2 * R);
     PF_STAGE_ARRAYS(WS, (pf_ws1<TE, TS>(2 * R)));
     __shared__ int prs[PF_TILE], xrows[PF_TILE];
@@ -908,7 +912,7 @@ static void launch_pf(const PfArgs& a, const PfPlan& p, hipStream_t s) {
     launch_quantize_q8_1(a.x, a.xq, a.H, p.xq_stride / Q8_1_BYTES * QK, a.T, s);
     hipLaunchKernelGGL(k_pf_topk, dim3(a.T), dim3(64), 0, s, a);
     hipLaunchKernelGGL(k_pf_plan, dim3(1), dim3(1024), 0, s, a);
-    hipLaunchKernelGGL((k_pf_gate_up<TE, TS>), dim3(a.F / PF_GU_ROWS, p.max_tiles), dim3(PF_THREADS), 0, s, a);
+    hipLaunchKernelGGL((k_pf_gate_up<TE, TS>), dim3(a.F / pf_gu_rows<TE>(), p.max_tiles), dim3(PF_THREADS), 0, s, a);
     hipLaunchKernelGGL((k_pf_down<TE, TS>), dim3(a.H / 128, p.max_tiles), dim3(PF_THREADS), 0, s, a);
     hipLaunchKernelGGL(k_pf_combine, dim3((a.H / 4 + 255) / 256, a.T), dim3(256), 0, s, a);
 }
