@@ -789,11 +789,19 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_gate_up(PfArgs a) {
     }
 }
 
-// P5: grid (H/128, max_tiles).  Wave w: down rows r0 + 32w .. +31 (two
+// 16-row tiles per wave of k_pf_down (64 * ntn rows per work-group): IQ3_S
+// experts one (four work-groups per CU; 512-token chunk -5 us), the others
+// two (alike)
+template <int TE>
+constexpr int pf_dn_ntn() { return TE == T_IQ3_S ? 1 : 2; }
+
+// P5: grid (H/DR, max_tiles), DR = 128 (IQ3_S experts: 64, one 16-row tile
+// per wave).  DR = 128: wave w: down rows r0 + 32w .. +31 (two
 // 16-row tiles) for the tile's 16 pairs; K = F.
 template <int TE, int TS>
 __global__ __launch_bounds__(PF_THREADS) void k_pf_down(PfArgs a) {
-    PF_STAGE_ARRAYS((pf_ws0<TE, TS>(128)), (pf_ws1<TE, TS>(128)));
+    constexpr int NTN = pf_dn_ntn<TE>(), DR = 64 * NTN;
+    PF_STAGE_ARRAYS((pf_ws0<TE, TS>(DR)), (pf_ws1<TE, TS>(DR)));
     __shared__ int prs[PF_TILE];
     __shared__ uint32_t grid[(TE == T_IQ3_S || TS == T_IQ3_S) ? 512 : 1];
     const int ti = blockIdx.y;
@@ -805,8 +813,8 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_down(PfArgs a) {
         for (int i = tid; i < 512; i += PF_THREADS) grid[i] = c_iq3s_grid_pf[i];
     __syncthreads();
     const bool sh = e == a.E;
-    const int r0 = blockIdx.x * 128, wave = tid >> 6;
-    float acc[2][4];
+    const int r0 = blockIdx.x * DR, wave = tid >> 6;
+    float acc[NTN][4];
     auto run = [&](auto tag) {
         constexpr int T = decltype(tag)::value;
         const int64_t rb = row_bytes(T, a.F);
@@ -814,7 +822,7 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_down(PfArgs a) {
         // IQ3_S / Q6_K down rows (F / 256 superblocks of 110 / 210 bytes) are
         // 16-byte aligned only when F is a multiple of 2048: one stage
         constexpr bool two = T != T_IQ3_S && T != T_Q6_K && !(T == TS && pf_sh_one<TE, TS>());
-        pf_gemm<T, 2, 128, two>(s0, s1, d + r0 * rb, 128, d, rb, a.F / QK, a.hq, prs, a.hq_stride, wave * 32, grid,
+        pf_gemm<T, NTN, DR, two>(s0, s1, d + r0 * rb, DR, d, rb, a.F / QK, a.hq, prs, a.hq_stride, wave * 16 * NTN, grid,
                                 acc);
     };
     if constexpr (TE == TS) run(std::integral_constant<int, TE>{});   // one instance of the K loop
@@ -822,11 +830,11 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_down(PfArgs a) {
     else run(std::integral_constant<int, TS>{});
     const int lane = tid & 63, q = lane >> 4, c = lane & 15;
 #pragma unroll
-    for (int nn = 0; nn < 2; nn++)
+    for (int nn = 0; nn < NTN; nn++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int m = 4 * q + i;
-            if (m < n) a.dn[(int64_t)prs[m] * a.H + r0 + wave * 32 + 16 * nn + c] = acc[nn][i];
+            if (m < n) a.dn[(int64_t)prs[m] * a.H + r0 + wave * 16 * NTN + 16 * nn + c] = acc[nn][i];
         }
 }
 
@@ -913,7 +921,7 @@ static void launch_pf(const PfArgs& a, const PfPlan& p, hipStream_t s) {
     hipLaunchKernelGGL(k_pf_topk, dim3(a.T), dim3(64), 0, s, a);
     hipLaunchKernelGGL(k_pf_plan, dim3(1), dim3(1024), 0, s, a);
     hipLaunchKernelGGL((k_pf_gate_up<TE, TS>), dim3(a.F / pf_gu_rows<TE>(), p.max_tiles), dim3(PF_THREADS), 0, s, a);
-    hipLaunchKernelGGL((k_pf_down<TE, TS>), dim3(a.H / 128, p.max_tiles), dim3(PF_THREADS), 0, s, a);
+    hipLaunchKernelGGL((k_pf_down<TE, TS>), dim3(a.H / (64 * pf_dn_ntn<TE>()), p.max_tiles), dim3(PF_THREADS), 0, s, a);
     hipLaunchKernelGGL(k_pf_combine, dim3((a.H / 4 + 255) / 256, a.T), dim3(256), 0, s, a);
 }
 
