@@ -647,8 +647,9 @@ typedef __attribute__((address_space(1))) void glb_void_t;
 // pieces (16: global_load_lds_dwordx4, 4: _dword; every piece UNIT-aligned),
 // LDS row stride LSEG >= SEG (the padding is skipped), at most NRMAX rows, NTH
 // threads.  Piece -> (row, column) by constant divisors and the loop fully
-// unrolled, so a wave issues its copies back to back.
-template <int SEG, int LSEG, int UNIT, int NRMAX, int NTH, int CPOL>
+// unrolled, so a wave issues its copies back to back.  ONE: every row is g1's
+// (n1 == nrows): each copy is the uniform base plus a 32-bit lane offset.
+template <int SEG, int LSEG, int UNIT, int NRMAX, int NTH, int CPOL, bool ONE = false>
 __device__ __forceinline__ void stage_rows_fixed(uint8_t* __restrict__ lds, const uint8_t* g1, int n1,
                                                  const uint8_t* g2, int64_t gstride, int nrows, int tid) {
     constexpr int PER = SEG / UNIT, LPER = LSEG / UNIT, NW = NTH / 64;
@@ -662,7 +663,7 @@ __device__ __forceinline__ void stage_rows_fixed(uint8_t* __restrict__ lds, cons
     const int wave = tid >> 6;
     const unsigned tot = (unsigned)(LPER * nrows);
     // rows past n1 are g2's (32-bit offsets within a row run: gstride * rows < 2^31)
-    const uintptr_t b2 = (uintptr_t)g2 - (uintptr_t)((int64_t)n1 * gstride);
+    const uintptr_t b2 = ONE ? 0 : (uintptr_t)g2 - (uintptr_t)((int64_t)n1 * gstride);
     const unsigned gs = (unsigned)gstride;
 #pragma unroll
     for (int k = 0; k < IT; k++) {
@@ -670,8 +671,8 @@ __device__ __forceinline__ void stage_rows_fixed(uint8_t* __restrict__ lds, cons
         const unsigned c = (unsigned)(c0 + lane);
         const unsigned r = c / LPER, col = c - r * LPER;
         if (c < tot && (LPER == PER || col < PER)) {
-            const uintptr_t base = (int)r < n1 ? (uintptr_t)g1 : b2;
-            const uint8_t* src = (const uint8_t*)(base + (r * gs + col * UNIT));
+            const unsigned off = r * gs + col * UNIT;
+            const uint8_t* src = ONE ? g1 + off : (const uint8_t*)(((int)r < n1 ? (uintptr_t)g1 : b2) + off);
             if constexpr (UNIT == 16)
                 __builtin_amdgcn_global_load_lds((const glb_void_t*)src, (lds_void_t*)(lds + c0 * 16), 16, 0, CPOL);
             else

@@ -128,7 +128,10 @@ __device__ __forceinline__ void tile_chunk(uint8_t* __restrict__ tile, XLds* __r
     __syncthreads();   // previous users of tile / xs are done
     if constexpr (FAST) {
         static_assert(CB % 16 == 0, "16-byte pieces");
-        stage_rows_fixed<CB, CB + PAD, 16, RG * RPG, NTH, CPOL>(tile, base1 + goff, n1, base2 + goff, rb, nr, tid);
+        if (n2 == 0)
+            stage_rows_fixed<CB, CB + PAD, 16, RG * RPG, NTH, CPOL, true>(tile, base1 + goff, n1, nullptr, rb, nr, tid);
+        else
+            stage_rows_fixed<CB, CB + PAD, 16, RG * RPG, NTH, CPOL>(tile, base1 + goff, n1, base2 + goff, rb, nr, tid);
     } else {
         if (n1) stage_rows<stage_dw<T>(), CPOL>(tile, base1 + goff, rb, n1, seg, tid, NTH, lseg);
         if (n2) stage_rows<stage_dw<T>(), CPOL>(tile + n1 * lseg, base2 + goff, rb, n2, seg, tid, NTH, lseg);
