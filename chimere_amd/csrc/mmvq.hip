@@ -78,9 +78,69 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_mmvq(MmvqArgs a) {
     }
 }
 
+// One token, rows of exactly NCH 64-block chunks (2048 * NCH columns), whole
+// 16-row tiles, 16-byte aligned rows: the tile's copies, the activation
+// blocks, the dots and the L=16 tree with compile-time sizes and a
+// compile-time chunk count (the same fp32 order as tile_gemv; the general
+// path's run-time row count and chunk loop cost ~0.35 us of latency per
+// launch: Q8_0 4096x2048 4.24 -> 3.90 us, Q4_0 head 30.8 -> 28.6 us).
+template <int T, int NCH>
+__global__ __launch_bounds__(GEMV_THREADS) void k_mmvq_nc(MmvqArgs a) {
+    constexpr int CBLK = MMVQ_BLOCKS, CB = chunk_bytes<T>(CBLK), LS = CB + mmvq_pad<T>();
+    static_assert(CB % 16 == 0, "16-byte pieces");
+    __shared__ __attribute__((aligned(16))) uint8_t tile[TILE_ROWS * LS + 16];
+    __shared__ XLds xs[CBLK];
+    __shared__ uint32_t grid[T == T_IQ3_S ? 512 : 1];
+    const int tid = threadIdx.x, g = tid >> 4, j = tid & 15;
+    const int slot = blockIdx.y;
+    const int64_t e = a.ids ? (int64_t)a.ids[slot] : (int64_t)slot;
+    constexpr int64_t RB = (int64_t)NCH * CB;
+    const uint8_t* W = a.W + e * a.w_slot_stride + (int64_t)blockIdx.x * TILE_ROWS * RB;
+    const uint8_t* X = a.x + slot * a.x_slot_stride;
+    if constexpr (T == T_IQ3_S)
+        for (int i = tid; i < 512; i += GEMV_THREADS) grid[i] = c_iq3s_grid_mmvq[i];
+    float acc = 0.0f;
+#pragma unroll 1
+    for (int c = 0; c < NCH; c++) {
+        if (c > 0) __syncthreads();   // every wave is done with the previous chunk
+        stage_rows_fixed<CB, LS, 16, TILE_ROWS, GEMV_THREADS, CPOL_STREAM, true>(tile, W + c * CB, TILE_ROWS, nullptr,
+                                                                                  RB, TILE_ROWS, tid);
+        if (tid < CBLK) {
+            XBlk xb;
+            load_xblk(X + (int64_t)(c * CBLK + tid) * Q8_1_BYTES, xb);
+            XLds& o = xs[tid];
+#pragma unroll
+            for (int k = 0; k < 8; k++) o.q[k] = xb.q[k];
+            o.d = xb.d;
+            o.sumq = T == T_Q4_0S ? (int)xb.sbits : xb.sumq;
+        }
+        lds_copy_wait();
+        __syncthreads();
+#pragma unroll 1
+        for (int b = j; b < CBLK; b += SLOTS) {
+            XBlk xb;
+            xlds_to_blk(xs[b], xb);
+            WBlk wb;
+            block_decode<T>(tile + g * LS, b, grid, wb);
+            acc = wacc<T>(wb, xb, acc);
+        }
+    }
+    const float v = slot_reduce16(acc);
+    if (j == 0) a.y[slot * a.y_slot_stride + blockIdx.x * TILE_ROWS + g] = v;
+}
+
 template <int T>
 static void launch_t(const MmvqArgs& a, int nslots, hipStream_t s) {
     dim3 grid((unsigned)((a.nrows + TILE_ROWS - 1) / TILE_ROWS), (unsigned)nslots);
+    if constexpr (chunk_bytes<T>(MMVQ_BLOCKS) % 16 == 0) {
+        const int nch = a.ncols / (MMVQ_BLOCKS * QK);
+        if (a.ntok == 1 && a.ncols % (MMVQ_BLOCKS * QK) == 0 && (nch == 1 || nch == 2) && a.nrows % TILE_ROWS == 0 &&
+            (((uintptr_t)a.W | (uintptr_t)a.w_slot_stride) & 15) == 0) {
+            if (nch == 1) hipLaunchKernelGGL((k_mmvq_nc<T, 1>), grid, dim3(GEMV_THREADS), 0, s, a);
+            else hipLaunchKernelGGL((k_mmvq_nc<T, 2>), grid, dim3(GEMV_THREADS), 0, s, a);
+            return;
+        }
+    }
     dim3 blk(GEMV_THREADS);
     switch (a.ntok) {
 #define CASE(N) case N: hipLaunchKernelGGL((k_mmvq<T, N>), grid, blk, 0, s, a); break;

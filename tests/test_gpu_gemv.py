@@ -58,7 +58,7 @@ def _case(t, nrows, ncols, seed):
     return w, x, O.quantize_q8_1(x)
 
 
-SHAPES = [(4096, 2048), (37, 2048), (512, 2048), (2048, 512), (300, 8192), (16, 256)]
+SHAPES = [(4096, 2048), (37, 2048), (512, 2048), (2048, 512), (300, 8192), (16, 256), (256, 4096)]
 
 
 @pytest.mark.parametrize("t", [O.Q8_0, O.Q4_0, O.IQ3_S])
@@ -177,7 +177,7 @@ def test_q4_0_head_full_size(dev):
 
 KQ_FN = {O.Q4_K: ("chimere_mmvq_q4k", "chimere_mmvq_q4k_f32"), O.Q5_K: ("chimere_mmvq_q5k", "chimere_mmvq_q5k_f32"),
          O.Q6_K: ("chimere_mmvq_q6k", "chimere_mmvq_q6k_f32"), O.MXFP4: ("chimere_mmvq_mxfp4", None)}
-KQ_SHAPES = [(4096, 2048), (37, 2304), (300, 4096), (16, 256)]
+KQ_SHAPES = [(4096, 2048), (37, 2304), (300, 4096), (16, 256), (512, 4096)]
 
 
 @pytest.mark.parametrize("t,nrows,ncols", [(t, r, c) for r, c in KQ_SHAPES for t in (O.Q4_K, O.Q5_K, O.Q6_K, O.MXFP4)]
