@@ -515,15 +515,15 @@ __device__ __forceinline__ float e1_dots(const uint8_t* buf, int pre, const XLds
 
 // The item: gate/up rows [32w, 32w+32) of one expert, h block w, and its down
 // terms (lane_acc[pair][w][r], F <= 512).
-template <int T>
+template <int T, int HC>
 __device__ __forceinline__ void e1_item(const MoeArgs& a, uint8_t* bufA, uint8_t* bufB, const XLds* xs,
                                         const uint32_t* grid, float (*hg)[QK], float (*hu)[QK], int pair, int w,
                                         const uint8_t* gate, const uint8_t* up) {
     constexpr int CBLK = e1_cblk<T>();
     const int tid = threadIdx.x;
-    const int nbH = a.H / QK;
+    const int nbH = (HC ? HC : a.H) / QK;
     const int nc = (nbH + CBLK - 1) / CBLK;
-    const int64_t rb = row_bytes(T, a.H);
+    const int64_t rb = row_bytes(T, nbH * QK);
     gate += (int64_t)w * QK * rb;
     up += (int64_t)w * QK * rb;
     int preA = e1_issue<T>(bufA, gate, up, rb, 0, nbH), preB = 0;
@@ -603,7 +603,9 @@ __device__ __forceinline__ void e1_prefetch(const E1Prefetch& p, const int* uexp
     if (p.K < 0) *p.sink_dst = (int)sink;   // never taken: keeps the loads
 }
 
-template <int TE, int TS>
+// HC / FC: H and F as compile-time constants (0: the run-time a.H / a.F);
+// the shapes of the reference model run an instance with both fixed.
+template <int TE, int TS, int HC = 0, int FC = 0>
 __global__ __launch_bounds__(EX_THREADS) void k_moe_expert1(MoeArgs a) {
     constexpr int CB = e1_stride<TE>() > e1_stride<TS>() ? e1_stride<TE>() : e1_stride<TS>();
     // + 16: lds_u32 of a row's last block reads up to 4 bytes past the row
@@ -616,7 +618,8 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert1(MoeArgs a) {
     __shared__ float s_w[MAX_K];
     __shared__ uint64_t s_tk[128];
     const int tid = threadIdx.x, wave = tid >> 6;
-    const int NB = a.F / QK, nbH = a.H / QK;
+    const int Hs = HC ? HC : a.H, Fs = FC ? FC : a.F;
+    const int NB = Fs / QK, nbH = Hs / QK;
     const int x = blockIdx.x & 7, lb = blockIdx.x >> 3, G8 = gridDim.x >> 3;
     // items of XCD x (work-group ids are dealt round-robin to the 8 XCDs): the
     // row blocks of the routed unit x (the x-th selected expert), then the
@@ -655,7 +658,7 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert1(MoeArgs a) {
             const int nh = G8 - nx, hb = lb - nx;
             E1Prefetch p;
             p.down = a.down; p.sh_down = a.sh_down; p.sd = a.sd;
-            p.mb = (int64_t)a.H * row_bytes(TE, a.F); p.sb = (int64_t)a.H * row_bytes(TS, a.F);
+            p.mb = (int64_t)Hs * row_bytes(TE, Fs); p.sb = (int64_t)Hs * row_bytes(TS, Fs);
             p.K = a.K; p.has_shared = a.has_shared;
             p.sink_dst = a.plan;
             {   // start the down-row loads once the items' gate/up copies are
@@ -669,7 +672,7 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert1(MoeArgs a) {
             return;
         }
         const int e = s_ids[x];
-        e1_item<TE>(a, bufA, bufB, xs, grid, hg, hu, x, lb, a.gate + e * a.sg, a.up + e * a.su);
+        e1_item<TE, HC>(a, bufA, bufB, xs, grid, hg, hu, x, lb, a.gate + e * a.sg, a.up + e * a.su);
     } else {
         for (int i = tid; i < nbH; i += EX_THREADS) {
             XBlk xb;
@@ -678,7 +681,7 @@ __global__ __launch_bounds__(EX_THREADS) void k_moe_expert1(MoeArgs a) {
 #pragma unroll
             for (int k = 0; k < 8; k++) xs[i].q[k] = xb.q[k];
         }
-        e1_item<TS>(a, bufA, bufB, xs, grid, hg, hu, a.K, x + 8 * (lb - nr * NB), a.sh_gate, a.sh_up);
+        e1_item<TS, HC>(a, bufA, bufB, xs, grid, hg, hu, a.K, x + 8 * (lb - nr * NB), a.sh_gate, a.sh_up);
     }
 }
 
@@ -1354,7 +1357,11 @@ static void launch_layer_nt(const MoeArgs& a, int stage, hipStream_t s) {
                   (TS == T_Q4_0 || TS == T_Q8_0 || TS == T_IQ3_S || TS == T_Q4_K || TS == T_Q5_K)) {
         if (expert1_fits(a, TE, TS)) {
             if (stage < 0 || stage == 1)
-                hipLaunchKernelGGL((k_moe_expert1<TE, TS>), dim3(expert_grid(256)), dim3(EX_THREADS), 0, s, a);
+                if (a.H == 2048 && a.F == 512)
+                    hipLaunchKernelGGL((k_moe_expert1<TE, TS, 2048, 512>), dim3(expert_grid(256)), dim3(EX_THREADS), 0,
+                                       s, a);
+                else
+                    hipLaunchKernelGGL((k_moe_expert1<TE, TS>), dim3(expert_grid(256)), dim3(EX_THREADS), 0, s, a);
             if (stage < 0 || stage == 2)
                 hipLaunchKernelGGL((k_moe_dc1<TE, TS>), dim3(a.H / DC1_ROWS), dim3((a.K + a.has_shared + 1) * 64), 0,
                                    s, a);
