@@ -81,8 +81,10 @@ struct Plan {
 // K1: grid (E + has_gate) * TS work-groups (router rows, then the
 // shared-expert gate row; TS work-groups per row, each for NT of the tokens)
 // + the x quantizers.
-template <int NT, int TS = 1>
+// HC: H as a compile-time constant (0: the run-time a.H)
+template <int NT, int TS = 1, int HC = 0>
 __global__ __launch_bounds__(256) void k_moe_route(MoeArgs a) {
+    const int H = HC ? HC : a.H;
     __shared__ float red[NT * 256];
     const int ng = a.sh_gate_w ? 1 : 0;
     const int nrw = (a.E + ng) * TS;
@@ -91,9 +93,9 @@ __global__ __launch_bounds__(256) void k_moe_route(MoeArgs a) {
     if (row >= a.E + ng) {
         // Q8_1(x): 8 blocks per work-group (one per half-wave), so that this
         // part of the grid finishes with the router rows
-        const int nb = a.H / QK, qwg = (nb + 7) / 8;
+        const int nb = H / QK, qwg = (nb + 7) / 8;
         const int r = row - a.E - ng, t = r / qwg, b0 = (r - t * qwg) * 8;
-        const float* xt = a.x + (int64_t)t * a.H + (int64_t)b0 * QK;
+        const float* xt = a.x + (int64_t)t * H + (int64_t)b0 * QK;
         uint8_t* dst = a.xq + t * a.xq_stride + b0 * Q8_1_BYTES;
         quantize_blocks(
             min(8, nb - b0), [&](int b, int i) { return xt[b * QK + i]; },
@@ -108,8 +110,8 @@ __global__ __launch_bounds__(256) void k_moe_route(MoeArgs a) {
     if (t0 >= a.M) return;
     const int nt = min(NT, a.M - t0);
     float v[NT];
-    const float* A = row < a.E ? a.router + (int64_t)row * a.H : a.sh_gate_w;
-    f32_row_dot<NT>(A, a.x + (int64_t)t0 * a.H, a.H, nt, red, v);
+    const float* A = row < a.E ? a.router + (int64_t)row * H : a.sh_gate_w;
+    f32_row_dot<NT>(A, a.x + (int64_t)t0 * H, H, nt, red, v);
     if (threadIdx.x == 0) {
         for (int t = 0; t < nt; t++) {
             if (row < a.E) a.logits[(t0 + t) * a.E + row] = a.bias ? v[t] + a.bias[row] : v[t];
@@ -836,7 +838,8 @@ __device__ __forceinline__ float dc1_row_lds(uint8_t* rows, const uint8_t* d0, i
 constexpr int E1_MAX_K = 8;
 static_assert((E1_MAX_K + 2) * 64 <= 1024, "dc1 work-group size");
 
-template <int TE, int TS>
+// FC: F as a compile-time constant (0: the run-time a.F)
+template <int TE, int TS, int FC = 0>
 __global__ __launch_bounds__((E1_MAX_K + 2) * 64) void k_moe_dc1(MoeArgs a) {
     __shared__ float dn[DC1_ROWS][E1_MAX_K + 1];
     __shared__ float s_wk[E1_MAX_K + 1];   // routing weights, then the shared-expert gate logit
@@ -845,7 +848,8 @@ __global__ __launch_bounds__((E1_MAX_K + 2) * 64) void k_moe_dc1(MoeArgs a) {
     const int tid = threadIdx.x, j = tid & 15, rr = (tid >> 4) & (DC1_ROWS - 1), p = tid >> 6;
     const int tile_i = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
     const int r = tile_i * DC1_ROWS + rr;
-    const int NB = a.F / QK, K = a.K;
+    const int F = FC ? FC : a.F;
+    const int NB = F / QK, K = a.K;
     const bool act = j < NB && r < a.H;
     const uint8_t* hb = a.hq + (int64_t)p * a.hq_stride + j * Q8_1_BYTES;
     float v = 0.0f;
@@ -862,12 +866,12 @@ __global__ __launch_bounds__((E1_MAX_K + 2) * 64) void k_moe_dc1(MoeArgs a) {
         else if (lane == K && a.has_shared && a.sh_gate_w) s_wk[K] = a.glogit[0];
     } else if (p < K) {
         const int e = a.plan[PLAN_UEXP + p];
-        v = dc1_row<TE>(a.down + (int64_t)e * a.sd + (int64_t)r * row_bytes(TE, a.F), j, hb, grid, act);
+        v = dc1_row<TE>(a.down + (int64_t)e * a.sd + (int64_t)r * row_bytes(TE, F), j, hb, grid, act);
     } else if constexpr (is_kquant<TS>()) {
-        const int64_t rbF = row_bytes(TS, a.F);
+        const int64_t rbF = row_bytes(TS, F);
         v = dc1_row_lds<TS>(srows, a.sh_down + (int64_t)tile_i * DC1_ROWS * rbF, rbF, rr, j, hb, act);
     } else {
-        v = dc1_row<TS>(a.sh_down + (int64_t)r * row_bytes(TS, a.F), j, hb, grid, act);
+        v = dc1_row<TS>(a.sh_down + (int64_t)r * row_bytes(TS, F), j, hb, grid, act);
     }
     if (j == 0 && p < K + a.has_shared) dn[rr][p] = v;
     __syncthreads();
@@ -1351,20 +1355,28 @@ static bool expert1_fits(const MoeArgs& a, int te, int ts) {
 // stage < 0: all three kernels; 0, 1, 2: only K1, K2 or K3
 template <int TE, int TS, int NT>
 static void launch_layer_nt(const MoeArgs& a, int stage, hipStream_t s) {
-    if (stage < 0 || stage == 0)
-        hipLaunchKernelGGL((k_moe_route<NT>), dim3(route_grid(a)), dim3(256), 0, s, a);
+    if (stage < 0 || stage == 0) {
+        if (a.H == 2048) hipLaunchKernelGGL((k_moe_route<NT, 1, 2048>), dim3(route_grid(a)), dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((k_moe_route<NT>), dim3(route_grid(a)), dim3(256), 0, s, a);
+    }
     if constexpr (NT == 1 && (TE == T_Q4_0 || TE == T_Q8_0 || TE == T_IQ3_S) &&
                   (TS == T_Q4_0 || TS == T_Q8_0 || TS == T_IQ3_S || TS == T_Q4_K || TS == T_Q5_K)) {
         if (expert1_fits(a, TE, TS)) {
-            if (stage < 0 || stage == 1)
+            if (stage < 0 || stage == 1) {
                 if (a.H == 2048 && a.F == 512)
                     hipLaunchKernelGGL((k_moe_expert1<TE, TS, 2048, 512>), dim3(expert_grid(256)), dim3(EX_THREADS), 0,
                                        s, a);
                 else
                     hipLaunchKernelGGL((k_moe_expert1<TE, TS>), dim3(expert_grid(256)), dim3(EX_THREADS), 0, s, a);
-            if (stage < 0 || stage == 2)
-                hipLaunchKernelGGL((k_moe_dc1<TE, TS>), dim3(a.H / DC1_ROWS), dim3((a.K + a.has_shared + 1) * 64), 0,
-                                   s, a);
+            }
+            if (stage < 0 || stage == 2) {
+                if (a.F == 512)
+                    hipLaunchKernelGGL((k_moe_dc1<TE, TS, 512>), dim3(a.H / DC1_ROWS),
+                                       dim3((a.K + a.has_shared + 1) * 64), 0, s, a);
+                else
+                    hipLaunchKernelGGL((k_moe_dc1<TE, TS>), dim3(a.H / DC1_ROWS), dim3((a.K + a.has_shared + 1) * 64),
+                                       0, s, a);
+            }
             return;
         }
     }
@@ -1385,7 +1397,12 @@ static void launch_layer_multi(const MoeArgs& a, int stage, hipStream_t s) {
         // 49.8 -> 49.2 us uniform, 40.9 -> 39.4 us Zipf against one
         // work-group per row; one token each or two rows per work-group
         // measured slower)
-        hipLaunchKernelGGL((k_moe_route<MAX_TOK / ROUTE_TS, ROUTE_TS>), dim3(route_grid(a, ROUTE_TS)), dim3(256), 0, s, a);
+        if (a.H == 2048)
+            hipLaunchKernelGGL((k_moe_route<MAX_TOK / ROUTE_TS, ROUTE_TS, 2048>), dim3(route_grid(a, ROUTE_TS)), dim3(256),
+                               0, s, a);
+        else
+            hipLaunchKernelGGL((k_moe_route<MAX_TOK / ROUTE_TS, ROUTE_TS>), dim3(route_grid(a, ROUTE_TS)), dim3(256), 0, s,
+                               a);
         hipLaunchKernelGGL(k_moe_plan, dim3(1), dim3(PLAN_THREADS), 0, s, a);
     }
     if (stage < 0 || stage == 1)
