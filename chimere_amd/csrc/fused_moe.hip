@@ -64,7 +64,10 @@ __device__ __forceinline__ float blk_dot_f32(const WBlk& w, const float* __restr
     return s;
 }
 
+// HC / FC: H and F as compile-time constants (0: the run-time a.H / a.F)
+template <int HC = 0, int FC = 0>
 __global__ __launch_bounds__(FM_THREADS) void k_fm_gate_up(FmArgs a) {
+    const int H = HC ? HC : a.H, F = FC ? FC : a.F;
     __shared__ __attribute__((aligned(16))) float xs[FM_MAX_H];
     __shared__ __attribute__((aligned(16))) uint8_t tile[2 * FM_GR * FM_CB + 16];
     __shared__ uint32_t grid[512];
@@ -72,8 +75,8 @@ __global__ __launch_bounds__(FM_THREADS) void k_fm_gate_up(FmArgs a) {
     const int tid = threadIdx.x, g = tid >> 6, j = tid & 63;
     const int w = blockIdx.x, k = blockIdx.y;
     const int64_t e = a.ids[k];
-    const int nb = a.H / QK;
-    const int64_t rb = (int64_t)a.H / 256 * 110;
+    const int nb = H / QK;
+    const int64_t rb = (int64_t)H / 256 * 110;
     const uint8_t* g0 = a.gate + e * a.bg + (int64_t)w * FM_GR * rb;
     const uint8_t* u0 = a.up + e * a.bu + (int64_t)w * FM_GR * rb;
     float acc = 0.0f;
@@ -84,7 +87,7 @@ __global__ __launch_bounds__(FM_THREADS) void k_fm_gate_up(FmArgs a) {
         stage_rows<true, CPOL_STREAM>(tile, g0 + goff, rb, FM_GR, seg, tid, FM_THREADS);
         stage_rows<true, CPOL_STREAM>(tile + FM_GR * seg, u0 + goff, rb, FM_GR, seg, tid, FM_THREADS);
         if (b0 == 0) {   // the activation row and the codebook, while the first chunk's rows are in flight
-            for (int i = tid; i < a.H / 4; i += FM_THREADS) ((float4*)xs)[i] = ((const float4*)a.x)[i];
+            for (int i = tid; i < H / 4; i += FM_THREADS) ((float4*)xs)[i] = ((const float4*)a.x)[i];
             for (int i = tid; i < 512; i += FM_THREADS) grid[i] = c_iq3s_grid_fm[i];
         }
         lds_copy_wait();
@@ -106,10 +109,12 @@ __global__ __launch_bounds__(FM_THREADS) void k_fm_gate_up(FmArgs a) {
         else hu[g - FM_GR] = v;
     }
     __syncthreads();
-    if (tid < FM_GR) a.h[(int64_t)k * a.F + w * FM_GR + tid] = det_silu(hg[tid]) * hu[tid];
+    if (tid < FM_GR) a.h[(int64_t)k * F + w * FM_GR + tid] = det_silu(hg[tid]) * hu[tid];
 }
 
+template <int HC = 0, int FC = 0>
 __global__ __launch_bounds__(256) void k_fm_down(FmArgs a) {
+    const int H = HC ? HC : a.H, F = FC ? FC : a.F;
     constexpr int ROWB = FM_MAX_F / 256 * 110;   // bytes of a down row at most
     __shared__ __attribute__((aligned(16))) uint8_t wl[16 * ROWB + 16];
     __shared__ uint32_t grid[512];
@@ -118,25 +123,25 @@ __global__ __launch_bounds__(256) void k_fm_down(FmArgs a) {
     __shared__ float s_w[FM_MAX_K];
     const int tid = threadIdx.x, g = tid >> 4, j = tid & 15;
     const int K = a.K, R = 16 / K, r0 = blockIdx.x * R;
-    const int nb = a.F / QK;
-    const int rb = a.F / 256 * 110;
+    const int nb = F / QK;
+    const int rb = F / 256 * 110;
     if (tid < K) {
         s_ids[tid] = a.ids[tid];
         s_w[tid] = a.wts[tid];
     }
     for (int i = tid; i < 512; i += 256) grid[i] = c_iq3s_grid_fm[i];
     // group g: down row r0 + g / K of expert g % K
-    const bool act = g < R * K && r0 + g / K < a.H;
+    const bool act = g < R * K && r0 + g / K < H;
     const int k = g % K;
     // prefetched while the ids load: this lane's h block (F <= 512: block j
     // only) and the output values of the combining threads
     float hb[QK];
     if (act && j < nb) {
-        const float* hk = a.h + (int64_t)k * a.F + QK * j;
+        const float* hk = a.h + (int64_t)k * F + QK * j;
 #pragma unroll
         for (int i = 0; i < QK / 4; i++) *(float4*)(hb + 4 * i) = *(const float4*)(hk + 4 * i);
     }
-    const bool comb = tid < R && r0 + tid < a.H;
+    const bool comb = tid < R && r0 + tid < H;
     const float out0 = comb ? a.out[r0 + tid] : 0.0f;
     __syncthreads();   // s_ids, s_w, grid
     if (act) {
@@ -212,8 +217,13 @@ void chimere_fused_moe_iq3s(const float* hidden, const void* gate_exps, const vo
     a.H = H; a.F = F; a.K = K;
     a.bg = expert_bytes_gate; a.bu = expert_bytes_up; a.bd = expert_bytes_down;
     const int R = 16 / K;
-    hipLaunchKernelGGL(k_fm_gate_up, dim3(F / FM_GR, K), dim3(FM_THREADS), 0, stream, a);
-    hipLaunchKernelGGL(k_fm_down, dim3((H + R - 1) / R), dim3(256), 0, stream, a);
+    if (H == 2048 && F == 512) {
+        hipLaunchKernelGGL((k_fm_gate_up<2048, 512>), dim3(F / FM_GR, K), dim3(FM_THREADS), 0, stream, a);
+        hipLaunchKernelGGL((k_fm_down<2048, 512>), dim3((H + R - 1) / R), dim3(256), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((k_fm_gate_up<>), dim3(F / FM_GR, K), dim3(FM_THREADS), 0, stream, a);
+        hipLaunchKernelGGL((k_fm_down<>), dim3((H + R - 1) / R), dim3(256), 0, stream, a);
+    }
     check_launch("fused_moe_iq3s");
 }
 
