@@ -938,7 +938,7 @@ constexpr int KG_CHUNK = 32;
 template <int T>
 constexpr int kg_chunk() { return T == T_Q8_0 ? 16 : KG_CHUNK; }
 // KG: K chunks of 16 blocks, double-buffered where two 64-row buffers of
-// kg_buf bytes fit (Q4_0, Q4_K: 288-byte rows; IQ3_S: 272-byte slots for the
+// kg_buf bytes fit (Q4_0, Q4_K: 288-byte rows; IQ3_S: 240-byte slots for the
 // 16-byte aligned spans of its 220-byte chunks); Q8_0 / Q5_K / Q6_K rows are
 // single-buffered.  Each item carries at most KG_NT tokens, so the tile, two
 // tokens' activation chunks, the codebook and h fit in 40 KB: four
@@ -947,7 +947,7 @@ constexpr int kg_chunk() { return T == T_Q8_0 ? 16 : KG_CHUNK; }
 constexpr int KG_BLK = 16;
 constexpr int KG_BUF = 64 * 16 * 18 + 16;
 template <int T>
-constexpr int kg_buf() { return T == T_IQ3_S ? 64 * 16 * 17 + 16 : KG_BUF; }
+constexpr int kg_buf() { return T == T_IQ3_S ? 64 * 16 * 15 + 16 : KG_BUF; }
 template <int T>
 constexpr bool kg_db() { return 64 * chunk_bytes<T>(KG_BLK) + 16 <= kg_buf<T>(); }
 template <int T>
