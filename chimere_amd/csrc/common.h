@@ -855,6 +855,17 @@ __device__ __forceinline__ void copy16_lds_untracked(const void* g, void* lds_wa
                      : "memory");
 }
 
+// The dword form: lane l deposits its 4 bytes at lds_wave + 4*l
+__device__ __forceinline__ void copy4_lds_untracked(const void* g, void* lds_wave) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_wave);
+    uint32_t saved;
+    __asm__ volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\t"
+                     "s_mov_b32 m0, %0"
+                     : "=&s"(saved)
+                     : "v"(g), "s"(m)
+                     : "memory");
+}
+
 // Work-group barrier that waits only for this wave's LDS accesses: the
 // release fence of __syncthreads() would also wait for every outstanding
 // asynchronous copy (they write LDS), including the next chunk's.  The empty

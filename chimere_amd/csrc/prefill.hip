@@ -50,6 +50,12 @@ struct PfArgs {
     int* ntiles;     // [1]
     uint8_t* hq;     // [T*K + T][hq_stride] Q8_1(h) per pair
     float* dn;       // [T*K + T][H] down-projection output per pair
+    // per-block metadata of xq / hq (row strides xq_stride / 36, hq_stride /
+    // 36 entries): f32 of the stored f16 scale, and -8 * (sum of the quants)
+    float* xmd;
+    int* xms;
+    float* hmd;
+    int* hms;
     int64_t xq_stride, hq_stride;
     int max_tiles;
 };
@@ -161,6 +167,17 @@ __global__ __launch_bounds__(256) void k_pf_router(PfArgs a) {
 __global__ __launch_bounds__(64) void k_pf_topk(PfArgs a) {
     __shared__ uint64_t s_tk[128];
     const int t = blockIdx.x;
+    // the token's Q8_1 block metadata for the gate/up launch (f32 of the
+    // stored scale, -8 * quant sum), while the logits load
+    const int64_t nbx = a.xq_stride / Q8_1_BYTES;
+    for (int b = threadIdx.x; b < a.H / QK; b += 64) {
+        const uint8_t* blk = a.xq + (int64_t)t * a.xq_stride + (int64_t)b * Q8_1_BYTES;
+        int sq = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) sq = dot4(*(const int*)(blk + 4 + 4 * k), 0x01010101, sq);
+        a.xmd[t * nbx + b] = h2f(*(const uint16_t*)blk);
+        a.xms[t * nbx + b] = -8 * sq;
+    }
     topk_wave_any(a.logits + (int64_t)t * a.E, a.E, a.K, a.ids + t * a.K, a.wts + t * a.K, s_tk);
 }
 
@@ -578,8 +595,8 @@ struct PfStage {
 template <int T, int NTN, int NR, bool AL>
 __device__ __forceinline__ void pf_gemm_k(const PfStage& s0, const PfStage& s1, const uint8_t* w0, int n0,
                                           const uint8_t* w1, int64_t rb, int nbk, const uint8_t* xsrc,
-                                          const int* xrows, int64_t xstride, int wrow0, const uint32_t* grid,
-                                          float (&acc)[NTN][4]) {
+                                          const int* xrows, int64_t xstride, const float* xmd, const int* xms,
+                                          int wrow0, const uint32_t* grid, float (&acc)[NTN][4]) {
     constexpr int CB = pf_row_chunk_bytes<T>(), CBL = pf_lds_row<T>(), CBLP = pf_lds_row_al<T>();
     static_assert(!AL || (CBL % 16 == 0 && CBLP % 16 == 0), "chunk rows in 16-byte pieces");
     // pieces per row (copied) and per LDS row slot (the rest of a slot is padding)
@@ -638,8 +655,18 @@ __device__ __forceinline__ void pf_gemm_k(const PfStage& s0, const PfStage& s1, 
                 }
             }
         }
+        // the chunk's activation metadata (xd, xs of the stage: entry
+        // b * PF_TILE + m for block b of row m) from the precomputed arrays:
+        // waves 0, 1 the scales, waves 2, 3 the sums, one dword copy each
+        static_assert(PF_THREADS == 256 && PF_TILE * PF_CHUNK == 128, "metadata copy geometry");
+        const int64_t mstride = xstride / 36;
+        const int me = (wave & 1) * 64 + lane, mb = me / PF_TILE, mm = me - mb * PF_TILE;
+        const void* msrc = wave < 2 ? (const void*)(xmd + xrows[mm] * mstride + mb)
+                                    : (const void*)(xms + xrows[mm] * mstride + mb);
         auto issue = [&](int c, const PfStage& s) {
             const int64_t goff = (int64_t)c * CB & ~(int64_t)15, xoff = (int64_t)c * PF_CHUNK * 36;
+            copy4_lds_untracked((const uint8_t*)msrc + (int64_t)c * PF_CHUNK * 4,
+                                wave < 2 ? (void*)(s.xd + (wave & 1) * 64) : (void*)(s.xs + (wave & 1) * 64));
 #pragma unroll
             for (int k = 0; k < NIT; k++) {
                 const int c0 = wave * 64 + k * PF_THREADS;
@@ -659,10 +686,8 @@ __device__ __forceinline__ void pf_gemm_k(const PfStage& s0, const PfStage& s1, 
         // c - 1 was computed from: every wave has passed the barrier since)
         auto step = [&](int c, const PfStage& cur, const PfStage& nxt) {
             wait_vm<0>();
-            lds_barrier();   // chunk c landed (every wave's share)
-            pf_xmeta(cur.x, cur.xd, cur.xs, PF_XROW_AL);
+            lds_barrier();   // chunk c (weights, activations, metadata) landed: every wave's share
             if (c + 1 < nc) issue(c + 1, nxt);
-            lds_barrier();   // metadata written
             pf_mma_chunk<T, NTN, true>(cur.x, PF_XROW_AL, cur.xd, cur.xs, cur.w + wrow0 * CBLP + (c * CB & 15), CBLP,
                                        PF_CHUNK, grid, acc);
         };
@@ -681,16 +706,17 @@ __device__ __forceinline__ void pf_gemm_k(const PfStage& s0, const PfStage& s1, 
 template <int T, int NTN, int NR, bool TWO = true>
 __device__ __forceinline__ void pf_gemm(const PfStage& s0, const PfStage& s1, const uint8_t* w0, int n0,
                                         const uint8_t* w1, int64_t rb, int nbk, const uint8_t* xsrc,
-                                        const int* xrows, int64_t xstride, int wrow0, const uint32_t* grid,
-                                        float (&acc)[NTN][4]) {
+                                        const int* xrows, int64_t xstride, const float* xmd, const int* xms,
+                                        int wrow0, const uint32_t* grid, float (&acc)[NTN][4]) {
     // the two-stage path copies 16-byte pieces: rows and activations 16-byte aligned
     const bool al16 = (((uintptr_t)w0 | (uintptr_t)w1 | (uintptr_t)rb | (uintptr_t)xsrc | (uintptr_t)xstride) & 15) == 0;
     if constexpr (TWO)
         if (al16) {
-            pf_gemm_k<T, NTN, NR, true>(s0, s1, w0, n0, w1, rb, nbk, xsrc, xrows, xstride, wrow0, grid, acc);
+            pf_gemm_k<T, NTN, NR, true>(s0, s1, w0, n0, w1, rb, nbk, xsrc, xrows, xstride, xmd, xms, wrow0, grid,
+                                          acc);
             return;
         }
-    pf_gemm_k<T, NTN, NR, false>(s0, s1, w0, n0, w1, rb, nbk, xsrc, xrows, xstride, wrow0, grid, acc);
+    pf_gemm_k<T, NTN, NR, false>(s0, s1, w0, n0, w1, rb, nbk, xsrc, xrows, xstride, xmd, xms, wrow0, grid, acc);
 }
 
 template <int T>
@@ -761,8 +787,8 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_gate_up(PfArgs a) {
         const uint8_t* g = sh ? a.sh_gate : a.gate + (int64_t)e * a.sg;
         const uint8_t* u = sh ? a.sh_up : a.up + (int64_t)e * a.su;
         pf_gemm<T, NTN, 2 * R, !(T == TS && pf_sh_one<TE, TS>())>(s0, s1, g + f0 * rb, R, u + f0 * rb, rb, a.H / QK,
-                                                                 a.xq, xrows, a.xq_stride, mat * R + rh * 16 * NTN,
-                                                                 grid, acc);
+                                                                 a.xq, xrows, a.xq_stride, a.xmd, a.xms,
+                                                                 mat * R + rh * 16 * NTN, grid, acc);
     };
     if constexpr (TE == TS) run(std::integral_constant<int, TE>{});   // one instance of the K loop
     else if (!sh) run(std::integral_constant<int, TE>{});
@@ -785,7 +811,16 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_gate_up(PfArgs a) {
         const int qv = amax == 0.0f ? 0 : (int)__builtin_roundf(xi / d);
         uint8_t* o = a.hq + (int64_t)prs[m] * a.hq_stride + (f0 / QK + blk) * Q8_1_BYTES;
         o[4 + i] = (uint8_t)(int8_t)qv;
-        if (i == 0) *(uint32_t*)o = f2h(d) | (f2h(sum) << 16);
+        // the block's metadata for the down launch (the quant sum is exact:
+        // integers below 2^12 at every step of the float tree)
+        const float sq = bfly32_sum((float)qv);
+        if (i == 0) {
+            const uint32_t dh = f2h(d);
+            *(uint32_t*)o = dh | (f2h(sum) << 16);
+            const int64_t mi = (int64_t)prs[m] * (a.hq_stride / Q8_1_BYTES) + f0 / QK + blk;
+            a.hmd[mi] = h2f(dh);
+            a.hms[mi] = -8 * (int)sq;
+        }
     }
 }
 
@@ -822,8 +857,8 @@ __global__ __launch_bounds__(PF_THREADS) void k_pf_down(PfArgs a) {
         // IQ3_S / Q6_K down rows (F / 256 superblocks of 110 / 210 bytes) are
         // 16-byte aligned only when F is a multiple of 2048: one stage
         constexpr bool two = T != T_IQ3_S && T != T_Q6_K && !(T == TS && pf_sh_one<TE, TS>());
-        pf_gemm<T, NTN, DR, two>(s0, s1, d + r0 * rb, DR, d, rb, a.F / QK, a.hq, prs, a.hq_stride, wave * 16 * NTN, grid,
-                                acc);
+        pf_gemm<T, NTN, DR, two>(s0, s1, d + r0 * rb, DR, d, rb, a.F / QK, a.hq, prs, a.hq_stride, a.hmd, a.hms,
+                                 wave * 16 * NTN, grid, acc);
     };
     if constexpr (TE == TS) run(std::integral_constant<int, TE>{});   // one instance of the K loop
     else if (!sh) run(std::integral_constant<int, TE>{});
@@ -884,7 +919,7 @@ void launch_quantize_q8_1(const float* x, void* out, int64_t ncols, int64_t ncol
                           hipStream_t s);
 
 struct PfPlan {
-    size_t logits, glogit, ids, wts, xq, spairs, tiles, ntiles, hq, dn, total;
+    size_t logits, glogit, ids, wts, xq, spairs, tiles, ntiles, hq, dn, xmd, xms, hmd, hms, total;
     int64_t xq_stride, hq_stride;
     int max_tiles;
 };
@@ -908,6 +943,10 @@ static PfPlan plan_pf(int H, int F, int E, int K, int T) {
     p.ntiles = o; o += al256p(4);
     p.hq = o; o += al256p(P * p.hq_stride);
     p.dn = o; o += al256p(P * H * 4);
+    p.xmd = o; o += al256p((size_t)T * (p.xq_stride / Q8_1_BYTES) * 4);
+    p.xms = o; o += al256p((size_t)T * (p.xq_stride / Q8_1_BYTES) * 4);
+    p.hmd = o; o += al256p(P * (p.hq_stride / Q8_1_BYTES) * 4);
+    p.hms = o; o += al256p(P * (p.hq_stride / Q8_1_BYTES) * 4);
     p.total = o;
     return p;
 }
@@ -981,6 +1020,8 @@ void chimere_moe_prefill(const chimere_moe_layer* L, const float* x, float* out,
     a.xq = w + p.xq; a.spairs = (int*)(w + p.spairs);
     a.tiles = (int*)(w + p.tiles); a.ntiles = (int*)(w + p.ntiles);
     a.hq = w + p.hq; a.dn = (float*)(w + p.dn);
+    a.xmd = (float*)(w + p.xmd); a.xms = (int*)(w + p.xms);
+    a.hmd = (float*)(w + p.hmd); a.hms = (int*)(w + p.hms);
     a.xq_stride = p.xq_stride; a.hq_stride = p.hq_stride; a.max_tiles = p.max_tiles;
     const int te = L->expert_type, ts = has_sh ? L->shared_type : te;
     auto with_ts = [&](auto te_tag) {
