@@ -592,7 +592,8 @@ struct PfStage {
 // separate the stages), and the barriers wait for LDS accesses only: the
 // release fence of __syncthreads() would also wait for the copies in flight.
 // Otherwise one stage, copied and waited for per chunk.
-template <int T, int NTN, int NR, bool AL>
+// SPAN: the one-stage path's dword span copies (below) for 4-byte aligned rows
+template <int T, int NTN, int NR, bool AL, bool SPAN = false>
 __device__ __forceinline__ void pf_gemm_k(const PfStage& s0, const PfStage& s1, const uint8_t* w0, int n0,
                                           const uint8_t* w1, int64_t rb, int nbk, const uint8_t* xsrc,
                                           const int* xrows, int64_t xstride, const float* xmd, const int* xms,
@@ -609,15 +610,50 @@ __device__ __forceinline__ void pf_gemm_k(const PfStage& s0, const PfStage& s1, 
     const int nc = nbk / PF_CHUNK;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if constexpr (!AL) {
+        // SPAN and 4-byte aligned rows (IQ3_S rows of 2 superblocks, Q6_K ...):
+        // chunk c is copied as the dword-aligned span holding it, `pre` bytes
+        // into LDS rows of stride CBLP, with dword asynchronous copies mapped
+        // piece -> (row, column) by constant divisors; other rows go through
+        // stage_rows
+        constexpr int LP = CBLP / 4, NW = PF_THREADS / 64;   // the padded row stride (banks)
+        const bool al4 = (((uintptr_t)w0 | (uintptr_t)w1 | (uintptr_t)rb) & 3) == 0;
         for (int c = 0; c < nc; c++) {
             const int64_t goff = (int64_t)c * CB, xoff = (int64_t)c * PF_CHUNK * 36;
-            stage_rows(s0.w, w0 + goff, rb, n0, CB, threadIdx.x, PF_THREADS);
-            pf_issue(s0.w + n0 * CB, w1 + goff, rb, NR - n0, CB, s0.x, xsrc, xrows, xstride, xoff);
+            const int pre = (int)(goff & 3);
+            const bool span = SPAN && al4 && pre + CB <= CBLP;
+            if (span) {
+                const int sp = (pre + CB + 3) >> 2;   // dwords per row (the span ends inside the row)
+                // the lane through an empty asm: the piece addresses are formed
+                // here, not hoisted (registers) out of the chunk loop
+                int ln = lane;
+                asm volatile("" : "+v"(ln));
+                const uintptr_t b1 = (uintptr_t)(w0 + goff - pre);
+                const uintptr_t b2 = (uintptr_t)(w1 + goff - pre) - (uintptr_t)((int64_t)n0 * rb);
+#pragma unroll
+                for (int k = 0; k < (NR * LP + PF_THREADS - 1) / PF_THREADS; k++) {
+                    const int c0 = (k * NW + wave) * 64;
+                    const unsigned cc = (unsigned)(c0 + ln), r = cc / LP, col = cc - r * LP;
+                    if (cc < (unsigned)(NR * LP) && (int)col < sp) {
+                        const uint8_t* src = (const uint8_t*)(((int)r < n0 ? b1 : b2) + (uintptr_t)((int64_t)r * rb) +
+                                                              col * 4);
+                        __builtin_amdgcn_global_load_lds((const glb_void_t*)src, (lds_void_t*)(s0.w + c0 * 4), 4, 0,
+                                                         0);
+                    }
+                }
+                pf_issue(nullptr, nullptr, rb, 0, CB, s0.x, xsrc, xrows, xstride, xoff);
+            } else {
+                stage_rows(s0.w, w0 + goff, rb, n0, CB, threadIdx.x, PF_THREADS);
+                pf_issue(s0.w + n0 * CB, w1 + goff, rb, NR - n0, CB, s0.x, xsrc, xrows, xstride, xoff);
+            }
             lds_copy_wait();
             __syncthreads();
             pf_xmeta(s0.x, s0.xd, s0.xs, PF_XROW);
             __syncthreads();
-            pf_mma_chunk<T, NTN, false>(s0.x, PF_XROW, s0.xd, s0.xs, s0.w + wrow0 * CB, CB, PF_CHUNK, grid, acc);
+            if (span)
+                pf_mma_chunk<T, NTN, false>(s0.x, PF_XROW, s0.xd, s0.xs, s0.w + wrow0 * CBLP + pre, CBLP, PF_CHUNK,
+                                            grid, acc);
+            else
+                pf_mma_chunk<T, NTN, false>(s0.x, PF_XROW, s0.xd, s0.xs, s0.w + wrow0 * CB, CB, PF_CHUNK, grid, acc);
             __syncthreads();
         }
     } else {
@@ -716,7 +752,10 @@ __device__ __forceinline__ void pf_gemm(const PfStage& s0, const PfStage& s1, co
                                           acc);
             return;
         }
-    pf_gemm_k<T, NTN, NR, false>(s0, s1, w0, n0, w1, rb, nbk, xsrc, xrows, xstride, xmd, xms, wrow0, grid, acc);
+    // (the span copies only where the one-stage path is the path: on a
+    // two-stage caller's rare fallback they would only add registers)
+    pf_gemm_k<T, NTN, NR, false, !TWO>(s0, s1, w0, n0, w1, rb, nbk, xsrc, xrows, xstride, xmd, xms, wrow0, grid,
+                                       acc);
 }
 
 template <int T>
