@@ -410,10 +410,12 @@ __device__ __forceinline__ long pf_b_frag(const uint8_t* row, int b, int q, uint
         const uint32_t qh = (PRE ? (b < 4 ? f.qh0 >> (8 * b) : f.qh1 >> (8 * (b - 4))) : row[66 + b]) >> (2 * q);
         const uint32_t i0 = (qs & 0xFFu) | ((qh & 1u) << 8), i1 = (qs >> 8) | ((qh & 2u) << 7);
         const uint32_t sg = row[74 + 4 * b + q];
-        const uint32_t b0 = nib_bits(sg & 0xFu), b1 = nib_bits(sg >> 4);
-        const uint32_t m0 = __builtin_amdgcn_perm(0u, 0u, b0 | 0x0C0C0C0Cu), m1 = __builtin_amdgcn_perm(0u, 0u, b1 | 0x0C0C0C0Cu);
-        lo = (grid[i0] ^ m0) + b0;
-        hi = (grid[i1] ^ m1) + b1;
+        // byte masks of the two sign nibbles (byte_sign_masks on the byte
+        // replicated), negation as (g ^ m) + (m & 1) per byte
+        uint32_t m0, m1;
+        byte_sign_masks(sg * 0x01010101u, 0, m0, m1);
+        lo = (grid[i0] ^ m0) + (m0 & 0x01010101u);
+        hi = (grid[i1] ^ m1) + (m1 & 0x01010101u);
         *mult = 1 + 2 * (int)(((PRE ? f.sc >> (4 * b) : row[106 + (b >> 1)] >> (4 * (b & 1)))) & 0xFu);
     } else if constexpr (T == T_Q4_0) {
         // bytes o .. o+7 of the row hold the 16 nibbles (low nibbles for
