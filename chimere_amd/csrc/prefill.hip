@@ -410,10 +410,10 @@ __device__ __forceinline__ long pf_b_frag(const uint8_t* row, int b, int q, uint
         const uint32_t qh = (PRE ? (b < 4 ? f.qh0 >> (8 * b) : f.qh1 >> (8 * (b - 4))) : row[66 + b]) >> (2 * q);
         const uint32_t i0 = (qs & 0xFFu) | ((qh & 1u) << 8), i1 = (qs >> 8) | ((qh & 2u) << 7);
         const uint32_t sg = row[74 + 4 * b + q];
-        // byte masks of the two sign nibbles (byte_sign_masks on the byte
-        // replicated), negation as (g ^ m) + (m & 1) per byte
+        // byte masks of the two sign nibbles, negation as (g ^ m) + (m & 1)
+        // per byte
         uint32_t m0, m1;
-        byte_sign_masks(sg * 0x01010101u, 0, m0, m1);
+        byte_sign_masks(sg, 0, m0, m1);
         lo = (grid[i0] ^ m0) + (m0 & 0x01010101u);
         hi = (grid[i1] ^ m1) + (m1 & 0x01010101u);
         *mult = 1 + 2 * (int)(((PRE ? f.sc >> (4 * b) : row[106 + (b >> 1)] >> (4 * (b & 1)))) & 0xFu);
@@ -619,11 +619,38 @@ __device__ __forceinline__ void pf_gemm_k(const PfStage& s0, const PfStage& s1, 
         // stage_rows
         constexpr int LP = CBLP / 4, NW = PF_THREADS / 64;   // the padded row stride (banks)
         const bool al4 = (((uintptr_t)w0 | (uintptr_t)w1 | (uintptr_t)rb) & 3) == 0;
+        // IQ3_S rows (even addresses; the decode reads bytes and halfwords
+        // only), one 16-row tile per wave: each row's chunk is copied as the
+        // 16-byte aligned span holding it, starting (row address + chunk
+        // offset) % 16 bytes into its LDS row -- per lane, since lane c reads
+        // row c of the tile.  An aligned 16-byte piece never leaves the page
+        // of the valid bytes it holds.
+        constexpr bool S16 = SPAN && T == T_IQ3_S && NTN == 1;
+        static_assert(!S16 || ((CB + 15 + 15) / 16 * 16 <= CBLP && CBLP % 16 == 0), "IQ3_S span fits its row");
         for (int c = 0; c < nc; c++) {
             const int64_t goff = (int64_t)c * CB, xoff = (int64_t)c * PF_CHUNK * 36;
             const int pre = (int)(goff & 3);
             const bool span = SPAN && al4 && pre + CB <= CBLP;
-            if (span) {
+            if (S16 && span) {
+                constexpr int LQ = CBLP / 16;   // 16-byte slots per LDS row
+                int ln = lane;
+                asm volatile("" : "+v"(ln));
+                const uintptr_t b1 = (uintptr_t)(w0 + goff);
+                const uintptr_t b2 = (uintptr_t)(w1 + goff) - (uintptr_t)((int64_t)n0 * rb);
+#pragma unroll
+                for (int k = 0; k < (NR * LQ + PF_THREADS - 1) / PF_THREADS; k++) {
+                    const int c0 = (k * NW + wave) * 64;
+                    const unsigned cc = (unsigned)(c0 + ln), r = cc / LQ, col = cc - r * LQ;
+                    if (cc < (unsigned)(NR * LQ)) {
+                        const uintptr_t ra = ((int)r < n0 ? b1 : b2) + (uintptr_t)((int64_t)r * rb);
+                        const uintptr_t st = ra & ~(uintptr_t)15;
+                        if ((uintptr_t)col * 16 < ra + CB - st)
+                            __builtin_amdgcn_global_load_lds((const glb_void_t*)(st + col * 16),
+                                                             (lds_void_t*)(s0.w + c0 * 16), 16, 0, 0);
+                    }
+                }
+                pf_issue(nullptr, nullptr, rb, 0, CB, s0.x, xsrc, xrows, xstride, xoff);
+            } else if (span) {
                 const int sp = (pre + CB + 3) >> 2;   // dwords per row (the span ends inside the row)
                 // the lane through an empty asm: the piece addresses are formed
                 // here, not hoisted (registers) out of the chunk loop
@@ -651,7 +678,14 @@ __device__ __forceinline__ void pf_gemm_k(const PfStage& s0, const PfStage& s1, 
             __syncthreads();
             pf_xmeta(s0.x, s0.xd, s0.xs, PF_XROW);
             __syncthreads();
-            if (span)
+            if (S16 && span) {
+                const int rl = wrow0 + (lane & 15);   // this lane's row
+                const uintptr_t ra = (rl < n0 ? (uintptr_t)w0 + (uintptr_t)((int64_t)rl * rb)
+                                              : (uintptr_t)w1 + (uintptr_t)((int64_t)(rl - n0) * rb)) +
+                                     (uintptr_t)goff;
+                pf_mma_chunk<T, NTN, false>(s0.x, PF_XROW, s0.xd, s0.xs, s0.w + wrow0 * CBLP + (int)(ra & 15), CBLP,
+                                            PF_CHUNK, grid, acc);
+            } else if (span)
                 pf_mma_chunk<T, NTN, false>(s0.x, PF_XROW, s0.xd, s0.xs, s0.w + wrow0 * CBLP + pre, CBLP, PF_CHUNK,
                                             grid, acc);
             else
