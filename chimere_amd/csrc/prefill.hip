@@ -407,8 +407,21 @@ __device__ __forceinline__ long pf_b_frag(const uint8_t* row, int b, int q, uint
         // bits 0..3 / 4..7 of signs[4b+q]
         *dw = PRE ? f.d : lds_u16(row, 0);
         const uint32_t qs = lds_u16(row, 2 + 8 * b + 2 * q);
-        const uint32_t qh = (PRE ? (b < 4 ? f.qh0 >> (8 * b) : f.qh1 >> (8 * (b - 4))) : row[66 + b]) >> (2 * q);
-        const uint32_t i0 = (qs & 0xFFu) | ((qh & 1u) << 8), i1 = (qs >> 8) | ((qh & 2u) << 7);
+        uint32_t i0, i1;
+        if constexpr (PRE) {
+            // high bits 2q, 2q+1 of the superblock's qh bytes as 0/1 bytes
+            // (formed once per superblock: the same for every block), each
+            // index one v_perm: byte 0 from qs, byte 1 the block's high bit
+            const uint32_t w = b < 4 ? f.qh0 : f.qh1;
+            const uint32_t h0 = (w >> (2 * q)) & 0x01010101u, h1 = (w >> (2 * q + 1)) & 0x01010101u;
+            const uint32_t sel = 0x0C0C0000u | ((uint32_t)(4 + (b & 3)) << 8);
+            i0 = __builtin_amdgcn_perm(h0, qs, sel);
+            i1 = __builtin_amdgcn_perm(h1, qs, sel | 1u);
+        } else {
+            const uint32_t qh = (uint32_t)row[66 + b] >> (2 * q);
+            i0 = (qs & 0xFFu) | ((qh & 1u) << 8);
+            i1 = (qs >> 8) | ((qh & 2u) << 7);
+        }
         const uint32_t sg = row[74 + 4 * b + q];
         // byte masks of the two sign nibbles, negation as (g ^ m) + (m & 1)
         // per byte
