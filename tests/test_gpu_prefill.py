@@ -69,6 +69,19 @@ def test_prefill_aligned_rows(dev, et, st, gate_vec):
     prefill_check(layer, torch.randn(37, 2048, generator=g, device=dev))
 
 
+@pytest.mark.parametrize("et,st", [(O.IQ3_S, O.IQ3_S), (O.IQ3_S, O.Q8_0)])
+def test_prefill_iq3s_down_spans(dev, et, st):
+    """F = 1024: 440-byte IQ3_S down rows, four one-superblock K chunks per
+    row; each row chunk starts at (440 r + 110 c) % 16 = 0, 2, ..., 14 bytes
+    past a 16-byte boundary, so the down's per-row 16-byte span copies place
+    it at every even offset of its LDS row (H = 512: the gate/up's 220-byte
+    rows, not 16-byte aligned, take the one-stage path's row staging)."""
+    print(f"prefill iq3s down spans et={et} st={st}", flush=True)
+    layer = build(dev, 500 + et + st, H=512, F=1024, E=32, K=4, et=et, st=st, gate_vec=True)
+    g = torch.Generator(device=dev).manual_seed(41)
+    prefill_check(layer, torch.randn(41, 512, generator=g, device=dev))
+
+
 def test_prefill_config5_512(dev):
     """512 tokens, H=2048, F=512, E=256, top-8, Q4_0 experts + Q4_0 shared:
     every token's output, index and weight bit-exact against the oracle.  All
